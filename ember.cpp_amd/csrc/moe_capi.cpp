@@ -1,0 +1,279 @@
+// The C ABI of the MoE FFN (include/ember_moe.h): descriptor validation, the scratch layout and the
+// launch sequence router -> route -> dispatch -> gate/up(+SwiGLU) -> down -> [shared expert] ->
+// combine, all on the caller's stream with no host synchronisation (cuda_kernels.cu:3628-3684 has
+// the same shape: router GEMM, routing kernel, expert products, SwiGLU, combine).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "moe_internal.hpp"
+
+namespace ember_moe {
+namespace {
+
+constexpr int kMaxE = 512;  // route_kernel keeps one bit per (lane, 64-expert stripe) and LDS rows of E
+constexpr int kMaxK = 64;   // picks live in a 64-entry LDS array per wave
+
+size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
+
+int64_t row_bytes(int type, int K) {
+  switch (type) {
+    case EMBER_TYPE_F32: return K % 4 ? -1 : 4 * (int64_t)K;
+    case EMBER_TYPE_F16:
+    case EMBER_TYPE_BF16: return K % 8 ? -1 : 2 * (int64_t)K;
+    case EMBER_TYPE_Q8_0: return K % 64 ? -1 : (int64_t)K / 32 * 34;
+    case EMBER_TYPE_Q4_K: return K % 256 ? -1 : (int64_t)K / 256 * 144;
+    default: return -2;
+  }
+}
+
+int check_matrix(const void* p, int type, int K) {
+  if (!p) return EMBER_ERR_NULL;
+  const int64_t rb = row_bytes(type, K);
+  if (rb == -2) return EMBER_ERR_TYPE;
+  if (rb < 0) return EMBER_ERR_SHAPE;
+  if (reinterpret_cast<uintptr_t>(p) % 16) return EMBER_ERR_ALIGN;
+  return EMBER_OK;
+}
+
+bool is_routed(const ember_moe_layer* w) {
+  return w->scoring == EMBER_SCORE_SIGMOID || w->selection_bias != nullptr || w->groups_n > 1;
+}
+
+int validate(const ember_moe_layer* w) {
+  if (!w) return EMBER_ERR_NULL;
+  if (w->d <= 0 || w->d_ff <= 0 || w->E <= 0 || w->k <= 0 || w->E > kMaxE || w->k > kMaxK) return EMBER_ERR_SHAPE;
+  if (w->scoring != EMBER_SCORE_SOFTMAX && w->scoring != EMBER_SCORE_SIGMOID) return EMBER_ERR_SHAPE;
+  if (w->groups_n > 1) {
+    // graph_ir.cpp:2696-2700 refuses the same combinations.
+    if (w->E % w->groups_n || w->groups_top < 1 || w->groups_top > w->groups_n ||
+        w->groups_top * (w->E / w->groups_n) < w->k)
+      return EMBER_ERR_SHAPE;
+  }
+  if (!w->router) return EMBER_ERR_NULL;
+  if (reinterpret_cast<uintptr_t>(w->router) % 16 || w->d % 4) return EMBER_ERR_ALIGN;
+  int s;
+  if ((s = check_matrix(w->gate, w->gate_type, w->d)) || (s = check_matrix(w->up, w->up_type, w->d)) ||
+      (s = check_matrix(w->down, w->down_type, w->d_ff)))
+    return s;
+  if (w->gate_type != w->up_type) return EMBER_ERR_TYPE;  // one fused gate/up kernel per type
+  if (w->d_ff % 4) return EMBER_ERR_SHAPE;                // h rows are read as float4
+  if (w->d_ff_shared < 0) return EMBER_ERR_SHAPE;
+  if (w->d_ff_shared > 0) {
+    if ((s = check_matrix(w->gate_shared, w->gate_shared_type, w->d)) ||
+        (s = check_matrix(w->up_shared, w->up_shared_type, w->d)) ||
+        (s = check_matrix(w->down_shared, w->down_shared_type, w->d_ff_shared)))
+      return s;
+    if (w->gate_shared_type != w->up_shared_type) return EMBER_ERR_TYPE;
+    if (w->d_ff_shared % 4) return EMBER_ERR_SHAPE;
+  }
+  return EMBER_OK;
+}
+
+// Route/dispatch part of the scratch (also ember_moe_route's whole scratch).
+struct RouteLayout {
+  size_t rank, chunk_cnt, used, n_used, pos, end;
+};
+RouteLayout route_layout(int T, int E, int k, size_t base) {
+  RouteLayout l;
+  const size_t slots = (size_t)T * k, nchunks = (slots + 63) / 64;
+  size_t o = base;
+  l.rank = o; o = align_up(o + slots * 4);
+  l.chunk_cnt = o; o = align_up(o + nchunks * E * 4);
+  l.used = o; o = align_up(o + (size_t)E * 4);
+  l.n_used = o; o = align_up(o + 4);
+  l.pos = o; o = align_up(o + slots * 4);
+  l.end = o;
+  return l;
+}
+
+struct Layout {
+  size_t logits, idx, gates, offsets, perm, h, y, hs, ys;
+  RouteLayout r;
+  size_t end;
+};
+Layout layout(const ember_moe_layer* w, int T) {
+  Layout l;
+  const size_t slots = (size_t)T * w->k;
+  size_t o = 0;
+  l.logits = o; o = align_up(o + (size_t)T * w->E * 4);
+  l.idx = o; o = align_up(o + slots * 4);
+  l.gates = o; o = align_up(o + slots * 4);
+  l.offsets = o; o = align_up(o + (size_t)(w->E + 1) * 4);
+  l.perm = o; o = align_up(o + slots * 4);
+  l.r = route_layout(T, w->E, w->k, o); o = l.r.end;
+  l.h = o; o = align_up(o + slots * w->d_ff * 4);
+  l.y = o; o = align_up(o + slots * w->d * 4);
+  l.hs = o; o = align_up(o + (size_t)T * w->d_ff_shared * 4);
+  l.ys = o; o = align_up(o + (w->d_ff_shared > 0 ? (size_t)T * w->d * 4 : 0));
+  l.end = o;
+  return l;
+}
+
+template <class P>
+P* at(void* base, size_t off) {
+  return reinterpret_cast<P*>(static_cast<char*>(base) + off);
+}
+
+DispatchScratch dispatch_scratch(void* scratch, const RouteLayout& r, int32_t* offsets, int32_t* perm) {
+  DispatchScratch ds;
+  ds.rank = at<int32_t>(scratch, r.rank);
+  ds.chunk_cnt = at<int32_t>(scratch, r.chunk_cnt);
+  ds.offsets = offsets;
+  ds.used = at<int32_t>(scratch, r.used);
+  ds.n_used = at<int32_t>(scratch, r.n_used);
+  ds.perm = perm;
+  ds.pos = at<int32_t>(scratch, r.pos);
+  return ds;
+}
+
+}  // namespace
+}  // namespace ember_moe
+
+using namespace ember_moe;
+
+extern "C" {
+
+const char* ember_moe_strerror(int status) {
+  switch (status) {
+    case EMBER_OK: return "ok";
+    case EMBER_ERR_SHAPE: return "invalid shape";
+    case EMBER_ERR_TYPE: return "unsupported tensor type";
+    case EMBER_ERR_SCRATCH: return "scratch buffer missing or too small";
+    case EMBER_ERR_NULL: return "null pointer";
+    case EMBER_ERR_LAUNCH: return "kernel launch failed";
+    case EMBER_ERR_ALIGN: return "pointer or row not 16-byte aligned";
+    default: return "unknown status";
+  }
+}
+
+size_t ember_moe_scratch_bytes(const ember_moe_layer* w, int T) {
+  if (validate(w) != EMBER_OK || T < 0) return 0;
+  return layout(w, std::max(T, 1)).end;
+}
+
+int ember_moe_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* scratch, size_t scratch_bytes,
+                  hipStream_t st) {
+  int s = validate(w);
+  if (s) return s;
+  if (T < 0) return EMBER_ERR_SHAPE;
+  if (T == 0) return EMBER_OK;
+  if (!x || !out) return EMBER_ERR_NULL;
+  if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(out) % 16) return EMBER_ERR_ALIGN;
+  const Layout l = layout(w, T);
+  if (!scratch || scratch_bytes < l.end) return EMBER_ERR_SCRATCH;
+  if (reinterpret_cast<uintptr_t>(scratch) % 256) return EMBER_ERR_ALIGN;
+
+  const int d = w->d, d_ff = w->d_ff, E = w->E, k = w->k;
+  float* logits = at<float>(scratch, l.logits);
+  int32_t* idx = at<int32_t>(scratch, l.idx);
+  float* gates = at<float>(scratch, l.gates);
+  int32_t* offsets = at<int32_t>(scratch, l.offsets);
+  int32_t* perm = at<int32_t>(scratch, l.perm);
+  const DispatchScratch ds = dispatch_scratch(scratch, l.r, offsets, perm);
+  float* h = at<float>(scratch, l.h);
+  float* y = at<float>(scratch, l.y);
+
+  if ((s = launch_router_logits(x, T, d, E, w->router, logits, st))) return s;
+  const int groups_n = std::max(w->groups_n, 1), groups_top = std::max(w->groups_top, 1);
+  if ((s = launch_route(logits, T, E, k, w->renorm ? 1 : 0, is_routed(w) ? 1 : 0,
+                        w->scoring == EMBER_SCORE_SIGMOID ? 1 : 0, w->selection_bias, groups_n, groups_top, idx,
+                        gates, st)))
+    return s;
+  if ((s = launch_dispatch(idx, T, k, E, ds, st))) return s;
+
+  ProjArgs a{};
+  a.offsets = offsets;
+  a.used = ds.used;
+  a.n_used = ds.n_used;
+  a.perm = perm;
+  a.k = k;
+  a.T = T;
+  a.max_segments = std::min(E, T * k);
+  // gate/up + SwiGLU: x rows gathered through perm, h in sorted order.
+  a.w0 = w->gate;
+  a.w1 = w->up;
+  a.type = w->gate_type;
+  a.rows = d_ff;
+  a.K = d;
+  a.expert_stride = row_bytes(w->gate_type, d) * d_ff;
+  a.in = x;
+  a.out = h;
+  a.gated = true;
+  a.in_by_perm = true;
+  if ((s = launch_projection(a, st))) return s;
+  // down: h -> y, both in sorted order.
+  a.w0 = w->down;
+  a.w1 = nullptr;
+  a.type = w->down_type;
+  a.rows = d;
+  a.K = d_ff;
+  a.expert_stride = row_bytes(w->down_type, d_ff) * d;
+  a.in = h;
+  a.out = y;
+  a.gated = false;
+  a.in_by_perm = false;
+  if ((s = launch_projection(a, st))) return s;
+
+  float* ys = nullptr;
+  if (w->d_ff_shared > 0) {
+    float* hs = at<float>(scratch, l.hs);
+    ys = at<float>(scratch, l.ys);
+    ProjArgs b{};
+    b.T = T;
+    b.max_segments = 1;
+    b.w0 = w->gate_shared;
+    b.w1 = w->up_shared;
+    b.type = w->gate_shared_type;
+    b.rows = w->d_ff_shared;
+    b.K = d;
+    b.in = x;
+    b.out = hs;
+    b.gated = true;
+    if ((s = launch_projection(b, st))) return s;
+    b.w0 = w->down_shared;
+    b.w1 = nullptr;
+    b.type = w->down_shared_type;
+    b.rows = d;
+    b.K = w->d_ff_shared;
+    b.in = hs;
+    b.out = ys;
+    b.gated = false;
+    if ((s = launch_projection(b, st))) return s;
+  }
+  return launch_combine(y, gates, ds.pos, ys, w->out_scale == 0.0f ? 1.0f : w->out_scale, T, k, d, out, st);
+}
+
+int ember_moe_router_logits(const float* x, int T, int d, int E, const float* router, float* logits, hipStream_t st) {
+  if (T < 0 || d <= 0 || E <= 0) return EMBER_ERR_SHAPE;
+  if (T == 0) return EMBER_OK;
+  if (!x || !router || !logits) return EMBER_ERR_NULL;
+  return launch_router_logits(x, T, d, E, router, logits, st);
+}
+
+size_t ember_moe_route_scratch_bytes(int T, int E, int k) {
+  if (T < 0 || E <= 0 || k <= 0) return 0;
+  return route_layout(std::max(T, 1), E, k, 0).end;
+}
+
+int ember_moe_route(const float* logits, int T, int E, int k, int renorm, int scoring, const float* selection_bias,
+                    int groups_n, int groups_top, int32_t* idx, float* gates, int32_t* offsets, int32_t* perm,
+                    void* scratch, size_t scratch_bytes, hipStream_t st) {
+  if (T < 0 || E <= 0 || k <= 0 || E > kMaxE || k > kMaxK) return EMBER_ERR_SHAPE;
+  if (scoring != EMBER_SCORE_SOFTMAX && scoring != EMBER_SCORE_SIGMOID) return EMBER_ERR_SHAPE;
+  groups_n = std::max(groups_n, 1);
+  groups_top = std::max(groups_top, 1);
+  if (groups_n > 1 && (E % groups_n || groups_top > groups_n || groups_top * (E / groups_n) < k))
+    return EMBER_ERR_SHAPE;
+  if (T == 0) return EMBER_OK;
+  if (!logits || !idx || !gates || !offsets || !perm) return EMBER_ERR_NULL;
+  const RouteLayout r = route_layout(T, E, k, 0);
+  if (!scratch || scratch_bytes < r.end) return EMBER_ERR_SCRATCH;
+  const bool routed = scoring == EMBER_SCORE_SIGMOID || selection_bias || groups_n > 1;
+  int s = launch_route(logits, T, E, k, renorm ? 1 : 0, routed ? 1 : 0, scoring == EMBER_SCORE_SIGMOID ? 1 : 0,
+                       selection_bias, groups_n, groups_top, idx, gates, st);
+  if (s) return s;
+  return launch_dispatch(idx, T, k, E, dispatch_scratch(scratch, r, offsets, perm), st);
+}
+
+}  // extern "C"

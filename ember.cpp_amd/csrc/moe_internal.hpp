@@ -1,0 +1,53 @@
+// Internal declarations shared by the MoE FFN translation units (not part of the C ABI).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include "ember_moe.h"
+#include "moe_math.hpp"
+
+namespace ember_moe {
+
+// Device buffers of the dispatch step, carved from the caller's scratch.
+struct DispatchScratch {
+  int32_t* rank;       // [T*k] rank of each slot among equal experts in its 64-slot chunk
+  int32_t* chunk_cnt;  // [ceil(T*k/64)][E] counts, then per-chunk base positions
+  int32_t* offsets;    // [E+1]
+  int32_t* used;       // [E] experts with at least one slot, ascending
+  int32_t* n_used;     // [1]
+  int32_t* perm;       // [T*k] sorted position -> slot t*k+j
+  int32_t* pos;        // [T*k] slot -> sorted position (-1: no pick)
+};
+
+int launch_router_logits(const float* x, int T, int d, int E, const float* R, float* logits, hipStream_t st);
+int launch_route(const float* logits, int T, int E, int k, int renorm, int routed, int sigmoid, const float* bias,
+                 int groups_n, int groups_top, int32_t* idx, float* gates, hipStream_t st);
+int launch_dispatch(const int32_t* idx, int T, int k, int E, const DispatchScratch& ds, hipStream_t st);
+
+// One projection over a set of token segments: out[p][row] for rows [0, rows) of a
+// [rows][K] matrix per expert (or the single shared matrix).
+struct ProjArgs {
+  const void* w0;      // gate (or the only) stack base
+  const void* w1;      // up stack base (gated projections) or null
+  int type;            // ggml type of w0 / w1
+  int rows, K;         // matrix shape per expert
+  int64_t expert_stride;  // bytes between consecutive experts' matrices
+  const float* in;     // activations: x [T][K] (gated) or h [npos][K] (down)
+  float* out;          // h [npos][rows] (gated) or y [npos][rows] (down)
+  // Segments: routed (offsets/used/n_used/perm valid, k > 0) or shared (one segment of T tokens).
+  const int32_t* offsets;
+  const int32_t* used;
+  const int32_t* n_used;
+  const int32_t* perm;
+  int k;               // slots per token; the input row of sorted position p is perm[p] / k (gated)
+  int T;
+  int max_segments;    // grid.y upper bound on segments
+  bool gated;          // gate/up pair + SwiGLU (input rows gathered through perm) vs plain
+  bool in_by_perm;     // input row of position p is perm[p]/k (x for routed gated); else p
+};
+
+int launch_projection(const ProjArgs& a, hipStream_t st);
+
+int launch_combine(const float* y, const float* gates, const int32_t* pos, const float* y_shared, float scale, int T,
+                   int k, int d, float* out, hipStream_t st);
+
+}  // namespace ember_moe

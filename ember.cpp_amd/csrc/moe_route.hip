@@ -1,0 +1,450 @@
+// Router logits, routing (top-k + gates) and the stable counting-sort dispatch for the MoE FFN.
+//
+// Bit-exactness contract (reference: utils.cpp:704-836, cpu_dot.h:12-21):
+//  * logits are the FP64 fixed-order dot of the reference: eight FP64 chains over i = 8q + c,
+//    ((c0+c1)+(c2+c3)) + ((c4+c5)+(c6+c7)) + tail, rounded to f32. Products of two f32 are exact
+//    in f64, so FMA vs multiply-add cannot change a chain; the chains are kept strictly sequential.
+//  * top-k: k passes of argmax with strict > (ties to the lower index), picks sorted ascending.
+//  * gates: (float)(exp((double)(r - mx)) / z), z the ascending double sum, exp = glibc's algorithm
+//    (moe_math.hpp); the DeepSeek-style router runs the reference's float algorithm serially.
+// The dispatch permutation has no reference counterpart: slots s = t*k + j are stably sorted by
+// expert id (offsets[E+1], perm[p] = s, pos[s] = p), built without atomics on global memory.
+#include "moe_internal.hpp"
+
+namespace ember_moe {
+using namespace ember_math;
+
+// ---------------------------------------------------------------------------------------------
+// Router logits, small T: one thread per (token, expert, chain); the 8 chains of a pair are 8
+// consecutive lanes of one wave and are combined there in the reference's order.
+__global__ void __launch_bounds__(256) router_logits_direct(const float* __restrict__ x, const float* __restrict__ R,
+                                                            float* __restrict__ logits, int T, int d, int E) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int c = (int)(gid & 7);
+  const int64_t pair = gid >> 3;
+  const bool valid = pair < (int64_t)T * E;
+  const int t = valid ? (int)(pair / E) : 0;
+  const int e = valid ? (int)(pair % E) : 0;
+  const float* xr = x + (size_t)t * d;
+  const float* rr = R + (size_t)e * d;
+  const int n8 = d - d % 8;
+  double acc = 0.0;
+  if (valid)
+    for (int i = c; i < n8; i += 8) acc = acc + (double)rr[i] * (double)xr[i];
+  const int lane = threadIdx.x & 63;
+  const int base = lane & ~7;
+  double a[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) a[j] = __shfl(acc, base + j, 64);
+  if (valid && c == 0) {
+    double tail = 0.0;
+    for (int i = n8; i < d; ++i) tail = tail + (double)rr[i] * (double)xr[i];
+    const double v = (((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]))) + tail;
+    logits[pair] = (float)v;
+  }
+}
+
+// Router logits, large T: a 32-token x 16-expert tile per 256-thread block. Thread (chain c, group g)
+// keeps 4 tokens x 4 experts of chain c; x and R stream through LDS in 64-element K tiles, and each
+// chain visits its elements in increasing index order, so the sums are the reference's exactly.
+constexpr int RL_TT = 32, RL_TE = 16, RL_KT = 64;
+__global__ void __launch_bounds__(256) router_logits_tiled(const float* __restrict__ x, const float* __restrict__ R,
+                                                           float* __restrict__ logits, int T, int d, int E) {
+  __shared__ float xs[RL_TT][RL_KT + 1];
+  __shared__ float rs[RL_TE][RL_KT + 1];
+  __shared__ double part[RL_TT * RL_TE][9];
+  const int tid = threadIdx.x;
+  const int c = tid & 7, g = tid >> 3;
+  const int tq = g & 7, eq = g >> 3;  // 8 token quads x 4 expert quads
+  const int t0 = blockIdx.x * RL_TT, e0 = blockIdx.y * RL_TE;
+  const int n8 = d - d % 8;
+  double acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = 0.0;
+  for (int k0 = 0; k0 < n8; k0 += RL_KT) {
+    const int kn = min(RL_KT, n8 - k0);
+    for (int i = tid; i < RL_TT * RL_KT; i += 256) {
+      const int tt = i / RL_KT, kk = i % RL_KT;
+      const int t = t0 + tt;
+      xs[tt][kk] = (t < T && kk < kn) ? x[(size_t)t * d + k0 + kk] : 0.0f;
+    }
+    for (int i = tid; i < RL_TE * RL_KT; i += 256) {
+      const int ee = i / RL_KT, kk = i % RL_KT;
+      const int e = e0 + ee;
+      rs[ee][kk] = (e < E && kk < kn) ? R[(size_t)e * d + k0 + kk] : 0.0f;
+    }
+    __syncthreads();
+    for (int kk = c; kk < kn; kk += 8) {
+      double xv[4], rv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xv[i] = (double)xs[tq * 4 + i][kk];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) rv[j] = (double)rs[eq * 4 + j][kk];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = acc[i][j] + rv[j] * xv[i];
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) part[(tq * 4 + i) * RL_TE + eq * 4 + j][c] = acc[i][j];
+  __syncthreads();
+  for (int p = tid; p < RL_TT * RL_TE; p += 256) {
+    const int t = t0 + p / RL_TE, e = e0 + p % RL_TE;
+    if (t >= T || e >= E) continue;
+    const double* a = part[p];
+    double tail = 0.0;
+    for (int i = n8; i < d; ++i) tail = tail + (double)R[(size_t)e * d + i] * (double)x[(size_t)t * d + i];
+    const double v = (((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]))) + tail;
+    logits[(size_t)t * E + e] = (float)v;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Routing: one wave per token.
+
+__device__ inline float smax(float a, float b) { return (a < b) ? b : a; }  // std::max(a, b)
+
+// a is a strictly better argmax candidate than b: larger value, ties to the lower index; -1 = none.
+__device__ inline bool better(float va, int ia, float vb, int ib) {
+  if (ia < 0) return false;
+  if (ib < 0) return true;
+  return va > vb || (va == vb && ia < ib);
+}
+
+__device__ inline void wave_sync_lds() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// moe_ffn_f32_cpu's routing (utils.cpp:706-733), serial, for rows holding a NaN.
+__device__ void route_softmax_serial(const float* r, int E, int k, int renorm, char* taken, int* picks,
+                                     int32_t* idx, float* gates) {
+  for (int e = 0; e < E; ++e) taken[e] = 0;
+  const int kk = min(k, E);
+  for (int j = 0; j < kk; ++j) {
+    int best = -1;
+    for (int e = 0; e < E; ++e)
+      if (!taken[e] && (best < 0 || r[e] > r[best])) best = e;
+    taken[best] = 1;
+    picks[j] = best;
+  }
+  for (int a = 1; a < kk; ++a)
+    for (int b = a; b > 0 && picks[b - 1] > picks[b]; --b) {
+      const int tmp = picks[b];
+      picks[b] = picks[b - 1];
+      picks[b - 1] = tmp;
+    }
+  float mx = -__builtin_inff();
+  double z = 0.0;
+  if (renorm) {
+    for (int j = 0; j < kk; ++j) mx = smax(mx, r[picks[j]]);
+    for (int j = 0; j < kk; ++j) z = z + exp_glibc((double)(r[picks[j]] - mx));
+  } else {
+    for (int e = 0; e < E; ++e) mx = smax(mx, r[e]);
+    for (int e = 0; e < E; ++e) z = z + exp_glibc((double)(r[e] - mx));
+  }
+  for (int j = 0; j < k; ++j) {
+    idx[j] = j < kk ? picks[j] : -1;
+    gates[j] = j < kk ? (float)(exp_glibc((double)(r[picks[j]] - mx)) / z) : 0.0f;
+  }
+}
+
+// moe_ffn_routed_f32_cpu's router (utils.cpp:766-820), serial: float scores, selection bias, groups.
+__device__ void route_routed_serial(const float* r, int E, int k, int renorm, int sigmoid, const float* bias,
+                                    int groups_n, int groups_top, float* s, float* c, char* cand, char* taken,
+                                    int* picks, int32_t* idx, float* gates) {
+  if (sigmoid) {
+    for (int e = 0; e < E; ++e) s[e] = 1.0f / (1.0f + expf_glibc(-r[e]));
+  } else {
+    float mx = -__builtin_inff();
+    for (int e = 0; e < E; ++e) mx = smax(mx, r[e]);
+    float z = 0.0f;
+    for (int e = 0; e < E; ++e) {
+      s[e] = expf_glibc(r[e] - mx);
+      z = z + s[e];
+    }
+    for (int e = 0; e < E; ++e) s[e] = s[e] / z;
+  }
+  for (int e = 0; e < E; ++e) c[e] = bias ? s[e] + bias[e] : s[e];
+  for (int e = 0; e < E; ++e) cand[e] = 1;
+  if (groups_n > 1) {
+    const int per = E / groups_n;
+    float* gscore = c + E;  // the caller reserves 2E floats at c; groups_n <= E
+    for (int g = 0; g < groups_n; ++g) {
+      float top1 = -__builtin_inff(), top2 = -__builtin_inff();
+      for (int e = g * per; e < (g + 1) * per; ++e) {
+        if (c[e] > top1) {
+          top2 = top1;
+          top1 = c[e];
+        } else if (c[e] > top2) {
+          top2 = c[e];
+        }
+      }
+      gscore[g] = per == 1 ? top1 : top1 + top2;
+    }
+    for (int g = 0; g < groups_n; ++g) taken[g] = 0;
+    for (int j = 0; j < groups_top && j < groups_n; ++j) {
+      int best = -1;
+      for (int g = 0; g < groups_n; ++g)
+        if (!taken[g] && (best < 0 || gscore[g] > gscore[best])) best = g;
+      taken[best] = 1;
+    }
+    for (int e = 0; e < E; ++e) cand[e] = taken[e / per];
+  }
+  for (int e = 0; e < E; ++e) taken[e] = 0;
+  int n = 0;
+  for (int j = 0; j < k; ++j) {
+    int best = -1;
+    for (int e = 0; e < E; ++e)
+      if (cand[e] && !taken[e] && (best < 0 || c[e] > c[best])) best = e;
+    if (best < 0) break;
+    taken[best] = 1;
+    picks[n++] = best;
+  }
+  for (int a = 1; a < n; ++a)
+    for (int b = a; b > 0 && picks[b - 1] > picks[b]; --b) {
+      const int tmp = picks[b];
+      picks[b] = picks[b - 1];
+      picks[b - 1] = tmp;
+    }
+  float z = 0.0f;
+  for (int j = 0; j < n; ++j) z = z + s[picks[j]];
+  for (int j = 0; j < k; ++j) {
+    idx[j] = j < n ? picks[j] : -1;
+    gates[j] = j < n ? (renorm ? s[picks[j]] / z : s[picks[j]]) : 0.0f;
+  }
+}
+
+// Per-wave LDS footprint of route_kernel for E experts.
+__host__ __device__ inline size_t route_wave_lds(int E) {
+  const size_t bytes = (size_t)E * 8 /*ex*/ + (size_t)E * 4 /*s*/ + (size_t)2 * E * 4 /*c + group scores*/ +
+                       (size_t)64 * 4 /*picks*/ + (size_t)((2 * E + 3) & ~3) /*cand, taken*/ + (size_t)E * 4 /*row*/;
+  return (bytes + 15) & ~(size_t)15;
+}
+
+// One wave per token. Softmax scoring without bias / groups (moe_ffn_f32_cpu) runs a parallel argmax
+// whose result equals the serial strict-> scan for NaN-free rows; rows with a NaN, and the
+// DeepSeek-style router, run the reference's serial algorithm on lane 0.
+__global__ void __launch_bounds__(256) route_kernel(const float* __restrict__ logits, int T, int E, int k, int renorm,
+                                                    int routed, int sigmoid, const float* __restrict__ bias,
+                                                    int groups_n, int groups_top, int32_t* __restrict__ idx,
+                                                    float* __restrict__ gates) {
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + wave;
+  if (t >= T) return;
+  unsigned char* wl = lds_raw + (size_t)wave * route_wave_lds(E);
+  double* ex = reinterpret_cast<double*>(wl);
+  float* s = reinterpret_cast<float*>(wl + (size_t)E * 8);
+  float* cbuf = s + E;
+  int* picks = reinterpret_cast<int*>(cbuf + 2 * E);
+  char* cand = reinterpret_cast<char*>(picks + 64);
+  char* taken = cand + E;
+  float* row = reinterpret_cast<float*>(wl + route_wave_lds(E) - (size_t)E * 4);
+  const float* r = logits + (size_t)t * E;
+  int32_t* idx_t = idx + (size_t)t * k;
+  float* gate_t = gates + (size_t)t * k;
+
+  bool has_nan = false;
+  for (int e = lane; e < E; e += 64) {
+    const float v = r[e];
+    row[e] = v;
+    has_nan |= (v != v);
+  }
+  has_nan = __any(has_nan);
+  wave_sync_lds();
+  if (routed || has_nan) {
+    if (lane == 0) {
+      if (routed)
+        route_routed_serial(row, E, k, renorm, sigmoid, bias, groups_n, groups_top, s, cbuf, cand, taken, picks, idx_t,
+                            gate_t);
+      else
+        route_softmax_serial(row, E, k, renorm, taken, picks, idx_t, gate_t);
+    }
+    return;
+  }
+  // Parallel top-k: lane-local best over its experts e = lane + 64q, then a butterfly over the wave.
+  uint32_t mine_taken = 0;  // bit q: expert lane + 64q taken (E <= 2048)
+  const int kk = min(k, E);
+  for (int j = 0; j < kk; ++j) {
+    float bv = 0.0f;
+    int bi = -1;
+    for (int e = lane, q = 0; e < E; e += 64, ++q)
+      if (!((mine_taken >> q) & 1u) && better(row[e], e, bv, bi)) {
+        bv = row[e];
+        bi = e;
+      }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const float ov = __shfl_xor(bv, off, 64);
+      const int oi = __shfl_xor(bi, off, 64);
+      if (better(ov, oi, bv, bi)) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    if ((bi & 63) == lane) mine_taken |= 1u << (bi >> 6);
+    if (lane == 0) picks[j] = bi;
+  }
+  wave_sync_lds();
+  if (lane == 0)
+    for (int a = 1; a < kk; ++a)
+      for (int b = a; b > 0 && picks[b - 1] > picks[b]; --b) {
+        const int tmp = picks[b];
+        picks[b] = picks[b - 1];
+        picks[b - 1] = tmp;
+      }
+  wave_sync_lds();
+  float mx = -__builtin_inff();
+  double z = 0.0;
+  if (renorm) {
+    for (int j = 0; j < kk; ++j) mx = smax(mx, row[picks[j]]);
+    for (int j = 0; j < kk; ++j) z = z + exp_glibc((double)(row[picks[j]] - mx));
+  } else {
+    // The maximum of a NaN-free row does not depend on the scan order (only the sign of a zero
+    // maximum can, and r - (+0) and r - (-0) round to equal exp arguments for every r).
+    for (int e = lane; e < E; e += 64) mx = smax(mx, row[e]);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) mx = smax(mx, __shfl_xor(mx, off, 64));
+    for (int e = lane; e < E; e += 64) ex[e] = exp_glibc((double)(row[e] - mx));
+    wave_sync_lds();
+    for (int e = 0; e < E; ++e) z = z + ex[e];  // ascending, as the reference sums
+  }
+  if (lane < k) {
+    if (lane < kk) {
+      const int e = picks[lane];
+      idx_t[lane] = e;
+      gate_t[lane] = (float)(exp_glibc((double)(row[e] - mx)) / z);
+    } else {
+      idx_t[lane] = -1;
+      gate_t[lane] = 0.0f;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Dispatch: stable counting sort of the T*k slots by expert. Slots are cut into 64-slot chunks,
+// one wave each. (1) rank of each slot among equal experts earlier in its chunk, and per-chunk
+// per-expert counts; (2) one block scans the counts into per-expert offsets and per-chunk bases;
+// (3) each slot lands at base[chunk][e] + rank.
+
+__global__ void __launch_bounds__(256) dispatch_count(const int32_t* __restrict__ idx, int nslots, int E,
+                                                      int32_t* __restrict__ rank, int32_t* __restrict__ chunk_cnt) {
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int chunk = blockIdx.x * 4 + wave;
+  const int nchunks = (nslots + 63) / 64;
+  if (chunk >= nchunks) return;
+  int* cnt = reinterpret_cast<int*>(lds_raw) + (size_t)wave * E;
+  for (int e = lane; e < E; e += 64) cnt[e] = 0;
+  wave_sync_lds();
+  const int s = chunk * 64 + lane;
+  const int e = s < nslots ? idx[s] : -1;
+  int rk = 0, later = 0;
+  for (int j = 0; j < 64; ++j) {
+    const int oe = __shfl(e, j, 64);
+    if (oe == e) {
+      if (j < lane) ++rk;
+      if (j > lane) ++later;
+    }
+  }
+  if (s < nslots) rank[s] = rk;
+  if (e >= 0 && later == 0) cnt[e] = rk + 1;
+  wave_sync_lds();
+  for (int ee = lane; ee < E; ee += 64) chunk_cnt[(size_t)chunk * E + ee] = cnt[ee];
+}
+
+// One block: offsets[E+1], the ascending list of experts with tokens (used[], n_used), and
+// chunk_cnt overwritten with each chunk's base position per expert.
+__global__ void __launch_bounds__(1024) dispatch_scan(int32_t* __restrict__ chunk_cnt, int nchunks, int E,
+                                                      int32_t* __restrict__ offsets, int32_t* __restrict__ used,
+                                                      int32_t* __restrict__ n_used) {
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  int* tot = reinterpret_cast<int*>(lds_raw);
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    int acc = 0;
+    for (int c = 0; c < nchunks; ++c) acc += chunk_cnt[(size_t)c * E + e];
+    tot[e] = acc;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int run = 0, nu = 0;
+    for (int e = 0; e < E; ++e) {
+      const int n = tot[e];
+      offsets[e] = run;
+      tot[e] = run;
+      run += n;
+      if (n > 0) used[nu++] = e;
+    }
+    offsets[E] = run;
+    *n_used = nu;
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    int run = tot[e];
+    for (int c = 0; c < nchunks; ++c) {
+      const int n = chunk_cnt[(size_t)c * E + e];
+      chunk_cnt[(size_t)c * E + e] = run;
+      run += n;
+    }
+  }
+}
+
+__global__ void __launch_bounds__(256) dispatch_scatter(const int32_t* __restrict__ idx, int nslots, int E,
+                                                        const int32_t* __restrict__ rank,
+                                                        const int32_t* __restrict__ chunk_base,
+                                                        int32_t* __restrict__ perm, int32_t* __restrict__ pos) {
+  const int s = blockIdx.x * blockDim.x + threadIdx.x;
+  if (s >= nslots) return;
+  const int e = idx[s];
+  if (e < 0) {
+    pos[s] = -1;
+    return;
+  }
+  const int p = chunk_base[(size_t)(s / 64) * E + e] + rank[s];
+  perm[p] = s;
+  pos[s] = p;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Host-side launchers.
+
+int launch_router_logits(const float* x, int T, int d, int E, const float* R, float* logits, hipStream_t st) {
+  if (T <= 0) return EMBER_OK;
+  if (T >= 32 && E >= 8) {
+    dim3 grid((T + RL_TT - 1) / RL_TT, (E + RL_TE - 1) / RL_TE);
+    router_logits_tiled<<<grid, 256, 0, st>>>(x, R, logits, T, d, E);
+  } else {
+    const int64_t threads = (int64_t)T * E * 8;
+    router_logits_direct<<<(unsigned)((threads + 255) / 256), 256, 0, st>>>(x, R, logits, T, d, E);
+  }
+  return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
+}
+
+int launch_route(const float* logits, int T, int E, int k, int renorm, int routed, int sigmoid, const float* bias,
+                 int groups_n, int groups_top, int32_t* idx, float* gates, hipStream_t st) {
+  if (T <= 0) return EMBER_OK;
+  const size_t lds = 4 * route_wave_lds(E);
+  route_kernel<<<(T + 3) / 4, 256, lds, st>>>(logits, T, E, k, renorm, routed, sigmoid, bias, groups_n, groups_top, idx,
+                                              gates);
+  return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
+}
+
+int launch_dispatch(const int32_t* idx, int T, int k, int E, const DispatchScratch& ds, hipStream_t st) {
+  const int nslots = T * k;
+  const int nchunks = (nslots + 63) / 64;
+  if (nslots <= 0) return EMBER_OK;
+  dispatch_count<<<(nchunks + 3) / 4, 256, 4 * (size_t)E * sizeof(int), st>>>(idx, nslots, E, ds.rank, ds.chunk_cnt);
+  dispatch_scan<<<1, 1024, (size_t)E * sizeof(int), st>>>(ds.chunk_cnt, nchunks, E, ds.offsets, ds.used, ds.n_used);
+  dispatch_scatter<<<(nslots + 255) / 256, 256, 0, st>>>(idx, nslots, E, ds.rank, ds.chunk_cnt, ds.perm, ds.pos);
+  return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
+}
+
+}  // namespace ember_moe

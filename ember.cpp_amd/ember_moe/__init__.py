@@ -1,0 +1,348 @@
+"""Python binding of the MI355X MoE FFN C ABI (include/ember_moe.h) and host utilities.
+
+The C ABI is the product boundary; this module is a thin ctypes layer used by the tests and the
+benchmark. Device memory and streams come from PyTorch (plumbing only): tensors are passed to the
+library as raw pointers. There is no fallback: if ``libember_moe.so`` is missing, importing
+``ember_moe.lib()`` raises.
+
+Reference interface mirrored: ``moe_ffn_cuda`` / ``moe_ffn_scratch_floats`` (cuda_kernels.h:668-693)
+— same arguments (x, T, d, d_ff, E, k, renorm, router, gate/up/down stacks, scratch, out, stream),
+generalised to quantized expert stacks and the IR's router options (graph_ir.cpp:2677-2710).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass, field
+from typing import Optional
+
+import numpy as np
+
+_PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+# ggml type ids (ggml_types.h:20-40)
+F32, F16, Q8_0, Q4_K, BF16 = 0, 1, 8, 12, 30
+TYPE_NAMES = {F32: "f32", F16: "f16", Q8_0: "q8_0", Q4_K: "q4_k", BF16: "bf16"}
+TYPE_IDS = {v: k for k, v in TYPE_NAMES.items()}
+
+SCORE_SOFTMAX, SCORE_SIGMOID = 0, 1
+
+OK, ERR_SHAPE, ERR_TYPE, ERR_SCRATCH, ERR_NULL, ERR_LAUNCH, ERR_ALIGN = 0, -1, -2, -3, -4, -5, -6
+
+
+class EmberError(RuntimeError):
+    def __init__(self, status: int, what: str = ""):
+        self.status = status
+        super().__init__(f"{what}: {strerror(status)} ({status})" if what else f"{strerror(status)} ({status})")
+
+
+class Layer(ctypes.Structure):
+    """ember_moe_layer (include/ember_moe.h)."""
+
+    _fields_ = [
+        ("d", ctypes.c_int), ("d_ff", ctypes.c_int), ("E", ctypes.c_int), ("k", ctypes.c_int),
+        ("renorm", ctypes.c_int), ("scoring", ctypes.c_int),
+        ("selection_bias", ctypes.c_void_p),
+        ("groups_n", ctypes.c_int), ("groups_top", ctypes.c_int),
+        ("out_scale", ctypes.c_float),
+        ("router", ctypes.c_void_p),
+        ("gate", ctypes.c_void_p), ("gate_type", ctypes.c_int),
+        ("up", ctypes.c_void_p), ("up_type", ctypes.c_int),
+        ("down", ctypes.c_void_p), ("down_type", ctypes.c_int),
+        ("d_ff_shared", ctypes.c_int),
+        ("gate_shared", ctypes.c_void_p), ("gate_shared_type", ctypes.c_int),
+        ("up_shared", ctypes.c_void_p), ("up_shared_type", ctypes.c_int),
+        ("down_shared", ctypes.c_void_p), ("down_shared_type", ctypes.c_int),
+    ]
+
+
+_lib = None
+_host = None
+
+
+def lib_path() -> str:
+    return os.path.join(_PKG_DIR, "libember_moe.so")
+
+
+def host_lib_path() -> str:
+    return os.path.join(_PKG_DIR, "libember_moe_host.so")
+
+
+def lib() -> ctypes.CDLL:
+    """The HIP library. Raises if it has not been built (no CPU fallback exists)."""
+    global _lib
+    if _lib is None:
+        p = lib_path()
+        if not os.path.exists(p):
+            raise RuntimeError(f"{p} is missing: build it with __graft_entry__.build() (no fallback path exists)")
+        L = ctypes.CDLL(p)
+        vp, i, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+        L.ember_moe_scratch_bytes.argtypes = [ctypes.POINTER(Layer), i]
+        L.ember_moe_scratch_bytes.restype = sz
+        L.ember_moe_ffn.argtypes = [ctypes.POINTER(Layer), vp, i, vp, vp, sz, vp]
+        L.ember_moe_ffn.restype = i
+        L.ember_moe_router_logits.argtypes = [vp, i, i, i, vp, vp, vp]
+        L.ember_moe_router_logits.restype = i
+        L.ember_moe_route_scratch_bytes.argtypes = [i, i, i]
+        L.ember_moe_route_scratch_bytes.restype = sz
+        L.ember_moe_route.argtypes = [vp, i, i, i, i, i, vp, i, i, vp, vp, vp, vp, vp, sz, vp]
+        L.ember_moe_route.restype = i
+        L.ember_moe_strerror.argtypes = [i]
+        L.ember_moe_strerror.restype = ctypes.c_char_p
+        _lib = L
+    return _lib
+
+
+def host() -> ctypes.CDLL:
+    global _host
+    if _host is None:
+        p = host_lib_path()
+        if not os.path.exists(p):
+            raise RuntimeError(f"{p} is missing: build it with __graft_entry__.build()")
+        H = ctypes.CDLL(p)
+        vp, i64 = ctypes.c_void_p, ctypes.c_int64
+        H.ember_fill_normal.argtypes = [vp, i64, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_float, ctypes.c_float]
+        H.ember_fill_normal.restype = None
+        H.ember_row_bytes.argtypes = [ctypes.c_int, i64]
+        H.ember_row_bytes.restype = i64
+        H.ember_quantize.argtypes = [ctypes.c_int, vp, i64, vp]
+        H.ember_quantize.restype = ctypes.c_int
+        H.ember_dequantize.argtypes = [ctypes.c_int, vp, i64, vp]
+        H.ember_dequantize.restype = ctypes.c_int
+        H.ember_f32_to_f16.argtypes = [ctypes.c_float]
+        H.ember_f32_to_f16.restype = ctypes.c_uint16
+        H.ember_f16_to_f32.argtypes = [ctypes.c_uint16]
+        H.ember_f16_to_f32.restype = ctypes.c_float
+        H.ember_f32_to_bf16.argtypes = [ctypes.c_float]
+        H.ember_f32_to_bf16.restype = ctypes.c_uint16
+        _host = H
+    return _host
+
+
+def strerror(status: int) -> str:
+    try:
+        return lib().ember_moe_strerror(status).decode()
+    except RuntimeError:
+        return f"status {status}"
+
+
+def _ptr(a) -> int:
+    if a is None:
+        return 0
+    if isinstance(a, np.ndarray):
+        return a.ctypes.data
+    return a.data_ptr()  # torch tensor
+
+
+# ----------------------------------------------------------------------------------------------
+# Host data utilities
+
+
+def normal(n: int, seed: int, stream: int, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    host().ember_fill_normal(out.ctypes.data, n, seed, stream, mean, std)
+    return out
+
+
+def row_bytes(type_id: int, n: int) -> int:
+    return int(host().ember_row_bytes(type_id, n))
+
+
+def quantize(type_id: int, x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    nbytes = row_bytes(type_id, x.size)
+    if nbytes < 0:
+        raise EmberError(ERR_SHAPE, f"quantize {TYPE_NAMES.get(type_id, type_id)} of {x.size} elements")
+    out = np.empty(nbytes, dtype=np.uint8)
+    s = host().ember_quantize(type_id, x.ctypes.data, x.size, out.ctypes.data)
+    if s:
+        raise EmberError(s, "quantize")
+    return out
+
+
+def dequantize(type_id: int, raw: np.ndarray, n: int) -> np.ndarray:
+    raw = np.ascontiguousarray(raw)
+    out = np.empty(n, dtype=np.float32)
+    s = host().ember_dequantize(type_id, raw.ctypes.data, n, out.ctypes.data)
+    if s:
+        raise EmberError(s, "dequantize")
+    return out
+
+
+# ----------------------------------------------------------------------------------------------
+# Device entry points (torch tensors on the GPU; stream defaults to torch's current stream)
+
+
+def _stream(stream) -> int:
+    if stream is not None:
+        return int(stream)
+    import torch
+
+    return int(torch.cuda.current_stream().cuda_stream)
+
+
+def scratch_bytes(layer: Layer, T: int) -> int:
+    return int(lib().ember_moe_scratch_bytes(ctypes.byref(layer), T))
+
+
+def moe_ffn(layer: Layer, x, T: int, out, scratch, scratch_nbytes: Optional[int] = None, stream=None) -> int:
+    """Calls ember_moe_ffn; returns the status (0 on success)."""
+    n = scratch_nbytes if scratch_nbytes is not None else (scratch.numel() * scratch.element_size() if scratch is not None else 0)
+    return int(lib().ember_moe_ffn(ctypes.byref(layer), _ptr(x), T, _ptr(out), _ptr(scratch), n, _stream(stream)))
+
+
+def router_logits(x, T: int, d: int, E: int, router, logits, stream=None) -> int:
+    return int(lib().ember_moe_router_logits(_ptr(x), T, d, E, _ptr(router), _ptr(logits), _stream(stream)))
+
+
+def route_scratch_bytes(T: int, E: int, k: int) -> int:
+    return int(lib().ember_moe_route_scratch_bytes(T, E, k))
+
+
+def route(logits, T, E, k, renorm, scoring, bias, groups_n, groups_top, idx, gates, offsets, perm, scratch,
+          stream=None) -> int:
+    n = scratch.numel() * scratch.element_size()
+    return int(lib().ember_moe_route(_ptr(logits), T, E, k, int(renorm), scoring, _ptr(bias), groups_n, groups_top,
+                                     _ptr(idx), _ptr(gates), _ptr(offsets), _ptr(perm), _ptr(scratch), n,
+                                     _stream(stream)))
+
+
+# ----------------------------------------------------------------------------------------------
+# Synthetic layers: weights generated on the host by the seeded generator,
+# quantized by this project's quantizers, uploaded once.
+
+
+@dataclass
+class LayerSpec:
+    d: int
+    d_ff: int
+    E: int
+    k: int
+    wtype: int = F32
+    renorm: bool = True
+    scoring: int = SCORE_SOFTMAX
+    bias_std: float = 0.0          # > 0: seeded selection bias ~ N(0, bias_std)
+    groups_n: int = 1
+    groups_top: int = 1
+    out_scale: float = 1.0
+    d_ff_shared: int = 0
+    shared_type: Optional[int] = None
+    weight_std: float = 0.02
+    router_std: Optional[float] = None  # default 1/sqrt(d)
+    seed: int = 0
+
+
+# generator streams for each tensor of a layer
+_STREAM = {"router": 1, "gate": 2, "up": 3, "down": 4, "bias": 5, "gate_sh": 6, "up_sh": 7, "down_sh": 8, "x": 100}
+
+
+@dataclass
+class HostLayer:
+    """Host copies: encoded bytes per tensor (the GGUF payload) and the spec."""
+
+    spec: LayerSpec
+    router: np.ndarray
+    gate: np.ndarray
+    up: np.ndarray
+    down: np.ndarray
+    bias: Optional[np.ndarray] = None
+    gate_sh: Optional[np.ndarray] = None
+    up_sh: Optional[np.ndarray] = None
+    down_sh: Optional[np.ndarray] = None
+
+    def dequantized(self, name: str) -> np.ndarray:
+        """The F32 stack the reference would hold after dequantize-at-load (weight_management.cpp:802-877)."""
+        s = self.spec
+        raw = getattr(self, name)
+        if name in ("gate", "up"):
+            n, t = s.E * s.d_ff * s.d, s.wtype
+        elif name == "down":
+            n, t = s.E * s.d * s.d_ff, s.wtype
+        else:
+            n, t = s.d * s.d_ff_shared, (s.shared_type if s.shared_type is not None else s.wtype)
+        return dequantize(t, raw, n)
+
+
+def make_host_layer(spec: LayerSpec) -> HostLayer:
+    s = spec
+    rstd = s.router_std if s.router_std is not None else 1.0 / np.sqrt(s.d)
+    router = normal(s.E * s.d, s.seed, _STREAM["router"], 0.0, rstd)
+
+    def stack(name, n, t):
+        return quantize(t, normal(n, s.seed, _STREAM[name], 0.0, s.weight_std))
+
+    hl = HostLayer(spec=s, router=router,
+                   gate=stack("gate", s.E * s.d_ff * s.d, s.wtype),
+                   up=stack("up", s.E * s.d_ff * s.d, s.wtype),
+                   down=stack("down", s.E * s.d * s.d_ff, s.wtype))
+    if s.bias_std > 0:
+        hl.bias = normal(s.E, s.seed, _STREAM["bias"], 0.0, s.bias_std)
+    if s.d_ff_shared > 0:
+        st = s.shared_type if s.shared_type is not None else s.wtype
+        hl.gate_sh = stack("gate_sh", s.d_ff_shared * s.d, st)
+        hl.up_sh = stack("up_sh", s.d_ff_shared * s.d, st)
+        hl.down_sh = stack("down_sh", s.d * s.d_ff_shared, st)
+    return hl
+
+
+def make_input(spec: LayerSpec, T: int, seed: Optional[int] = None) -> np.ndarray:
+    return normal(T * spec.d, spec.seed if seed is None else seed, _STREAM["x"], 0.0, 1.0).reshape(T, spec.d)
+
+
+@dataclass
+class DeviceLayer:
+    """Device-resident tensors of one layer and the C descriptor pointing at them."""
+
+    host: HostLayer
+    tensors: dict = field(default_factory=dict)
+    desc: Layer = field(default_factory=Layer)
+
+    @staticmethod
+    def upload(hl: HostLayer, device="cuda") -> "DeviceLayer":
+        import torch
+
+        dl = DeviceLayer(host=hl)
+        s = hl.spec
+
+        def up(a):
+            return torch.from_numpy(np.ascontiguousarray(a)).to(device)
+
+        for name in ("router", "gate", "up", "down", "bias", "gate_sh", "up_sh", "down_sh"):
+            a = getattr(hl, name)
+            if a is not None:
+                dl.tensors[name] = up(a)
+        t = dl.tensors
+        L = dl.desc
+        L.d, L.d_ff, L.E, L.k = s.d, s.d_ff, s.E, s.k
+        L.renorm, L.scoring = int(s.renorm), s.scoring
+        L.selection_bias = _ptr(t.get("bias"))
+        L.groups_n, L.groups_top = s.groups_n, s.groups_top
+        L.out_scale = s.out_scale
+        L.router = _ptr(t["router"])
+        L.gate, L.gate_type = _ptr(t["gate"]), s.wtype
+        L.up, L.up_type = _ptr(t["up"]), s.wtype
+        L.down, L.down_type = _ptr(t["down"]), s.wtype
+        L.d_ff_shared = s.d_ff_shared
+        if s.d_ff_shared > 0:
+            st = s.shared_type if s.shared_type is not None else s.wtype
+            L.gate_shared, L.gate_shared_type = _ptr(t["gate_sh"]), st
+            L.up_shared, L.up_shared_type = _ptr(t["up_sh"]), st
+            L.down_shared, L.down_shared_type = _ptr(t["down_sh"]), st
+        return dl
+
+    def forward(self, x, out=None, scratch=None, stream=None):
+        """Runs ember_moe_ffn on device tensor x [T][d]; returns (out, scratch)."""
+        import torch
+
+        T = x.shape[0]
+        if out is None:
+            out = torch.empty_like(x)
+        need = scratch_bytes(self.desc, T)
+        if need == 0:
+            raise EmberError(ERR_SHAPE, "ember_moe_scratch_bytes")
+        if scratch is None or scratch.numel() < need:
+            scratch = torch.empty(need, dtype=torch.uint8, device=x.device)
+        s = moe_ffn(self.desc, x, T, out, scratch, stream=stream)
+        if s:
+            raise EmberError(s, "ember_moe_ffn")
+        return out, scratch

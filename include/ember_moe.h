@@ -1,0 +1,90 @@
+/* C ABI of the MI355X-native mixture-of-experts FFN (libember_moe.so, HIP / gfx950).
+ *
+ * Replaces ember.cpp's CUDA operator
+ *     size_t moe_ffn_scratch_floats(int T, int d, int d_ff, int E, int k);          cuda_kernels.h:678
+ *     void moe_ffn_cuda(cublasHandle_t, const float* x, int T, int d, int d_ff, int E, int k,
+ *                       bool renorm, const float* router, const float* gate_exps,
+ *                       const float* up_exps, const float* down_exps, float* scratch,
+ *                       float* out, cudaStream_t);                                   cuda_kernels.h:691-693
+ * and its CPU twins moe_ffn_f32_cpu / moe_ffn_routed_f32_cpu (utils.h:45-51). Same contract as the
+ * CUDA operator: caller-owned device weights, input, output and scratch; one stream; no host
+ * synchronisation and no allocation inside the call, so it can be captured in a HIP graph; out[T][d]
+ * is overwritten. Differences: expert stacks may stay in their GGUF encoding (F32, F16, BF16, Q8_0,
+ * Q4_K) instead of being dequantized to F32 at load; the DeepSeek router options of the IR's
+ * moe_ffn op (graph_ir.cpp:2689-2709) and a shared expert (graph_ir.cpp:651-657, 919-928) are
+ * fields of the layer descriptor; errors are status codes, never exceptions.
+ *
+ * Layouts (ggml ne order, rows contiguous, blocks along a row):
+ *   router        f32 [E][d]                  (ffn_gate_inp)
+ *   gate, up      [E][d_ff][d] in `*_type`    (ffn_gate_exps, ffn_up_exps)
+ *   down          [E][d][d_ff] in `down_type` (ffn_down_exps)
+ *   *_shared      [d_ff_shared][d], [d][d_ff_shared]  (ffn_*_shexp)
+ *   x, out        f32 [T][d]
+ */
+#ifndef EMBER_MOE_H
+#define EMBER_MOE_H
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+#include "ember_moe_host.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum ember_moe_scoring {
+  EMBER_SCORE_SOFTMAX = 0, /* softmax of the router logits */
+  EMBER_SCORE_SIGMOID = 1  /* DeepSeek-V3 sigmoid scores (IR "scoring": "sigmoid") */
+};
+
+typedef struct ember_moe_layer {
+  int d, d_ff, E, k;
+  int renorm;                 /* 1: "renorm" gates (normalised over the k picks); 0: "raw" */
+  int scoring;                /* enum ember_moe_scoring */
+  const float* selection_bias;/* [E] device, or NULL (IR "selection_bias") */
+  int groups_n, groups_top;   /* group-limited routing (IR "groups"); groups_n <= 1: none */
+  float out_scale;            /* expert_weights_scale applied to the routed sum; 1: none */
+  const float* router;
+  const void* gate;  int gate_type;
+  const void* up;    int up_type;
+  const void* down;  int down_type;
+  int d_ff_shared;            /* 0: no shared expert */
+  const void* gate_shared; int gate_shared_type;
+  const void* up_shared;   int up_shared_type;
+  const void* down_shared; int down_shared_type;
+} ember_moe_layer;
+
+/* Scratch bytes ember_moe_ffn needs for T tokens of this layer (moe_ffn_scratch_floats' role,
+ * cuda_kernels.h:678, in bytes). Returns 0 for an invalid descriptor. */
+size_t ember_moe_scratch_bytes(const ember_moe_layer* w, int T);
+
+/* out[T][d] = the MoE FFN of x[T][d] (moe_ffn_cuda, cuda_kernels.cu:3628-3684; per token the
+ * result of moe_ffn_f32_cpu / moe_ffn_routed_f32_cpu, utils.cpp:704-836). T = 0 is a no-op.
+ * Returns an ember_status; on error nothing is launched. */
+int ember_moe_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* scratch,
+                  size_t scratch_bytes, hipStream_t stream);
+
+/* Router logits only: logits[T][E] = (float) of the FP64 fixed-order dot of router row e with x[t]
+ * (utils.cpp:707 with cpu_dot.h:12-21) — bit-identical to the reference's CPU logits. */
+int ember_moe_router_logits(const float* x, int T, int d, int E, const float* router, float* logits,
+                            hipStream_t stream);
+
+/* Routing and dispatch given logits (test / integration entry; no reference counterpart as one
+ * call — it isolates moe_route_sel_kernel's role, cuda_kernels.cu:3565-3604, plus the stable
+ * counting-sort dispatch). Per token: idx[T][k] ascending expert ids and gates[T][k] exactly as
+ * moe_ffn_f32_cpu (scoring softmax, no bias, no groups) or moe_ffn_routed_f32_cpu computes them.
+ * offsets[E+1]: per-expert starts in the sorted order; perm[T*k]: the slot t*k+j at each sorted
+ * position (a stable sort of the slots by expert). Scratch: ember_moe_route_scratch_bytes. */
+size_t ember_moe_route_scratch_bytes(int T, int E, int k);
+int ember_moe_route(const float* logits, int T, int E, int k, int renorm, int scoring,
+                    const float* selection_bias, int groups_n, int groups_top, int32_t* idx,
+                    float* gates, int32_t* offsets, int32_t* perm, void* scratch,
+                    size_t scratch_bytes, hipStream_t stream);
+
+/* Human-readable text for an ember_status. */
+const char* ember_moe_strerror(int status);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

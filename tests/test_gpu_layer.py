@@ -1,0 +1,106 @@
+"""GPU parity of the whole MoE FFN layer through the C ABI, against the oracle.
+
+Bars (north_star): F32 experts max-abs 1e-4 and rel-L2 1e-5 against the reference's CPU result;
+BF16 / F16 / Q8_0 / Q4_K rel-L2 2e-3 against the reference's dequantize-then-F32 result."""
+import numpy as np
+import pytest
+
+import ember_moe as em
+from gpu_util import rel_l2, run_gpu, run_oracle
+from golden_util import f32, load_cases
+
+pytestmark = pytest.mark.gpu
+
+F32_MAXABS, F32_RELL2, Q_RELL2 = 1e-4, 1e-5, 2e-3
+
+
+def check(spec, T, seed=None):
+    hl = em.make_host_layer(spec)
+    x = em.make_input(spec, T, seed)
+    print(f"layer {em.TYPE_NAMES[spec.wtype]} d={spec.d} d_ff={spec.d_ff} E={spec.E} k={spec.k} T={T}", flush=True)
+    y = run_gpu(hl, x)
+    want = run_oracle(hl, x)
+    assert np.all(np.isfinite(y))
+    if spec.wtype == em.F32 and (spec.d_ff_shared == 0 or spec.shared_type in (None, em.F32)):
+        assert np.max(np.abs(y - want)) < F32_MAXABS
+        assert rel_l2(y, want) < F32_RELL2
+    else:
+        assert rel_l2(y, want) < Q_RELL2
+    return y, want
+
+
+def test_c1_golden(gpu):
+    """BASELINE config 1 against the reference's own output bits (tests/golden/c1_layer.npz)."""
+    spec = em.LayerSpec(d=256, d_ff=688, E=8, k=2, wtype=em.F32, seed=0)
+    hl = em.make_host_layer(spec)
+    for name, c in load_cases("c1_layer.npz").items():
+        s = em.LayerSpec(**{**spec.__dict__, "renorm": bool(c["renorm"])})
+        hl.spec = s
+        x = em.make_input(s, int(c["T"]))
+        print("c1", name, flush=True)
+        y = run_gpu(hl, x)
+        want = f32(c["out_bits"])
+        assert np.max(np.abs(y - want)) < F32_MAXABS, name
+        assert rel_l2(y, want) < F32_RELL2, name
+
+
+@pytest.mark.parametrize("T", [1, 2, 5, 16, 17, 40, 64])
+@pytest.mark.parametrize("renorm", [True, False])
+def test_f32_small(gpu, T, renorm):
+    check(em.LayerSpec(d=96, d_ff=160, E=8, k=2, wtype=em.F32, renorm=renorm, seed=3, weight_std=0.3,
+                       router_std=0.3), T)
+
+
+@pytest.mark.parametrize("wtype", [em.Q8_0, em.BF16, em.F16])
+@pytest.mark.parametrize("T", [1, 3, 8, 33])
+def test_q8_bf16_f16(gpu, wtype, T):
+    check(em.LayerSpec(d=512, d_ff=384, E=8, k=2, wtype=wtype, seed=5), T)
+
+
+@pytest.mark.parametrize("T", [1, 4, 32, 70])
+def test_q4_k(gpu, T):
+    check(em.LayerSpec(d=512, d_ff=768, E=16, k=4, wtype=em.Q4_K, seed=6), T)
+
+
+@pytest.mark.parametrize("T", [1, 9])
+def test_deepseek_shared_bias_scale(gpu, T):
+    """C4-style router: softmax with a seeded selection bias ~ N(0, 2), a shared expert, a scale."""
+    check(em.LayerSpec(d=256, d_ff=192, E=16, k=6, wtype=em.BF16, bias_std=2.0, d_ff_shared=384, out_scale=2.5,
+                       seed=7), T)
+
+
+@pytest.mark.parametrize("T", [1, 6])
+def test_sigmoid_groups(gpu, T):
+    check(em.LayerSpec(d=128, d_ff=256, E=32, k=4, wtype=em.Q8_0, scoring=em.SCORE_SIGMOID, bias_std=0.5, groups_n=8,
+                       groups_top=3, seed=8), T)
+
+
+def test_k_greater_than_e(gpu):
+    check(em.LayerSpec(d=64, d_ff=128, E=4, k=6, wtype=em.F32, seed=9), 5)
+
+
+def test_deterministic(gpu):
+    spec = em.LayerSpec(d=512, d_ff=768, E=16, k=4, wtype=em.Q4_K, seed=6)
+    hl = em.make_host_layer(spec)
+    x = em.make_input(spec, 40)
+    a = run_gpu(hl, x)
+    b = run_gpu(hl, x)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_t_zero_and_errors(gpu):
+    import torch
+
+    spec = em.LayerSpec(d=256, d_ff=256, E=8, k=2, wtype=em.Q8_0, seed=1)
+    dl = em.DeviceLayer.upload(em.make_host_layer(spec))
+    x = torch.zeros((4, 256), device="cuda")
+    out = torch.full((4, 256), 7.0, device="cuda")
+    need = em.scratch_bytes(dl.desc, 4)
+    scratch = torch.empty(need, dtype=torch.uint8, device="cuda")
+    assert em.moe_ffn(dl.desc, x, 0, out, scratch) == em.OK
+    assert em.moe_ffn(dl.desc, x, 4, out, scratch, scratch_nbytes=need - 1) == em.ERR_SCRATCH
+    torch.cuda.synchronize()
+    assert torch.all(out == 7.0)  # nothing ran
+    assert em.moe_ffn(dl.desc, x, 4, out, scratch) == em.OK
+    torch.cuda.synchronize()
+    assert not torch.all(out == 7.0)
