@@ -1,0 +1,245 @@
+"""Benchmark of the MI355X MoE FFN on BASELINE config 2: a Mixtral-8x7B-shaped MoE layer
+(d 4096, 8 experts, top-2, SwiGLU d_ff 14336) with Q8_0 expert stacks and an F32 router, seeded
+synthetic weights N(0, 0.02) (router N(0, 1/sqrt(d))) and hidden states N(0, 1).
+
+One step = one ember_moe_ffn call over one batch of T tokens resident in HBM (the headline T is
+--tokens, default 1 = decode). Prints ONE JSON line. Besides the contract fields it carries:
+  roofline      the dominant kernel (gate/up + SwiGLU, HBM-bound): algorithmic bytes per launch over
+                its average duration from HIP events recorded around it on the launch stream
+  cpu_baseline  the reference's CPU MoE path (oracle/_ref, compiled from the reference's own sources
+                when present; else the oracle's restatement) on the box's host cores, on a bounded
+                token sample of the same layer
+  sweep         the other token counts of config 2 (µs/layer, tokens/s, roofline fractions)
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--tokens 1] [--sweep 1,8,128,2048]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [ROOT, os.path.join(ROOT, "ember.cpp_amd")]
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, 8 TB/s
+MFMA_PEAK = {"bf16": 2500.0, "int8": 5000.0, "fp32": 157.3}  # dense TFLOP/s (TOP/s for int8)
+Q8_0_BPW = 34.0 / 32.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def layer_spec():
+    import ember_moe as em
+
+    return em.LayerSpec(d=4096, d_ff=14336, E=8, k=2, wtype=em.Q8_0, seed=0)
+
+
+def realised_experts(em, dl, x, T):
+    """Distinct experts the batch routes to, from the product's own router and routing kernels."""
+    import torch
+
+    s = dl.host.spec
+    lg = torch.empty((T, s.E), dtype=torch.float32, device="cuda")
+    assert em.router_logits(x, T, s.d, s.E, dl.tensors["router"], lg) == 0
+    idx = torch.empty((T, s.k), dtype=torch.int32, device="cuda")
+    gates = torch.empty((T, s.k), dtype=torch.float32, device="cuda")
+    offsets = torch.empty(s.E + 1, dtype=torch.int32, device="cuda")
+    perm = torch.empty(T * s.k, dtype=torch.int32, device="cuda")
+    scr = torch.empty(em.route_scratch_bytes(T, s.E, s.k), dtype=torch.uint8, device="cuda")
+    assert em.route(lg, T, s.E, s.k, s.renorm, s.scoring, None, 1, 1, idx, gates, offsets, perm, scr) == 0
+    torch.cuda.synchronize()
+    return int(np.unique(idx.cpu().numpy()).size)
+
+
+def algorithmic(spec, T, U):
+    """Algorithmic HBM bytes of the gate/up launch and of the whole layer, and the layer's flops."""
+    d, dff, k, E = spec.d, spec.d_ff, spec.k, spec.E
+    gu = U * 2 * d * dff * Q8_0_BPW + T * k * d * 4 + T * k * dff * 4
+    layer = U * 3 * d * dff * Q8_0_BPW + E * d * 4 + 2 * T * d * 4
+    flops = 2.0 * T * k * 3 * d * dff + 2.0 * T * E * d
+    return gu, layer, flops
+
+
+def time_layer(em, dl, x, T, steps, warmup):
+    """Eager timing of K steps bracketed by synchronisations and events on the launch stream, then a
+    HIP-graph replay of the same call (checked bit-identical to the eager output)."""
+    import torch
+
+    out = torch.empty_like(x)
+    scratch = torch.empty(em.scratch_bytes(dl.desc, T), dtype=torch.uint8, device="cuda")
+    for _ in range(warmup):
+        dl.forward(x, out, scratch)
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(steps):
+        em.moe_ffn(dl.desc, x, T, out, scratch)
+    e1.record(st)
+    torch.cuda.synchronize()
+    eager_ms = e0.elapsed_time(e1) / steps
+    ref_out = out.clone()
+
+    graph_ms = None
+    try:
+        g = torch.cuda.CUDAGraph()
+        s2 = torch.cuda.Stream()
+        s2.wait_stream(st)
+        with torch.cuda.stream(s2):
+            em.moe_ffn(dl.desc, x, T, out, scratch)  # warm on the capture stream
+        st.wait_stream(s2)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g):
+            status = em.moe_ffn(dl.desc, x, T, out, scratch)
+        assert status == 0
+        out.zero_()
+        for _ in range(warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        if not torch.equal(out.view(torch.int32), ref_out.view(torch.int32)):
+            raise RuntimeError("graph replay differs from eager output")
+        e0.record(st)
+        for _ in range(steps):
+            g.replay()
+        e1.record(st)
+        torch.cuda.synchronize()
+        graph_ms = e0.elapsed_time(e1) / steps
+        if not torch.equal(out.view(torch.int32), ref_out.view(torch.int32)):
+            raise RuntimeError("graph replay differs from eager output")
+    except Exception as exc:  # the eager number stands alone
+        log(f"[bench] graph capture skipped: {exc}")
+
+    phases = {p: 0.0 for p in em.PHASES}
+    n = max(3, min(steps, 20))
+    for _ in range(n):
+        for p, v in em.moe_ffn_timed(dl.desc, x, T, out, scratch).items():
+            phases[p] += v / n
+    return eager_ms, graph_ms, phases, out
+
+
+def cpu_baseline(hl, x_host, T_headline, max_seconds=20.0):
+    """The reference's CPU path (utils.cpp moe_ffn_f32_cpu over dequantized F32 stacks,
+    weight_management.cpp:802-877), decode T = 1 single-threaded as model.cpp:759 runs it, timed on a
+    bounded sample of tokens of the same layer."""
+    from oracle import oracle as O
+
+    s = hl.spec
+    t0 = time.time()
+    R = hl.router
+    G, U, D = (hl.dequantized(n) for n in ("gate", "up", "down"))
+    log(f"[bench] cpu baseline: dequantized F32 stacks in {time.time() - t0:.1f}s")
+    use_ref = O.ref_available()
+    out = np.empty((1, s.d), np.float32)
+    done, t_start = 0, time.time()
+    while done < x_host.shape[0] and (time.time() - t_start) < max_seconds:
+        xt = np.ascontiguousarray(x_host[done:done + 1])
+        if use_ref:
+            O.ref().ref_moe_ffn_f32(xt.ctypes.data, 1, s.d, s.d_ff, s.E, s.k, R.ctypes.data, G.ctypes.data,
+                                    U.ctypes.data, D.ctypes.data, out.ctypes.data, int(s.renorm))
+        else:
+            out[:] = O.moe_layer(xt, R, G, U, D, s.d_ff, s.E, s.k, renorm=s.renorm, nthreads=1)
+        done += 1
+    el = time.time() - t_start
+    return {"value": done / el, "unit": "tokens/s", "cores": 1,
+            "kind": "reference" if use_ref else "port",
+            "sample": f"{done} decode tokens (T=1 calls) of the config-2 layer on F32 stacks dequantized from the "
+                      f"same Q8_0 bytes, single thread, {el:.1f}s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--tokens", type=int, default=1)
+    ap.add_argument("--sweep", type=str, default="1,8,128,2048")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for {args.gpus}); the multi-GPU layout is a design "
+              f"(DESIGN.md, 'More than one GPU'), not a measured path in this build.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import ember_moe as em
+
+    em.lib()
+    spec = layer_spec()
+    t0 = time.time()
+    hl = em.make_host_layer(spec)
+    log(f"[bench] generated + quantized the Q8_0 layer in {time.time() - t0:.1f}s")
+    dl = em.DeviceLayer.upload(hl)
+    torch.cuda.synchronize()
+
+    sweep_T = sorted(set([args.tokens] + [int(t) for t in args.sweep.split(",") if t]))
+    results = {}
+    for T in sweep_T:
+        x_host = em.make_input(spec, T)
+        x = torch.from_numpy(x_host).cuda()
+        U = realised_experts(em, dl, x, T)
+        eager_ms, graph_ms, phases, _ = time_layer(em, dl, x, T, args.steps, args.warmup)
+        best_ms = min(eager_ms, graph_ms) if graph_ms else eager_ms
+        gu_bytes, layer_bytes, flops = algorithmic(spec, T, U)
+        gu_ms = phases["gate_up"]
+        results[T] = dict(T=T, experts_hit=U, us_per_layer=best_ms * 1e3, eager_us=eager_ms * 1e3,
+                          graph_us=None if graph_ms is None else graph_ms * 1e3, tokens_per_s=T / (best_ms * 1e-3),
+                          layer_hbm_frac=layer_bytes / (best_ms * 1e-3) / (HBM_PEAK_GBS * 1e9),
+                          gate_up_us=gu_ms * 1e3, gate_up_gbs=gu_bytes / (gu_ms * 1e-3) / 1e9,
+                          layer_tflops=flops / (best_ms * 1e-3) / 1e12,
+                          phases_us={p: round(v * 1e3, 2) for p, v in phases.items()})
+        log(f"[bench] T={T}: {json.dumps(results[T])}")
+
+    h = results[args.tokens]
+    gu_bytes, _, _ = algorithmic(spec, args.tokens, h["experts_hit"])
+    line = {
+        "metric": "MoE-FFN tokens/s (Mixtral-shape Q8_0 layer)",
+        "value": h["tokens_per_s"],
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": h["us_per_layer"] / 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q8_0 weights, f32 activations/accumulation",
+        "data": "synthetic (seeded N(0,0.02) experts quantized to Q8_0, F32 router N(0,1/sqrt(d)), x ~ N(0,1))",
+        "config": {"workload": f"config 2: Mixtral-8x7B-shaped MoE layer, d 4096, E 8, top-2, d_ff 14336, "
+                               f"Q8_0 experts, T={args.tokens}",
+                   "tokens": args.tokens, "d": spec.d, "d_ff": spec.d_ff, "E": spec.E, "k": spec.k,
+                   "mode": "hipgraph" if h["graph_us"] is not None and h["graph_us"] <= h["eager_us"] else "eager"},
+        "roofline": {"kernel": "proj_kernel<Q8_0, gate/up + SwiGLU>", "bound": "hbm",
+                     "achieved": h["gate_up_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": h["gate_up_gbs"] / HBM_PEAK_GBS, "traffic": None,
+                     "bytes_per_launch": gu_bytes, "avg_launch_us": h["gate_up_us"]},
+        "layer_hbm_frac": h["layer_hbm_frac"],
+        "sweep": [results[T] for T in sweep_T],
+    }
+    if not args.no_cpu:
+        try:
+            line["cpu_baseline"] = cpu_baseline(hl, em.make_input(spec, 64), args.tokens)
+            line["cpu_baseline"]["host_cpu"] = _cpu_model()
+        except Exception as exc:
+            line["cpu_baseline"] = {"value": None, "error": str(exc)}
+    print(json.dumps(line), flush=True)
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip() + f" ({os.cpu_count()} logical cpus visible)"
+    except OSError:
+        pass
+    return None
+
+
+if __name__ == "__main__":
+    main()

@@ -152,8 +152,14 @@ size_t ember_moe_scratch_bytes(const ember_moe_layer* w, int T) {
   return layout(w, std::max(T, 1)).end;
 }
 
-int ember_moe_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* scratch, size_t scratch_bytes,
-                  hipStream_t st) {
+namespace {
+// Records ev[i] on the stream at phase boundary i when ev is non-null (ember_moe_ffn_timed).
+inline void mark(hipEvent_t* ev, int i, hipStream_t st) {
+  if (ev) hipEventRecord(ev[i], st);
+}
+
+int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* scratch, size_t scratch_bytes,
+            hipStream_t st, hipEvent_t* ev) {
   int s = validate(w);
   if (s) return s;
   if (T < 0) return EMBER_ERR_SHAPE;
@@ -174,13 +180,17 @@ int ember_moe_ffn(const ember_moe_layer* w, const float* x, int T, float* out, v
   float* h = at<float>(scratch, l.h);
   float* y = at<float>(scratch, l.y);
 
+  mark(ev, 0, st);
   if ((s = launch_router_logits(x, T, d, E, w->router, logits, st))) return s;
+  mark(ev, 1, st);
   const int groups_n = std::max(w->groups_n, 1), groups_top = std::max(w->groups_top, 1);
   if ((s = launch_route(logits, T, E, k, w->renorm ? 1 : 0, is_routed(w) ? 1 : 0,
                         w->scoring == EMBER_SCORE_SIGMOID ? 1 : 0, w->selection_bias, groups_n, groups_top, idx,
                         gates, st)))
     return s;
+  mark(ev, 2, st);
   if ((s = launch_dispatch(idx, T, k, E, ds, st))) return s;
+  mark(ev, 3, st);
 
   ProjArgs a{};
   a.offsets = offsets;
@@ -202,6 +212,7 @@ int ember_moe_ffn(const ember_moe_layer* w, const float* x, int T, float* out, v
   a.gated = true;
   a.in_by_perm = true;
   if ((s = launch_projection(a, st))) return s;
+  mark(ev, 4, st);
   // down: h -> y, both in sorted order.
   a.w0 = w->down;
   a.w1 = nullptr;
@@ -214,6 +225,7 @@ int ember_moe_ffn(const ember_moe_layer* w, const float* x, int T, float* out, v
   a.gated = false;
   a.in_by_perm = false;
   if ((s = launch_projection(a, st))) return s;
+  mark(ev, 5, st);
 
   float* ys = nullptr;
   if (w->d_ff_shared > 0) {
@@ -241,7 +253,32 @@ int ember_moe_ffn(const ember_moe_layer* w, const float* x, int T, float* out, v
     b.gated = false;
     if ((s = launch_projection(b, st))) return s;
   }
-  return launch_combine(y, gates, ds.pos, ys, w->out_scale == 0.0f ? 1.0f : w->out_scale, T, k, d, out, st);
+  mark(ev, 6, st);
+  s = launch_combine(y, gates, ds.pos, ys, w->out_scale == 0.0f ? 1.0f : w->out_scale, T, k, d, out, st);
+  mark(ev, 7, st);
+  return s;
+}
+}  // namespace
+
+int ember_moe_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* scratch, size_t scratch_bytes,
+                  hipStream_t st) {
+  return run_ffn(w, x, T, out, scratch, scratch_bytes, st, nullptr);
+}
+
+int ember_moe_ffn_timed(const ember_moe_layer* w, const float* x, int T, float* out, void* scratch,
+                        size_t scratch_bytes, hipStream_t st, float* phase_ms) {
+  if (!phase_ms) return EMBER_ERR_NULL;
+  hipEvent_t ev[8];
+  for (int i = 0; i < 8; ++i)
+    if (hipEventCreate(&ev[i]) != hipSuccess) return EMBER_ERR_LAUNCH;
+  int s = run_ffn(w, x, T, out, scratch, scratch_bytes, st, ev);
+  if (s == EMBER_OK && T > 0) {
+    if (hipEventSynchronize(ev[7]) != hipSuccess) s = EMBER_ERR_LAUNCH;
+    for (int i = 0; i < EMBER_MOE_NPHASES && s == EMBER_OK; ++i)
+      if (hipEventElapsedTime(&phase_ms[i], ev[i], ev[i + 1]) != hipSuccess) s = EMBER_ERR_LAUNCH;
+  }
+  for (int i = 0; i < 8; ++i) hipEventDestroy(ev[i]);
+  return s;
 }
 
 int ember_moe_router_logits(const float* x, int T, int d, int E, const float* router, float* logits, hipStream_t st) {

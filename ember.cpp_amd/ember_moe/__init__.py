@@ -81,6 +81,8 @@ def lib() -> ctypes.CDLL:
         L.ember_moe_scratch_bytes.restype = sz
         L.ember_moe_ffn.argtypes = [ctypes.POINTER(Layer), vp, i, vp, vp, sz, vp]
         L.ember_moe_ffn.restype = i
+        L.ember_moe_ffn_timed.argtypes = [ctypes.POINTER(Layer), vp, i, vp, vp, sz, vp, ctypes.POINTER(ctypes.c_float)]
+        L.ember_moe_ffn_timed.restype = i
         L.ember_moe_router_logits.argtypes = [vp, i, i, i, vp, vp, vp]
         L.ember_moe_router_logits.restype = i
         L.ember_moe_route_scratch_bytes.argtypes = [i, i, i]
@@ -189,6 +191,19 @@ def moe_ffn(layer: Layer, x, T: int, out, scratch, scratch_nbytes: Optional[int]
     """Calls ember_moe_ffn; returns the status (0 on success)."""
     n = scratch_nbytes if scratch_nbytes is not None else (scratch.numel() * scratch.element_size() if scratch is not None else 0)
     return int(lib().ember_moe_ffn(ctypes.byref(layer), _ptr(x), T, _ptr(out), _ptr(scratch), n, _stream(stream)))
+
+
+PHASES = ("router", "route", "dispatch", "gate_up", "down", "shared", "combine")
+
+
+def moe_ffn_timed(layer: Layer, x, T: int, out, scratch, stream=None):
+    """ember_moe_ffn_timed: runs the layer once, returns {phase: milliseconds}."""
+    ms = (ctypes.c_float * len(PHASES))()
+    n = scratch.numel() * scratch.element_size()
+    s = int(lib().ember_moe_ffn_timed(ctypes.byref(layer), _ptr(x), T, _ptr(out), _ptr(scratch), n, _stream(stream), ms))
+    if s:
+        raise EmberError(s, "ember_moe_ffn_timed")
+    return dict(zip(PHASES, list(ms)))
 
 
 def router_logits(x, T: int, d: int, E: int, router, logits, stream=None) -> int:

@@ -64,6 +64,15 @@ size_t ember_moe_scratch_bytes(const ember_moe_layer* w, int T);
 int ember_moe_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* scratch,
                   size_t scratch_bytes, hipStream_t stream);
 
+/* ember_moe_ffn with per-phase timing (the role of ember's PrefillOpTimer, model.cpp:1927-1975, which
+ * brackets each op with CUDA events). Records HIP events between the launches on `stream`, waits for
+ * the last one (this call synchronises the host; it is a profiling entry, not for graph capture) and
+ * writes the elapsed milliseconds of the EMBER_MOE_NPHASES phases: router logits, routing, dispatch,
+ * gate/up + SwiGLU, down, shared expert, combine. */
+#define EMBER_MOE_NPHASES 7
+int ember_moe_ffn_timed(const ember_moe_layer* w, const float* x, int T, float* out, void* scratch,
+                        size_t scratch_bytes, hipStream_t stream, float* phase_ms);
+
 /* Router logits only: logits[T][E] = (float) of the FP64 fixed-order dot of router row e with x[t]
  * (utils.cpp:707 with cpu_dot.h:12-21) — bit-identical to the reference's CPU logits. */
 int ember_moe_router_logits(const float* x, int T, int d, int E, const float* router, float* logits,
