@@ -87,11 +87,22 @@ RouteLayout route_layout(int T, int E, int k, size_t base) {
   return l;
 }
 
+struct ActLayout {
+  size_t q, scale, sum;
+};
 struct Layout {
   size_t logits, idx, gates, offsets, perm, h, y, hs, ys;
+  ActLayout xq, hq, hsq;  // int16 activations of x, h and the shared expert's h (quantized formats)
   RouteLayout r;
   size_t end;
 };
+size_t act_layout(size_t o, size_t rows, int K, bool on, ActLayout* a) {
+  const size_t n = on ? rows * (size_t)K : 0;
+  a->q = o; o = align_up(o + n * 2);
+  a->scale = o; o = align_up(o + n / 32 * 4);
+  a->sum = o; o = align_up(o + n / 32 * 4);
+  return o;
+}
 Layout layout(const ember_moe_layer* w, int T) {
   Layout l;
   const size_t slots = (size_t)T * w->k;
@@ -106,6 +117,11 @@ Layout layout(const ember_moe_layer* w, int T) {
   l.y = o; o = align_up(o + slots * w->d * 4);
   l.hs = o; o = align_up(o + (size_t)T * w->d_ff_shared * 4);
   l.ys = o; o = align_up(o + (w->d_ff_shared > 0 ? (size_t)T * w->d * 4 : 0));
+  const bool qx = type_quantizes_activations(w->gate_type) ||
+                  (w->d_ff_shared > 0 && type_quantizes_activations(w->gate_shared_type));
+  o = act_layout(o, T, w->d, qx, &l.xq);
+  o = act_layout(o, slots, w->d_ff, type_quantizes_activations(w->down_type), &l.hq);
+  o = act_layout(o, T, w->d_ff_shared, w->d_ff_shared > 0 && type_quantizes_activations(w->down_shared_type), &l.hsq);
   l.end = o;
   return l;
 }
@@ -113,6 +129,10 @@ Layout layout(const ember_moe_layer* w, int T) {
 template <class P>
 P* at(void* base, size_t off) {
   return reinterpret_cast<P*>(static_cast<char*>(base) + off);
+}
+
+ActQ act_at(void* scratch, const ActLayout& l, int K) {
+  return ActQ{at<int16_t>(scratch, l.q), at<float>(scratch, l.scale), at<int>(scratch, l.sum), K};
 }
 
 DispatchScratch dispatch_scratch(void* scratch, const RouteLayout& r, int32_t* offsets, int32_t* perm) {
@@ -184,13 +204,17 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
   if ((s = launch_router_logits(x, T, d, E, w->router, logits, st))) return s;
   mark(ev, 1, st);
   const int groups_n = std::max(w->groups_n, 1), groups_top = std::max(w->groups_top, 1);
-  if ((s = launch_route(logits, T, E, k, w->renorm ? 1 : 0, is_routed(w) ? 1 : 0,
-                        w->scoring == EMBER_SCORE_SIGMOID ? 1 : 0, w->selection_bias, groups_n, groups_top, idx,
-                        gates, st)))
+  if ((s = launch_route_dispatch(logits, T, E, k, w->renorm ? 1 : 0, is_routed(w) ? 1 : 0,
+                                 w->scoring == EMBER_SCORE_SIGMOID ? 1 : 0, w->selection_bias, groups_n, groups_top,
+                                 idx, gates, ds, st)))
     return s;
   mark(ev, 2, st);
-  if ((s = launch_dispatch(idx, T, k, E, ds, st))) return s;
   mark(ev, 3, st);
+
+  const ActQ xq = act_at(scratch, l.xq, d);
+  if (type_quantizes_activations(w->gate_type) ||
+      (w->d_ff_shared > 0 && type_quantizes_activations(w->gate_shared_type)))
+    if ((s = launch_quantize_act(x, T, d, xq, st))) return s;
 
   ProjArgs a{};
   a.offsets = offsets;
@@ -208,11 +232,15 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
   a.K = d;
   a.expert_stride = row_bytes(w->gate_type, d) * d_ff;
   a.in = x;
+  a.act = xq;
   a.out = h;
   a.gated = true;
   a.in_by_perm = true;
   if ((s = launch_projection(a, st))) return s;
   mark(ev, 4, st);
+  const ActQ hq = act_at(scratch, l.hq, d_ff);
+  if (type_quantizes_activations(w->down_type))
+    if ((s = launch_quantize_act(h, T * k, d_ff, hq, st))) return s;
   // down: h -> y, both in sorted order.
   a.w0 = w->down;
   a.w1 = nullptr;
@@ -221,6 +249,7 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
   a.K = d_ff;
   a.expert_stride = row_bytes(w->down_type, d_ff) * d;
   a.in = h;
+  a.act = hq;
   a.out = y;
   a.gated = false;
   a.in_by_perm = false;
@@ -240,15 +269,20 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     b.rows = w->d_ff_shared;
     b.K = d;
     b.in = x;
+    b.act = xq;
     b.out = hs;
     b.gated = true;
     if ((s = launch_projection(b, st))) return s;
+    const ActQ hsq = act_at(scratch, l.hsq, w->d_ff_shared);
+    if (type_quantizes_activations(w->down_shared_type))
+      if ((s = launch_quantize_act(hs, T, w->d_ff_shared, hsq, st))) return s;
     b.w0 = w->down_shared;
     b.w1 = nullptr;
     b.type = w->down_shared_type;
     b.rows = d;
     b.K = w->d_ff_shared;
     b.in = hs;
+    b.act = hsq;
     b.out = ys;
     b.gated = false;
     if ((s = launch_projection(b, st))) return s;
@@ -307,10 +341,9 @@ int ember_moe_route(const float* logits, int T, int E, int k, int renorm, int sc
   const RouteLayout r = route_layout(T, E, k, 0);
   if (!scratch || scratch_bytes < r.end) return EMBER_ERR_SCRATCH;
   const bool routed = scoring == EMBER_SCORE_SIGMOID || selection_bias || groups_n > 1;
-  int s = launch_route(logits, T, E, k, renorm ? 1 : 0, routed ? 1 : 0, scoring == EMBER_SCORE_SIGMOID ? 1 : 0,
-                       selection_bias, groups_n, groups_top, idx, gates, st);
-  if (s) return s;
-  return launch_dispatch(idx, T, k, E, dispatch_scratch(scratch, r, offsets, perm), st);
+  return launch_route_dispatch(logits, T, E, k, renorm ? 1 : 0, routed ? 1 : 0, scoring == EMBER_SCORE_SIGMOID ? 1 : 0,
+                               selection_bias, groups_n, groups_top, idx, gates,
+                               dispatch_scratch(scratch, r, offsets, perm), st);
 }
 
 }  // extern "C"

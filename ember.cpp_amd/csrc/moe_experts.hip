@@ -1,18 +1,24 @@
 // Expert projections of the MoE FFN for decode-sized segments: a bandwidth kernel that streams each
 // selected expert's rows once, dequantizes the llama.cpp blocks in registers and reduces across
-// lanes with cross-lane shuffles. Also the ordered combine.
+// lanes with cross-lane shuffles. Also the activation quantizer and the ordered combine.
 //
 // Reference semantics (utils.cpp:735-747): per selected expert, g = W_gate x, u = W_up x,
 // h = g * (1/(1+expf(-g))) * u, y = W_down h, out = sum over experts ascending of gate * y.
 // The reference evaluates these as FP64 dots over F32 weights dequantized at load
-// (weight_management.cpp:802-877); here each dot accumulates in FP32 over the dequantized values,
-// which keeps F32 layers within 1e-4 max-abs and quantized layers within 2e-3 rel-L2.
+// (weight_management.cpp:802-877). Here:
+//  * F32 / F16 / BF16 weights: FP32 dots over the exactly-decoded weights and FP32 activations
+//    (F32 layers stay within 1e-4 max-abs / 1e-5 rel-L2 of the reference);
+//  * Q8_0 / Q4_K weights: the activations are quantized to int16 per 32-element block (scale
+//    amax/32767, relative error ~2e-5) and each block's integer dot runs on v_dot2_i32_i16 with
+//    the weights' quants zero-extended to 16 bits (Q8_0 offset by +128, corrected with the block's
+//    activation sum), then scaled in FP32. Relative error stays near 1e-5, far inside 2e-3.
 //
-// Work layout: a lane owns one 32- or 64-element "chunk" of a row (chunk c of row r sits at a fixed
-// byte offset in the ggml row). L lanes (a power of two <= 64, L >= chunks per row when possible)
-// cover a row, so one wave covers 64/L rows at once; each thread keeps RR rows (x2 for gate/up)
-// in flight. A block is 4 waves; grid.x tiles the rows, grid.y the expert segments (experts that
-// received tokens, from the dispatch step), so no host synchronisation is needed.
+// Work layout: a lane owns a 32/64-element "chunk" of a row (fixed byte offset in the ggml row);
+// L lanes (a power of two <= 64) cover a row (looping when a row has more than L chunks), so a wave
+// covers 64/L rows. Each lane group walks row groups of RR rows (x2 for the gate/up pair) across
+// the whole segment (grid-stride), with the next step's weights loaded before the current step is
+// computed. grid.y enumerates expert segments (experts that received tokens, from the dispatch
+// step), so no host synchronisation is needed.
 #include "moe_internal.hpp"
 
 namespace ember_moe {
@@ -20,6 +26,33 @@ using namespace ember_math;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef u32x4 u32x4_a4 __attribute__((aligned(4)));
+typedef short short2_t __attribute__((ext_vector_type(2)));
+
+__device__ inline int sdot2(uint32_t a, uint32_t b, int c) {
+  return __builtin_amdgcn_sdot2(__builtin_bit_cast(short2_t, a), __builtin_bit_cast(short2_t, b), c, false);
+}
+// bytes 0,1 (sel 0) or 2,3 (sel 1) of w, zero-extended to two 16-bit lanes
+__device__ inline uint32_t u16pair(uint32_t w, int hi) {
+  return __builtin_amdgcn_perm(0u, w, hi ? 0x0c030c02u : 0x0c010c00u);
+}
+
+__device__ inline void load16(const uint8_t* p, uint32_t* raw) {
+  const u32x4 q = *reinterpret_cast<const u32x4*>(p);
+  raw[0] = q.x;
+  raw[1] = q.y;
+  raw[2] = q.z;
+  raw[3] = q.w;
+}
+
+// Activation operands of one chunk for one token.
+struct XF {                 // float activations (F32 / F16 / BF16 weights)
+  float v[64];
+};
+struct XQ {                 // int16 activations (Q8_0 / Q4_K weights): 64 values in 32 pairs
+  uint32_t w[32];
+  float s[2];               // per 32-block scale
+  int sum[2];               // per 32-block sum of the int16 values
+};
 
 template <int FMT>
 struct Fmt;
@@ -28,25 +61,28 @@ struct Fmt;
 template <>
 struct Fmt<EMBER_TYPE_F32> {
   static constexpr int CE = 32, NW = 32;
+  static constexpr bool QX = false;
   __host__ __device__ static int64_t row_bytes(int K) { return 4 * (int64_t)K; }
   __device__ static void load(const uint8_t* row, int c, int K, uint32_t* raw) {
-    const u32x4* p = reinterpret_cast<const u32x4*>(row + (size_t)c * 128);
-    const int n = K - c * CE;  // valid elements in this chunk (multiple of 4)
+    const int n = K - c * CE;  // valid elements (multiple of 4)
 #pragma unroll
     for (int v = 0; v < 8; ++v) {
-      u32x4 q = (4 * v < n) ? p[v] : u32x4{0, 0, 0, 0};
-      raw[4 * v] = q.x;
-      raw[4 * v + 1] = q.y;
-      raw[4 * v + 2] = q.z;
-      raw[4 * v + 3] = q.w;
+      if (4 * v < n) {
+        load16(row + (size_t)c * 128 + 16 * v, raw + 4 * v);
+      } else {
+        raw[4 * v] = raw[4 * v + 1] = raw[4 * v + 2] = raw[4 * v + 3] = 0u;
+      }
     }
   }
-  __device__ static float dot(const uint32_t* raw, const float* x, int) {
+  template <int MT>
+  __device__ static void dot_tokens(const uint32_t* raw, const uint8_t* lds, int row_lds, int c, int K, int nvalid,
+                                    float* out);
+  __device__ static float dot(const uint32_t* raw, const XF& x, int) {
     float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
     for (int i = 0; i < 32; i += 2) {
-      a0 = __builtin_fmaf(as_f32(raw[i]), x[i], a0);
-      a1 = __builtin_fmaf(as_f32(raw[i + 1]), x[i + 1], a1);
+      a0 = __builtin_fmaf(as_f32(raw[i]), x.v[i], a0);
+      a1 = __builtin_fmaf(as_f32(raw[i + 1]), x.v[i + 1], a1);
     }
     return a0 + a1;
   }
@@ -56,17 +92,17 @@ struct Fmt<EMBER_TYPE_F32> {
 template <int FMT>
 struct FmtHalf {
   static constexpr int CE = 64, NW = 32;
+  static constexpr bool QX = false;
   __host__ __device__ static int64_t row_bytes(int K) { return 2 * (int64_t)K; }
   __device__ static void load(const uint8_t* row, int c, int K, uint32_t* raw) {
-    const u32x4* p = reinterpret_cast<const u32x4*>(row + (size_t)c * 128);
     const int n = K - c * CE;  // multiple of 8
 #pragma unroll
     for (int v = 0; v < 8; ++v) {
-      u32x4 q = (8 * v < n) ? p[v] : u32x4{0, 0, 0, 0};
-      raw[4 * v] = q.x;
-      raw[4 * v + 1] = q.y;
-      raw[4 * v + 2] = q.z;
-      raw[4 * v + 3] = q.w;
+      if (8 * v < n) {
+        load16(row + (size_t)c * 128 + 16 * v, raw + 4 * v);
+      } else {
+        raw[4 * v] = raw[4 * v + 1] = raw[4 * v + 2] = raw[4 * v + 3] = 0u;
+      }
     }
   }
   __device__ static float lo(uint32_t w) {
@@ -77,12 +113,15 @@ struct FmtHalf {
     if (FMT == EMBER_TYPE_BF16) return as_f32(w & 0xffff0000u);
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
   }
-  __device__ static float dot(const uint32_t* raw, const float* x, int) {
+  template <int MT>
+  __device__ static void dot_tokens(const uint32_t* raw, const uint8_t* lds, int row_lds, int c, int K, int nvalid,
+                                    float* out);
+  __device__ static float dot(const uint32_t* raw, const XF& x, int) {
     float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
-      a0 = __builtin_fmaf(lo(raw[i]), x[2 * i], a0);
-      a1 = __builtin_fmaf(hi(raw[i]), x[2 * i + 1], a1);
+      a0 = __builtin_fmaf(lo(raw[i]), x.v[2 * i], a0);
+      a1 = __builtin_fmaf(hi(raw[i]), x.v[2 * i + 1], a1);
     }
     return a0 + a1;
   }
@@ -92,13 +131,12 @@ struct Fmt<EMBER_TYPE_BF16> : FmtHalf<EMBER_TYPE_BF16> {};
 template <>
 struct Fmt<EMBER_TYPE_F16> : FmtHalf<EMBER_TYPE_F16> {};
 
-__device__ inline int sbyte(const uint32_t* raw, int b) { return (int)(int8_t)((raw[b >> 2] >> (8 * (b & 3))) & 0xff); }
-__device__ inline int ubyte(const uint32_t* raw, int b) { return (int)((raw[b >> 2] >> (8 * (b & 3))) & 0xff); }
-
 // Q8_0: chunk = two 34-byte blocks = 68 B = 17 dwords (4-byte aligned when K % 64 == 0).
+// Dword 0 = {d_A, q0, q1}; 1..7 = q2..q29; 8 = {q30, q31, d_B}; 9..16 = block B's q0..q31.
 template <>
 struct Fmt<EMBER_TYPE_Q8_0> {
   static constexpr int CE = 64, NW = 17;
+  static constexpr bool QX = true;
   __host__ __device__ static int64_t row_bytes(int K) { return (int64_t)K / 32 * 34; }
   __device__ static void load(const uint8_t* row, int c, int, uint32_t* raw) {
     const uint8_t* p = row + (size_t)c * 68;
@@ -112,16 +150,50 @@ struct Fmt<EMBER_TYPE_Q8_0> {
     }
     raw[16] = *reinterpret_cast<const uint32_t*>(p + 64);
   }
-  __device__ static float dot(const uint32_t* raw, const float* x, int) {
+  // MT tokens' dots of one chunk; the activation rows are staged in LDS (act_lds_bytes layout).
+  // Each weight pair is converted once (q + 128, zero-extended to 16 bits) and used for every token.
+  template <int MT>
+  __device__ static void dot_tokens(const uint32_t* raw, const uint8_t* lds, int row_lds, int c, int K, int nvalid,
+                                    float* out) {
     const float dA = half_bits_to_float(raw[0] & 0xffff);
     const float dB = half_bits_to_float(raw[8] >> 16);
-    float sA = 0.0f, sB = 0.0f;
+    int ia[MT], ib[MT];
 #pragma unroll
-    for (int j = 0; j < 32; ++j) {
-      sA = __builtin_fmaf((float)sbyte(raw, 2 + j), x[j], sA);
-      sB = __builtin_fmaf((float)sbyte(raw, 36 + j), x[32 + j], sB);
+    for (int m = 0; m < MT; ++m) ia[m] = ib[m] = 0;
+#pragma unroll
+    for (int j4 = 0; j4 < 16; j4 += 4) {
+      uint32_t ua[4], ub[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        ua[j] = u16pair(raw[(1 + j4 + j) >> 1] ^ 0x80808080u, (1 + j4 + j) & 1);
+        ub[j] = u16pair(raw[9 + ((j4 + j) >> 1)] ^ 0x80808080u, (j4 + j) & 1);
+      }
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        if (m < nvalid) {
+          const uint8_t* xr = lds + m * row_lds + (size_t)c * 128;
+          const u32x4 xa = *reinterpret_cast<const u32x4*>(xr + 4 * j4);
+          const u32x4 xb = *reinterpret_cast<const u32x4*>(xr + 64 + 4 * j4);
+          ia[m] = sdot2(ua[0], xa.x, ia[m]);
+          ia[m] = sdot2(ua[1], xa.y, ia[m]);
+          ia[m] = sdot2(ua[2], xa.z, ia[m]);
+          ia[m] = sdot2(ua[3], xa.w, ia[m]);
+          ib[m] = sdot2(ub[0], xb.x, ib[m]);
+          ib[m] = sdot2(ub[1], xb.y, ib[m]);
+          ib[m] = sdot2(ub[2], xb.z, ib[m]);
+          ib[m] = sdot2(ub[3], xb.w, ib[m]);
+        }
+      }
     }
-    return dA * sA + dB * sB;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      if (m < nvalid) {
+        const uint8_t* xr = lds + m * row_lds;
+        const float* sc = reinterpret_cast<const float*>(xr + K * 2) + 2 * c;
+        const int* sm = reinterpret_cast<const int*>(xr + K * 2 + (K / 32) * 4) + 2 * c;
+        out[m] += dA * (sc[0] * (float)(ia[m] - 128 * sm[0])) + dB * (sc[1] * (float)(ib[m] - 128 * sm[1]));
+      }
+    }
   }
 };
 
@@ -130,16 +202,15 @@ struct Fmt<EMBER_TYPE_Q8_0> {
 template <>
 struct Fmt<EMBER_TYPE_Q4_K> {
   static constexpr int CE = 64, NW = 12;
+  static constexpr bool QX = true;
   __host__ __device__ static int64_t row_bytes(int K) { return (int64_t)K / 256 * 144; }
   __device__ static void load(const uint8_t* row, int c, int, uint32_t* raw) {
     const uint8_t* sb = row + (size_t)(c >> 2) * 144;
-    const u32x4 h = *reinterpret_cast<const u32x4*>(sb);
-    const u32x4 q0 = *reinterpret_cast<const u32x4*>(sb + 16 + 32 * (c & 3));
-    const u32x4 q1 = *reinterpret_cast<const u32x4*>(sb + 32 + 32 * (c & 3));
-    raw[0] = h.x; raw[1] = h.y; raw[2] = h.z; raw[3] = h.w;
-    raw[4] = q0.x; raw[5] = q0.y; raw[6] = q0.z; raw[7] = q0.w;
-    raw[8] = q1.x; raw[9] = q1.y; raw[10] = q1.z; raw[11] = q1.w;
+    load16(sb, raw);
+    load16(sb + 16 + 32 * (c & 3), raw + 4);
+    load16(sb + 32 + 32 * (c & 3), raw + 8);
   }
+  __device__ static int ubyte(const uint32_t* raw, int b) { return (int)((raw[b >> 2] >> (8 * (b & 3))) & 0xff); }
   // get_scale_min_k4 (quantization.cpp:145-155) on the 12 scale bytes (header bytes 4..15).
   __device__ static void scale_min(const uint32_t* raw, int j, int* sc, int* mn) {
     if (j < 4) {
@@ -150,42 +221,150 @@ struct Fmt<EMBER_TYPE_Q4_K> {
       *mn = (ubyte(raw, 8 + j) >> 4) | ((ubyte(raw, 4 + j) >> 6) << 4);
     }
   }
-  __device__ static float dot(const uint32_t* raw, const float* x, int c) {
+  template <int MT>
+  __device__ static void dot_tokens(const uint32_t* raw, const uint8_t* lds, int row_lds, int c, int K, int nvalid,
+                                    float* out) {
     const float d = half_bits_to_float(raw[0] & 0xffff), dmin = half_bits_to_float(raw[0] >> 16);
     const int q = c & 3;
     int scA, mA, scB, mB;
     scale_min(raw, 2 * q, &scA, &mA);
     scale_min(raw, 2 * q + 1, &scB, &mB);
-    float sA = 0.0f, sB = 0.0f, xA = 0.0f, xB = 0.0f;
+    int ia[MT], ib[MT];
 #pragma unroll
-    for (int l = 0; l < 32; ++l) {
-      const uint32_t byte = (raw[4 + (l >> 2)] >> (8 * (l & 3))) & 0xff;
-      sA = __builtin_fmaf((float)(byte & 0xf), x[l], sA);
-      sB = __builtin_fmaf((float)(byte >> 4), x[32 + l], sB);
-      xA += x[l];
-      xB += x[32 + l];
+    for (int m = 0; m < MT; ++m) ia[m] = ib[m] = 0;
+#pragma unroll
+    for (int k2 = 0; k2 < 8; k2 += 2) {
+      uint32_t ua[4], ub[4];
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const uint32_t w = raw[4 + k2 + kk];
+        const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+        ua[2 * kk] = u16pair(lo, 0);
+        ua[2 * kk + 1] = u16pair(lo, 1);
+        ub[2 * kk] = u16pair(hi, 0);
+        ub[2 * kk + 1] = u16pair(hi, 1);
+      }
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        if (m < nvalid) {
+          const uint8_t* xr = lds + m * row_lds + (size_t)c * 128;
+          const u32x4 xa = *reinterpret_cast<const u32x4*>(xr + 8 * k2);
+          const u32x4 xb = *reinterpret_cast<const u32x4*>(xr + 64 + 8 * k2);
+          ia[m] = sdot2(ua[0], xa.x, ia[m]);
+          ia[m] = sdot2(ua[1], xa.y, ia[m]);
+          ia[m] = sdot2(ua[2], xa.z, ia[m]);
+          ia[m] = sdot2(ua[3], xa.w, ia[m]);
+          ib[m] = sdot2(ub[0], xb.x, ib[m]);
+          ib[m] = sdot2(ub[1], xb.y, ib[m]);
+          ib[m] = sdot2(ub[2], xb.z, ib[m]);
+          ib[m] = sdot2(ub[3], xb.w, ib[m]);
+        }
+      }
     }
-    return (d * (float)scA) * sA - (dmin * (float)mA) * xA + (d * (float)scB) * sB - (dmin * (float)mB) * xB;
+    const float dA = d * (float)scA, mAf = dmin * (float)mA, dB = d * (float)scB, mBf = dmin * (float)mB;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      if (m < nvalid) {
+        const uint8_t* xr = lds + m * row_lds;
+        const float* sc = reinterpret_cast<const float*>(xr + K * 2) + 2 * c;
+        const int* sm = reinterpret_cast<const int*>(xr + K * 2 + (K / 32) * 4) + 2 * c;
+        out[m] += sc[0] * (dA * (float)ia[m] - mAf * (float)sm[0]) + sc[1] * (dB * (float)ib[m] - mBf * (float)sm[1]);
+      }
+    }
   }
 };
 
+// Bytes of one token's activation row as staged in LDS: f32 values, or int16 values followed by the
+// per-32-block scales and sums.
+__host__ __device__ inline int act_lds_bytes(bool qx, int K) { return qx ? K * 2 + (K / 32) * 8 : K * 4; }
+
+// Block-cooperative copy of activation row `row` into LDS slot `dst` (16-byte granules).
+__device__ inline void stage_row(bool qx, const ProjArgs& a, int row, uint8_t* dst) {
+  const int K = a.K;
+  if (qx) {
+    copy16_to_lds(dst, a.act.q + (size_t)row * K, K / 8);
+    float* sc = reinterpret_cast<float*>(dst + K * 2);
+    int* sm = reinterpret_cast<int*>(sc + K / 32);
+    const int nb = K / 32;
+    if (nb % 4 == 0) {  // rows of scales / sums start on 16-byte boundaries
+      copy16_to_lds(sc, a.act.scale + (size_t)row * nb, nb / 4);
+      copy16_to_lds(sm, a.act.sum + (size_t)row * nb, nb / 4);
+    } else {
+      for (int i = threadIdx.x; i < nb; i += blockDim.x) {
+        sc[i] = a.act.scale[(size_t)row * nb + i];
+        sm[i] = a.act.sum[(size_t)row * nb + i];
+      }
+    }
+  } else {
+    copy16_to_lds(dst, a.in + (size_t)row * K, K / 4);
+  }
+}
+
+// Activation operands of chunk c (element offset c*CE) from a staged row.
 template <int FMT>
-__device__ inline void load_x(const float* row, int c, int K, float* xv) {
+__device__ inline void lds_xf(const uint8_t* row, int c, int K, XF& x) {
   constexpr int CE = Fmt<FMT>::CE;
-  const float4* p = reinterpret_cast<const float4*>(row + (size_t)c * CE);
+  const float* p = reinterpret_cast<const float*>(row) + (size_t)c * CE;
   const int n = K - c * CE;
 #pragma unroll
   for (int v = 0; v < CE / 4; ++v) {
-    const float4 q = (4 * v < n) ? p[v] : make_float4(0.f, 0.f, 0.f, 0.f);
-    xv[4 * v] = q.x;
-    xv[4 * v + 1] = q.y;
-    xv[4 * v + 2] = q.z;
-    xv[4 * v + 3] = q.w;
+    const float4 q = (4 * v < n) ? *reinterpret_cast<const float4*>(p + 4 * v) : make_float4(0.f, 0.f, 0.f, 0.f);
+    x.v[4 * v] = q.x;
+    x.v[4 * v + 1] = q.y;
+    x.v[4 * v + 2] = q.z;
+    x.v[4 * v + 3] = q.w;
+  }
+}
+__device__ inline void lds_xq(const uint8_t* row, int c, int K, XQ& x) {
+  const uint8_t* p = row + (size_t)c * 128;
+#pragma unroll
+  for (int v = 0; v < 8; ++v) {
+    const u32x4 q = *reinterpret_cast<const u32x4*>(p + 16 * v);
+    x.w[4 * v] = q.x;
+    x.w[4 * v + 1] = q.y;
+    x.w[4 * v + 2] = q.z;
+    x.w[4 * v + 3] = q.w;
+  }
+  const float* sc = reinterpret_cast<const float*>(row + K * 2);
+  const int* sm = reinterpret_cast<const int*>(sc + K / 32);
+  x.s[0] = sc[2 * c];
+  x.s[1] = sc[2 * c + 1];
+  x.sum[0] = sm[2 * c];
+  x.sum[1] = sm[2 * c + 1];
+}
+
+// dot_tokens for the float formats: decode the chunk once per token from the staged f32 rows.
+template <int FMT, int MT>
+__device__ inline void dot_tokens_f(const uint32_t* raw, const uint8_t* lds, int row_lds, int c, int K, int nvalid,
+                                    float* out);
+template <int MT>
+__device__ void Fmt<EMBER_TYPE_F32>::dot_tokens(const uint32_t* raw, const uint8_t* lds, int row_lds, int c, int K,
+                                                int nvalid, float* out) {
+  dot_tokens_f<EMBER_TYPE_F32, MT>(raw, lds, row_lds, c, K, nvalid, out);
+}
+template <int FMT>
+template <int MT>
+__device__ void FmtHalf<FMT>::dot_tokens(const uint32_t* raw, const uint8_t* lds, int row_lds, int c, int K,
+                                         int nvalid, float* out) {
+  dot_tokens_f<FMT, MT>(raw, lds, row_lds, c, K, nvalid, out);
+}
+template <int FMT, int MT>
+__device__ inline void dot_tokens_f(const uint32_t* raw, const uint8_t* lds, int row_lds, int c, int K, int nvalid,
+                                    float* out) {
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    if (m < nvalid) {
+      XF xv;
+      lds_xf<FMT>(lds + m * row_lds, c, K, xv);
+      out[m] += Fmt<FMT>::dot(raw, xv, c);
+    }
   }
 }
 
 __device__ inline float swiglu(float g, float u) { return g * (1.0f / (1.0f + expf_glibc(-g))) * u; }
 
+// One projection pass. Thread layout: lane group of L lanes per row slot; RR rows per step; MT tokens
+// per pass over the weights. Steps (row group, chunk round) are double-buffered.
 template <int FMT, int RR, int MT, bool GATED>
 __global__ void __launch_bounds__(256) proj_kernel(ProjArgs a, int L_log2) {
   using F = Fmt<FMT>;
@@ -193,8 +372,9 @@ __global__ void __launch_bounds__(256) proj_kernel(ProjArgs a, int L_log2) {
   const int L = 1 << L_log2;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int sub = lane >> L_log2, rl = lane & (L - 1);
-  const int rows_per_wave = 64 >> L_log2;
-  const int RPW = 4 * rows_per_wave;
+  const int slots_per_block = 4 * (64 >> L_log2);
+  const int slot = blockIdx.x * slots_per_block + wave * (64 >> L_log2) + sub;
+  const int nslots = gridDim.x * slots_per_block;
   int e = 0, p0 = 0, M = a.T;
   if (a.used) {
     if ((int)blockIdx.y >= *a.n_used) return;
@@ -205,14 +385,26 @@ __global__ void __launch_bounds__(256) proj_kernel(ProjArgs a, int L_log2) {
   const int K = a.K;
   const int64_t rb = F::row_bytes(K);
   const int C = (K + F::CE - 1) / F::CE;
-  const uint8_t* W[2];
-  W[0] = static_cast<const uint8_t*>(a.w0) + (int64_t)e * a.expert_stride;
-  W[1] = GATED ? static_cast<const uint8_t*>(a.w1) + (int64_t)e * a.expert_stride : W[0];
-  int row[RR];
-#pragma unroll
-  for (int i = 0; i < RR; ++i) row[i] = blockIdx.x * (RPW * RR) + wave * rows_per_wave + sub + RPW * i;
+  const int NC = (C + L - 1) / L;  // chunk rounds per row (uniform across the lane group)
+  const uint8_t* W0 = static_cast<const uint8_t*>(a.w0) + (int64_t)e * a.expert_stride;
+  const uint8_t* W1 = GATED ? static_cast<const uint8_t*>(a.w1) + (int64_t)e * a.expert_stride : W0;
+  const int ngroups = (a.rows + RR - 1) / RR;
+  // number of steps this slot walks: row groups slot, slot + nslots, ... times NC chunk rounds
+  const int my_groups = slot < ngroups ? (ngroups - 1 - slot) / nslots + 1 : 0;
+  const int nsteps = my_groups * NC;
 
+  extern __shared__ __align__(16) uint8_t act_lds[];
+  const int row_lds = act_lds_bytes(F::QX, K);
   for (int m0 = 0; m0 < M; m0 += MT) {
+    __syncthreads();  // the previous token group's rows are no longer read
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      if (m0 + m < M) {
+        const int p = p0 + m0 + m;
+        stage_row(F::QX, a, a.in_by_perm ? a.perm[p] / a.k : p, act_lds + m * row_lds);
+      }
+    }
+    __syncthreads();
     float acc[G][RR][MT];
 #pragma unroll
     for (int g = 0; g < G; ++g)
@@ -220,58 +412,65 @@ __global__ void __launch_bounds__(256) proj_kernel(ProjArgs a, int L_log2) {
       for (int i = 0; i < RR; ++i)
 #pragma unroll
         for (int m = 0; m < MT; ++m) acc[g][i][m] = 0.0f;
-    int in_row[MT];
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      const int p = p0 + m0 + m;
-      in_row[m] = (m0 + m < M) ? (a.in_by_perm ? a.perm[p] / a.k : p) : 0;
-    }
-    for (int c = rl; c < C; c += L) {
+    const int nvalid = min(MT, M - m0);
+    for (int st = 0; st < nsteps; ++st) {
+      const int grp = slot + (st / NC) * nslots;
+      const int c = rl + (st % NC) * L;
       uint32_t raw[G][RR][F::NW];
 #pragma unroll
       for (int g = 0; g < G; ++g)
 #pragma unroll
         for (int i = 0; i < RR; ++i) {
-          if (row[i] < a.rows) {
-            F::load(W[g] + (int64_t)row[i] * rb, c, K, raw[g][i]);
+          const int r = grp * RR + i;
+          if (c < C && r < a.rows) {
+            F::load((g ? W1 : W0) + (int64_t)r * rb, c, K, raw[g][i]);
           } else {
 #pragma unroll
             for (int w = 0; w < F::NW; ++w) raw[g][i][w] = 0u;
           }
         }
+      if (c < C) {
 #pragma unroll
-      for (int m = 0; m < MT; ++m) {
-        if (m0 + m < M) {
-          float xv[F::CE];
-          load_x<FMT>(a.in + (size_t)in_row[m] * K, c, K, xv);
+        for (int g = 0; g < G; ++g)
 #pragma unroll
-          for (int g = 0; g < G; ++g)
-#pragma unroll
-            for (int i = 0; i < RR; ++i) acc[g][i][m] += F::dot(raw[g][i], xv, c);
-        }
+          for (int i = 0; i < RR; ++i) F::template dot_tokens<MT>(raw[g][i], act_lds, row_lds, c, K, nvalid, acc[g][i]);
       }
-    }
+      if (st % NC == NC - 1) {  // row group complete: reduce over the lane group and write
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+        for (int g = 0; g < G; ++g)
 #pragma unroll
-      for (int i = 0; i < RR; ++i)
+          for (int i = 0; i < RR; ++i)
 #pragma unroll
-        for (int m = 0; m < MT; ++m)
-          for (int off = L >> 1; off >= 1; off >>= 1) acc[g][i][m] += __shfl_xor(acc[g][i][m], off, 64);
-    if (rl == 0) {
+            for (int m = 0; m < MT; ++m) {
+              float v = acc[g][i][m];
+              for (int off = L >> 1; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+              acc[g][i][m] = v;
+            }
+        if (rl == 0) {
 #pragma unroll
-      for (int i = 0; i < RR; ++i) {
-        if (row[i] >= a.rows) continue;
+          for (int i = 0; i < RR; ++i) {
+            const int r = grp * RR + i;
+            if (r >= a.rows) continue;
 #pragma unroll
-        for (int m = 0; m < MT; ++m) {
-          if (m0 + m >= M) continue;
-          const size_t o = (size_t)(p0 + m0 + m) * a.rows + row[i];
-          a.out[o] = GATED ? swiglu(acc[0][i][m], acc[G - 1][i][m]) : acc[0][i][m];
+            for (int m = 0; m < MT; ++m) {
+              if (m >= nvalid) continue;
+              const size_t o = (size_t)(p0 + m0 + m) * a.rows + r;
+              a.out[o] = GATED ? swiglu(acc[0][i][m], acc[G - 1][i][m]) : acc[0][i][m];
+            }
+          }
         }
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+          for (int i = 0; i < RR; ++i)
+#pragma unroll
+            for (int m = 0; m < MT; ++m) acc[g][i][m] = 0.0f;
       }
     }
   }
 }
+
+constexpr int kProjLdsBytes = 64 * 1024;  // activation rows staged per block
 
 template <int FMT, int RR, bool GATED>
 int launch_proj_fmt(const ProjArgs& a, int MT, hipStream_t st) {
@@ -279,60 +478,119 @@ int launch_proj_fmt(const ProjArgs& a, int MT, hipStream_t st) {
   const int C = (a.K + F::CE - 1) / F::CE;
   int L_log2 = 0;
   while ((1 << L_log2) < C && L_log2 < 6) ++L_log2;
-  const int RPW = 4 * (64 >> L_log2);
-  dim3 grid((a.rows + RPW * RR - 1) / (RPW * RR), a.max_segments);
+  const int slots_per_block = 4 * (64 >> L_log2);
+  const int ngroups = (a.rows + RR - 1) / RR;
+  // enough blocks to fill the chip (~8 per CU over all segments), each slot walking a few groups
+  const int segs = std::max(a.max_segments, 1);
+  int blocks = (2048 + segs - 1) / segs;
+  blocks = std::min(blocks, (ngroups + slots_per_block - 1) / slots_per_block);
+  blocks = std::max(blocks, 1);
+  dim3 grid(blocks, a.max_segments);
   if (grid.y == 0) return EMBER_OK;
+  const int row_lds = act_lds_bytes(F::QX, a.K);
+  while (MT > 1 && MT * row_lds > kProjLdsBytes) MT >>= 1;
+  if (row_lds > kProjLdsBytes) return EMBER_ERR_SHAPE;
+  const size_t lds = (size_t)MT * row_lds;
   if (MT == 1)
-    proj_kernel<FMT, RR, 1, GATED><<<grid, 256, 0, st>>>(a, L_log2);
+    proj_kernel<FMT, RR, 1, GATED><<<grid, 256, lds, st>>>(a, L_log2);
   else if (MT == 2)
-    proj_kernel<FMT, RR, 2, GATED><<<grid, 256, 0, st>>>(a, L_log2);
+    proj_kernel<FMT, RR, 2, GATED><<<grid, 256, lds, st>>>(a, L_log2);
   else
-    proj_kernel<FMT, RR, 4, GATED><<<grid, 256, 0, st>>>(a, L_log2);
+    proj_kernel<FMT, RR, 4, GATED><<<grid, 256, lds, st>>>(a, L_log2);
   return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
 }
 
 template <bool GATED>
 int launch_proj_gated(const ProjArgs& a, int MT, hipStream_t st) {
-  constexpr int RR = GATED ? 2 : 4;
   switch (a.type) {
-    case EMBER_TYPE_F32: return launch_proj_fmt<EMBER_TYPE_F32, GATED ? 1 : 2, GATED>(a, MT, st);
-    case EMBER_TYPE_F16: return launch_proj_fmt<EMBER_TYPE_F16, RR, GATED>(a, MT, st);
-    case EMBER_TYPE_BF16: return launch_proj_fmt<EMBER_TYPE_BF16, RR, GATED>(a, MT, st);
-    case EMBER_TYPE_Q8_0: return launch_proj_fmt<EMBER_TYPE_Q8_0, RR, GATED>(a, MT, st);
-    case EMBER_TYPE_Q4_K: return launch_proj_fmt<EMBER_TYPE_Q4_K, RR, GATED>(a, MT, st);
+    case EMBER_TYPE_F32: return launch_proj_fmt<EMBER_TYPE_F32, 1, GATED>(a, MT, st);
+    case EMBER_TYPE_F16: return launch_proj_fmt<EMBER_TYPE_F16, 1, GATED>(a, MT, st);
+    case EMBER_TYPE_BF16: return launch_proj_fmt<EMBER_TYPE_BF16, 1, GATED>(a, MT, st);
+    case EMBER_TYPE_Q8_0: return launch_proj_fmt<EMBER_TYPE_Q8_0, GATED ? 1 : 2, GATED>(a, MT, st);
+    case EMBER_TYPE_Q4_K: return launch_proj_fmt<EMBER_TYPE_Q4_K, GATED ? 1 : 2, GATED>(a, MT, st);
     default: return EMBER_ERR_TYPE;
   }
 }
+
+bool type_quantizes_activations(int type) { return type == EMBER_TYPE_Q8_0 || type == EMBER_TYPE_Q4_K; }
 
 int launch_projection(const ProjArgs& a, hipStream_t st) {
   const int MT = a.T <= 1 ? 1 : (a.T <= 2 ? 2 : 4);
   return a.gated ? launch_proj_gated<true>(a, MT, st) : launch_proj_gated<false>(a, MT, st);
 }
 
+// Per-32-block int16 quantization of activation rows: q = rint(x / s), s = amax / 32767 (s = 0 for
+// an all-zero block), plus the block's sum of q. One thread per block of 32.
+__global__ void __launch_bounds__(256) quantize_act_kernel(const float* __restrict__ in, int rows, int K,
+                                                           int16_t* __restrict__ q, float* __restrict__ scale,
+                                                           int* __restrict__ sum) {
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int nb = K / 32;
+  if (b >= (int64_t)rows * nb) return;
+  const float4* p = reinterpret_cast<const float4*>(in + b * 32);
+  float v[32];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float4 t = p[i];
+    v[4 * i] = t.x;
+    v[4 * i + 1] = t.y;
+    v[4 * i + 2] = t.z;
+    v[4 * i + 3] = t.w;
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  const float s = amax / 32767.0f;
+  const float inv = amax > 0.0f ? 32767.0f / amax : 0.0f;
+  int tot = 0;
+  uint32_t packed[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int a0 = (int)__builtin_rintf(v[2 * i] * inv), a1 = (int)__builtin_rintf(v[2 * i + 1] * inv);
+    const int c0 = max(-32767, min(32767, a0)), c1 = max(-32767, min(32767, a1));
+    tot += c0 + c1;
+    packed[i] = (uint32_t)(uint16_t)c0 | ((uint32_t)(uint16_t)c1 << 16);
+  }
+  u32x4* dst = reinterpret_cast<u32x4*>(q + b * 32);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) dst[i] = u32x4{packed[4 * i], packed[4 * i + 1], packed[4 * i + 2], packed[4 * i + 3]};
+  scale[b] = s;
+  sum[b] = tot;
+}
+
+int launch_quantize_act(const float* in, int rows, int K, const ActQ& a, hipStream_t st) {
+  const int64_t n = (int64_t)rows * (K / 32);
+  if (n <= 0) return EMBER_OK;
+  quantize_act_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(in, rows, K, a.q, a.scale, a.sum);
+  return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
+}
+
 // out[t][o] = sum over j ascending (= experts ascending) of gate[t][j] * y[pos[t*k+j]][o], starting
 // from 0 (utils.cpp:736, 744-747); then (x * scale) + 0 (the IR's affine, graph_ir.cpp:923, 2727)
-// and + the shared expert's row (graph_ir.cpp:926-928).
+// and + the shared expert's row (graph_ir.cpp:926-928). One thread per output element.
 __global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ y, const float* __restrict__ gates,
                                                       const int32_t* __restrict__ pos,
                                                       const float* __restrict__ y_shared, float scale, int k, int d,
                                                       float* __restrict__ out) {
-  const int t = blockIdx.x;
-  for (int o = threadIdx.x; o < d; o += blockDim.x) {
-    float acc = 0.0f;
-    for (int j = 0; j < k; ++j) {
-      const int p = pos[(size_t)t * k + j];
-      if (p >= 0) acc = acc + gates[(size_t)t * k + j] * y[(size_t)p * d + o];
-    }
-    if (scale != 1.0f) acc = acc * scale + 0.0f;
-    if (y_shared) acc = acc + y_shared[(size_t)t * d + o];
-    out[(size_t)t * d + o] = acc;
+  const int t = blockIdx.y;
+  const int o = blockIdx.x * blockDim.x + threadIdx.x;
+  if (o >= d) return;
+  float acc = 0.0f;
+  for (int j = 0; j < k; ++j) {
+    const int p = pos[(size_t)t * k + j];
+    const float g = gates[(size_t)t * k + j];
+    if (p >= 0) acc = acc + g * y[(size_t)p * d + o];
   }
+  if (scale != 1.0f) acc = acc * scale + 0.0f;
+  if (y_shared) acc = acc + y_shared[(size_t)t * d + o];
+  out[(size_t)t * d + o] = acc;
 }
 
 int launch_combine(const float* y, const float* gates, const int32_t* pos, const float* y_shared, float scale, int T,
                    int k, int d, float* out, hipStream_t st) {
   if (T <= 0) return EMBER_OK;
-  combine_kernel<<<T, 256, 0, st>>>(y, gates, pos, y_shared, scale, k, d, out);
+  dim3 grid((d + 255) / 256, T);
+  combine_kernel<<<grid, 256, 0, st>>>(y, gates, pos, y_shared, scale, k, d, out);
   return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
 }
 

@@ -2,10 +2,31 @@
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <algorithm>
 #include "ember_moe.h"
 #include "moe_math.hpp"
 
 namespace ember_moe {
+
+// Block-cooperative copy of n 16-byte granules from global memory to LDS. Loads are issued in
+// batches of 8 per thread before any store, so a thread waits for one memory latency per batch
+// instead of one per granule.
+__device__ inline void copy16_to_lds(void* dst, const void* src, int n) {
+  typedef uint32_t v4 __attribute__((ext_vector_type(4)));
+  v4* d = static_cast<v4*>(dst);
+  const v4* g = static_cast<const v4*>(src);
+  const int stride = blockDim.x;
+  for (int base = threadIdx.x; base < n; base += 8 * stride) {
+    v4 t[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (base + u * stride < n) t[u] = g[base + u * stride];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (base + u * stride < n) d[base + u * stride] = t[u];
+  }
+}
 
 // Device buffers of the dispatch step, carved from the caller's scratch.
 struct DispatchScratch {
@@ -22,6 +43,21 @@ int launch_router_logits(const float* x, int T, int d, int E, const float* R, fl
 int launch_route(const float* logits, int T, int E, int k, int renorm, int routed, int sigmoid, const float* bias,
                  int groups_n, int groups_top, int32_t* idx, float* gates, hipStream_t st);
 int launch_dispatch(const int32_t* idx, int T, int k, int E, const DispatchScratch& ds, hipStream_t st);
+// Routing + dispatch; one fused kernel for decode-sized batches, else launch_route + launch_dispatch.
+int launch_route_dispatch(const float* logits, int T, int E, int k, int renorm, int routed, int sigmoid,
+                          const float* bias, int groups_n, int groups_top, int32_t* idx, float* gates,
+                          const DispatchScratch& ds, hipStream_t st);
+
+// Activations quantized to int16 per 32-element block (for Q8_0 / Q4_K weights).
+struct ActQ {
+  int16_t* q;     // [rows][K]
+  float* scale;   // [rows][K/32]
+  int* sum;       // [rows][K/32]
+  int K;
+};
+
+bool type_quantizes_activations(int type);
+int launch_quantize_act(const float* in, int rows, int K, const ActQ& a, hipStream_t st);
 
 // One projection over a set of token segments: out[p][row] for rows [0, rows) of a
 // [rows][K] matrix per expert (or the single shared matrix).
@@ -31,7 +67,8 @@ struct ProjArgs {
   int type;            // ggml type of w0 / w1
   int rows, K;         // matrix shape per expert
   int64_t expert_stride;  // bytes between consecutive experts' matrices
-  const float* in;     // activations: x [T][K] (gated) or h [npos][K] (down)
+  const float* in;     // activations: x [T][K] (gated) or h [npos][K] (down), f32
+  ActQ act;            // the same activations quantized (used when `type` quantizes activations)
   float* out;          // h [npos][rows] (gated) or y [npos][rows] (down)
   // Segments: routed (offsets/used/n_used/perm valid, k > 0) or shared (one segment of T tokens).
   const int32_t* offsets;

@@ -14,6 +14,8 @@
 namespace ember_moe {
 using namespace ember_math;
 
+constexpr int kRouterLdsFloats = 16384;  // 64 KiB of LDS for the small-T router
+
 // ---------------------------------------------------------------------------------------------
 // Router logits, small T: one thread per (token, expert, chain); the 8 chains of a pair are 8
 // consecutive lanes of one wave and are combined there in the reference's order.
@@ -41,6 +43,51 @@ __global__ void __launch_bounds__(256) router_logits_direct(const float* __restr
     for (int i = n8; i < d; ++i) tail = tail + (double)rr[i] * (double)xr[i];
     const double v = (((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]))) + tail;
     logits[pair] = (float)v;
+  }
+}
+
+// Router logits, small T: block (expert group, token) stages x[t] and EG router rows in LDS with
+// coalesced 16-byte loads, then 8*EG threads run the eight FP64 chains of each expert from LDS (rows
+// padded by 8 floats so the chains of different experts fall in different banks).
+__host__ __device__ inline int router_lds_rows(int d) { return max(1, min(32, kRouterLdsFloats / (d + 8) - 1)); }
+
+__global__ void __launch_bounds__(256) router_logits_lds(const float* __restrict__ x, const float* __restrict__ R,
+                                                         float* __restrict__ logits, int T, int d, int E) {
+  extern __shared__ __align__(16) float rl_lds[];
+  const int EG = router_lds_rows(d);
+  const int t = blockIdx.y, e0 = blockIdx.x * EG;
+  const int ne = min(EG, E - e0);
+  const int ld = d + 8;
+  float* xs = rl_lds;
+  float* rs = rl_lds + ld;
+  const bool vec = (d % 4) == 0;
+  if (vec) {
+    copy16_to_lds(xs, x + (size_t)t * d, d / 4);
+    for (int j = 0; j < ne; ++j) copy16_to_lds(rs + j * ld, R + (size_t)(e0 + j) * d, d / 4);
+  } else {
+    for (int i = threadIdx.x; i < d; i += blockDim.x) xs[i] = x[(size_t)t * d + i];
+    for (int j = 0; j < ne; ++j)
+      for (int i = threadIdx.x; i < d; i += blockDim.x) rs[j * ld + i] = R[(size_t)(e0 + j) * d + i];
+  }
+  __syncthreads();
+  const int c = threadIdx.x & 7, j = threadIdx.x >> 3;
+  const int n8 = d - d % 8;
+  double acc = 0.0;
+  if (j < ne) {
+    const float* rr = rs + j * ld;
+#pragma unroll 8
+    for (int i = c; i < n8; i += 8) acc = acc + (double)rr[i] * (double)xs[i];
+  }
+  const int lane = threadIdx.x & 63;
+  double a[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) a[q] = __shfl(acc, (lane & ~7) + q, 64);
+  if (j < ne && c == 0) {
+    const float* rr = rs + j * ld;
+    double tail = 0.0;
+    for (int i = n8; i < d; ++i) tail = tail + (double)rr[i] * (double)xs[i];
+    const double v = (((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]))) + tail;
+    logits[(size_t)t * E + e0 + j] = (float)v;
   }
 }
 
@@ -229,18 +276,14 @@ __host__ __device__ inline size_t route_wave_lds(int E) {
   return (bytes + 15) & ~(size_t)15;
 }
 
-// One wave per token. Softmax scoring without bias / groups (moe_ffn_f32_cpu) runs a parallel argmax
-// whose result equals the serial strict-> scan for NaN-free rows; rows with a NaN, and the
-// DeepSeek-style router, run the reference's serial algorithm on lane 0.
-__global__ void __launch_bounds__(256) route_kernel(const float* __restrict__ logits, int T, int E, int k, int renorm,
-                                                    int routed, int sigmoid, const float* __restrict__ bias,
-                                                    int groups_n, int groups_top, int32_t* __restrict__ idx,
-                                                    float* __restrict__ gates) {
-  extern __shared__ __align__(16) unsigned char lds_raw[];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int t = blockIdx.x * 4 + wave;
-  if (t >= T) return;
-  unsigned char* wl = lds_raw + (size_t)wave * route_wave_lds(E);
+// Routes one token on one wave (all 64 lanes call it). Softmax scoring without bias / groups
+// (moe_ffn_f32_cpu) runs a parallel argmax whose result equals the serial strict-> scan for NaN-free
+// rows; rows with a NaN, and the DeepSeek-style router, run the reference's serial algorithm on
+// lane 0. wl: route_wave_lds(E) bytes of LDS owned by this wave.
+__device__ void route_token(const float* __restrict__ r, int E, int k, int renorm, int routed, int sigmoid,
+                            const float* __restrict__ bias, int groups_n, int groups_top, unsigned char* wl,
+                            int32_t* __restrict__ idx_t, float* __restrict__ gate_t) {
+  const int lane = threadIdx.x & 63;
   double* ex = reinterpret_cast<double*>(wl);
   float* s = reinterpret_cast<float*>(wl + (size_t)E * 8);
   float* cbuf = s + E;
@@ -248,10 +291,6 @@ __global__ void __launch_bounds__(256) route_kernel(const float* __restrict__ lo
   char* cand = reinterpret_cast<char*>(picks + 64);
   char* taken = cand + E;
   float* row = reinterpret_cast<float*>(wl + route_wave_lds(E) - (size_t)E * 4);
-  const float* r = logits + (size_t)t * E;
-  int32_t* idx_t = idx + (size_t)t * k;
-  float* gate_t = gates + (size_t)t * k;
-
   bool has_nan = false;
   for (int e = lane; e < E; e += 64) {
     const float v = r[e];
@@ -327,6 +366,18 @@ __global__ void __launch_bounds__(256) route_kernel(const float* __restrict__ lo
       gate_t[lane] = 0.0f;
     }
   }
+}
+
+__global__ void __launch_bounds__(256) route_kernel(const float* __restrict__ logits, int T, int E, int k, int renorm,
+                                                    int routed, int sigmoid, const float* __restrict__ bias,
+                                                    int groups_n, int groups_top, int32_t* __restrict__ idx,
+                                                    float* __restrict__ gates) {
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  const int wave = threadIdx.x >> 6;
+  const int t = blockIdx.x * 4 + wave;
+  if (t >= T) return;
+  route_token(logits + (size_t)t * E, E, k, renorm, routed, sigmoid, bias, groups_n, groups_top,
+              lds_raw + (size_t)wave * route_wave_lds(E), idx + (size_t)t * k, gates + (size_t)t * k);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -413,12 +464,71 @@ __global__ void __launch_bounds__(256) dispatch_scatter(const int32_t* __restric
   pos[s] = p;
 }
 
+// Decode-sized batches (T <= 8 tokens, T*k <= 512 slots, E <= 256): routing and the whole dispatch in
+// one block of 512 threads. Wave w routes token w; then each slot takes its rank among equal experts
+// at lower slots (a scan of the idx list in LDS), the per-expert offsets come from LDS counts.
+constexpr int kSmallT = 8, kSmallSlots = 512, kSmallE = 256;
+
+__global__ void __launch_bounds__(512) route_dispatch_small(const float* __restrict__ logits, int T, int E, int k,
+                                                            int renorm, int routed, int sigmoid,
+                                                            const float* __restrict__ bias, int groups_n,
+                                                            int groups_top, int32_t* __restrict__ idx,
+                                                            float* __restrict__ gates, DispatchScratch ds) {
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  const int wave = threadIdx.x >> 6;
+  const size_t wl = route_wave_lds(E);
+  int* sidx = reinterpret_cast<int*>(lds_raw + kSmallT * wl);
+  int* cnt = sidx + kSmallSlots;
+  if (wave < T)
+    route_token(logits + (size_t)wave * E, E, k, renorm, routed, sigmoid, bias, groups_n, groups_top,
+                lds_raw + wave * wl, idx + (size_t)wave * k, gates + (size_t)wave * k);
+  for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[e] = 0;
+  __syncthreads();  // idx (global, written by this block) is visible block-wide
+  const int n = T * k;
+  const int sl = threadIdx.x;
+  int e = -1;
+  if (sl < n) {
+    e = idx[sl];
+    sidx[sl] = e;
+    if (e >= 0) atomicAdd(&cnt[e], 1);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int run = 0, nu = 0;
+    for (int q = 0; q < E; ++q) {
+      const int c = cnt[q];
+      ds.offsets[q] = run;
+      cnt[q] = run;
+      run += c;
+      if (c > 0) ds.used[nu++] = q;
+    }
+    ds.offsets[E] = run;
+    *ds.n_used = nu;
+  }
+  __syncthreads();
+  if (sl < n) {
+    if (e < 0) {
+      ds.pos[sl] = -1;
+    } else {
+      int rk = 0;
+      for (int q = 0; q < sl; ++q) rk += (sidx[q] == e);
+      const int p = cnt[e] + rk;
+      ds.perm[p] = sl;
+      ds.pos[sl] = p;
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------------------------
 // Host-side launchers.
 
 int launch_router_logits(const float* x, int T, int d, int E, const float* R, float* logits, hipStream_t st) {
   if (T <= 0) return EMBER_OK;
-  if (T >= 32 && E >= 8) {
+  if (T < 32 && 2 * (d + 8) <= kRouterLdsFloats) {
+    const int EG = router_lds_rows(d);
+    dim3 grid((E + EG - 1) / EG, T);
+    router_logits_lds<<<grid, 256, (size_t)(EG + 1) * (d + 8) * sizeof(float), st>>>(x, R, logits, T, d, E);
+  } else if (T >= 32 && E >= 8) {
     dim3 grid((T + RL_TT - 1) / RL_TT, (E + RL_TE - 1) / RL_TE);
     router_logits_tiled<<<grid, 256, 0, st>>>(x, R, logits, T, d, E);
   } else {
@@ -434,6 +544,22 @@ int launch_route(const float* logits, int T, int E, int k, int renorm, int route
   const size_t lds = 4 * route_wave_lds(E);
   route_kernel<<<(T + 3) / 4, 256, lds, st>>>(logits, T, E, k, renorm, routed, sigmoid, bias, groups_n, groups_top, idx,
                                               gates);
+  return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
+}
+
+bool route_dispatch_fused(int T, int E, int k) { return T <= kSmallT && T * k <= kSmallSlots && E <= kSmallE; }
+
+int launch_route_dispatch(const float* logits, int T, int E, int k, int renorm, int routed, int sigmoid,
+                          const float* bias, int groups_n, int groups_top, int32_t* idx, float* gates,
+                          const DispatchScratch& ds, hipStream_t st) {
+  if (T <= 0) return EMBER_OK;
+  if (!route_dispatch_fused(T, E, k)) {
+    int s = launch_route(logits, T, E, k, renorm, routed, sigmoid, bias, groups_n, groups_top, idx, gates, st);
+    return s ? s : launch_dispatch(idx, T, k, E, ds, st);
+  }
+  const size_t lds = kSmallT * route_wave_lds(E) + (size_t)(kSmallSlots + E) * sizeof(int);
+  route_dispatch_small<<<1, 512, lds, st>>>(logits, T, E, k, renorm, routed, sigmoid, bias, groups_n, groups_top, idx,
+                                            gates, ds);
   return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
 }
 
