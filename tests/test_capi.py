@@ -1,0 +1,91 @@
+"""CPU checks of the C ABI library: it loads, exports every function include/*.h declares, and its
+validation paths (which return before any GPU work) give the documented status codes."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import ember_moe as em
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared(header: str):
+    text = open(os.path.join(ROOT, "include", header)).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:[\w\s\*]+?)\b(ember_\w+)\s*\(", text, flags=re.M)))
+
+
+def exported(path: str):
+    import subprocess
+
+    out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True, check=True).stdout
+    return {ln.split()[-1] for ln in out.splitlines() if " T " in ln}
+
+
+def test_hip_library_exports_every_declared_symbol():
+    names = declared("ember_moe.h")
+    assert {"ember_moe_ffn", "ember_moe_scratch_bytes", "ember_moe_route", "ember_moe_router_logits",
+            "ember_moe_ffn_timed", "ember_moe_route_scratch_bytes", "ember_moe_strerror"} <= set(names)
+    missing = set(names) - exported(em.lib_path())
+    assert not missing, missing
+    em.lib()  # loads
+
+
+def test_host_library_exports_every_declared_symbol():
+    names = declared("ember_moe_host.h")
+    assert "ember_quantize" in names and "ember_fill_normal" in names
+    missing = set(names) - exported(em.host_lib_path())
+    assert not missing, missing
+
+
+def _layer(**kw):
+    L = em.Layer()
+    base = dict(d=256, d_ff=512, E=8, k=2, renorm=1, scoring=0, groups_n=1, groups_top=1, out_scale=1.0,
+                router=0x1000, gate=0x2000, gate_type=em.Q8_0, up=0x3000, up_type=em.Q8_0, down=0x4000,
+                down_type=em.Q8_0)
+    base.update(kw)
+    for k, v in base.items():
+        setattr(L, k, v)
+    return L
+
+
+def test_scratch_bytes_and_validation():
+    L = _layer()
+    n1, n64 = em.scratch_bytes(L, 1), em.scratch_bytes(L, 64)
+    assert 0 < n1 < n64
+    assert em.scratch_bytes(_layer(E=0), 1) == 0
+    assert em.scratch_bytes(_layer(k=65), 1) == 0
+    assert em.scratch_bytes(_layer(gate_type=99), 1) == 0
+    assert em.scratch_bytes(_layer(d=96), 1) == 0          # Q8_0 rows must be whole 64-element chunks
+    assert em.scratch_bytes(_layer(gate=0x2004), 1) == 0   # 16-byte alignment
+    assert em.scratch_bytes(_layer(groups_n=3), 1) == 0     # E % groups
+    assert em.scratch_bytes(_layer(groups_n=4, groups_top=2), 1) > 0
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(E=0), em.ERR_SHAPE), (dict(gate_type=3), em.ERR_TYPE), (dict(router=0), em.ERR_NULL),
+    (dict(down=0x4008), em.ERR_ALIGN), (dict(up_type=em.BF16), em.ERR_TYPE),
+])
+def test_ffn_rejects_bad_descriptors_without_launching(kw, status):
+    L = _layer(**kw)
+    lib = em.lib()
+    s = lib.ember_moe_ffn(ctypes.byref(L), 0x10000, 4, 0x20000, 0x30000, 1 << 30, None)
+    assert s == status, em.strerror(s)
+
+
+def test_ffn_rejects_small_scratch_and_null_io():
+    L = _layer()
+    lib = em.lib()
+    need = em.scratch_bytes(L, 4)
+    assert lib.ember_moe_ffn(ctypes.byref(L), 0x10000, 4, 0x20000, 0x30000, need - 1, None) == em.ERR_SCRATCH
+    assert lib.ember_moe_ffn(ctypes.byref(L), 0, 4, 0x20000, 0x30000, need, None) == em.ERR_NULL
+    assert lib.ember_moe_ffn(ctypes.byref(L), 0x10000, -1, 0x20000, 0x30000, need, None) == em.ERR_SHAPE
+    assert lib.ember_moe_ffn(ctypes.byref(L), 0, 0, 0, 0, 0, None) == em.OK  # T = 0: nothing to do
+
+
+def test_strerror():
+    for s in (em.OK, em.ERR_SHAPE, em.ERR_TYPE, em.ERR_SCRATCH, em.ERR_NULL, em.ERR_LAUNCH, em.ERR_ALIGN):
+        assert em.strerror(s) and em.strerror(s) != "unknown status"
