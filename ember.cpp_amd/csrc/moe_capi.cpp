@@ -13,6 +13,7 @@ namespace {
 
 constexpr int kMaxE = 512;  // route_kernel keeps one bit per (lane, 64-expert stripe) and LDS rows of E
 constexpr int kMaxK = 64;   // picks live in a 64-entry LDS array per wave
+constexpr int kGemmMinT = 32;  // from this many tokens the expert products run on the MFMA grouped GEMM
 
 size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
 
@@ -92,6 +93,8 @@ struct ActLayout {
 };
 struct Layout {
   size_t logits, idx, gates, offsets, perm, h, y, hs, ys;
+  size_t x16, h16, hs16, tiles, n_tiles;  // MFMA path
+  bool gemm, gemm_shared;
   ActLayout xq, hq, hsq;  // int16 activations of x, h and the shared expert's h (quantized formats)
   RouteLayout r;
   size_t end;
@@ -122,6 +125,15 @@ Layout layout(const ember_moe_layer* w, int T) {
   o = act_layout(o, T, w->d, qx, &l.xq);
   o = act_layout(o, slots, w->d_ff, type_quantizes_activations(w->down_type), &l.hq);
   o = act_layout(o, T, w->d_ff_shared, w->d_ff_shared > 0 && type_quantizes_activations(w->down_shared_type), &l.hsq);
+  l.gemm = T >= kGemmMinT && gemm_supported(w->gate_type, w->d) && gemm_supported(w->down_type, w->d_ff);
+  l.gemm_shared = w->d_ff_shared > 0 && T >= kGemmMinT && gemm_supported(w->gate_shared_type, w->d) &&
+                  gemm_supported(w->down_shared_type, w->d_ff_shared);
+  const size_t tiles = l.gemm ? (size_t)gemm_max_tiles(T, w->k, w->E) : 0;
+  l.x16 = o; o = align_up(o + (l.gemm || l.gemm_shared ? (size_t)T * w->d * 2 : 0));
+  l.h16 = o; o = align_up(o + (l.gemm ? slots * w->d_ff * 2 : 0));
+  l.hs16 = o; o = align_up(o + (l.gemm_shared ? (size_t)T * w->d_ff_shared * 2 : 0));
+  l.tiles = o; o = align_up(o + tiles * 8);
+  l.n_tiles = o; o = align_up(o + 4);
   l.end = o;
   return l;
 }
@@ -212,9 +224,52 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
   mark(ev, 3, st);
 
   const ActQ xq = act_at(scratch, l.xq, d);
-  if (type_quantizes_activations(w->gate_type) ||
-      (w->d_ff_shared > 0 && type_quantizes_activations(w->gate_shared_type)))
+  const bool gemv_x = (!l.gemm && type_quantizes_activations(w->gate_type)) ||
+                      (w->d_ff_shared > 0 && !l.gemm_shared && type_quantizes_activations(w->gate_shared_type));
+  if (gemv_x)
     if ((s = launch_quantize_act(x, T, d, xq, st))) return s;
+  _Float16* x16 = at<_Float16>(scratch, l.x16);
+  if (l.gemm || l.gemm_shared)
+    if ((s = launch_to_f16(x, (int64_t)T * d, x16, st))) return s;
+
+  if (l.gemm) {
+    int32_t* tiles = at<int32_t>(scratch, l.tiles);
+    int32_t* n_tiles = at<int32_t>(scratch, l.n_tiles);
+    if ((s = launch_build_tiles(offsets, E, tiles, n_tiles, st))) return s;
+    _Float16* h16 = at<_Float16>(scratch, l.h16);
+    GemmArgs g{};
+    g.A = x16;
+    g.perm = perm;
+    g.k = k;
+    g.T = T;
+    g.W0 = w->gate;
+    g.W1 = w->up;
+    g.type = w->gate_type;
+    g.row_bytes = row_bytes(w->gate_type, d);
+    g.expert_stride = g.row_bytes * d_ff;
+    g.N = d_ff;
+    g.K = d;
+    g.tiles = tiles;
+    g.n_tiles = n_tiles;
+    g.offsets = offsets;
+    g.out_h = h16;
+    const int mt = gemm_max_tiles(T, k, E);
+    if ((s = launch_gemm(g, true, mt, st))) return s;
+    mark(ev, 4, st);
+    g.A = h16;
+    g.perm = nullptr;
+    g.W0 = w->down;
+    g.W1 = nullptr;
+    g.type = w->down_type;
+    g.row_bytes = row_bytes(w->down_type, d_ff);
+    g.expert_stride = g.row_bytes * d;
+    g.N = d;
+    g.K = d_ff;
+    g.out_h = nullptr;
+    g.out_y = y;
+    if ((s = launch_gemm(g, false, mt, st))) return s;
+    mark(ev, 5, st);
+  } else {
 
   ProjArgs a{};
   a.offsets = offsets;
@@ -256,8 +311,34 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
   if ((s = launch_projection(a, st))) return s;
   mark(ev, 5, st);
 
+  }
   float* ys = nullptr;
-  if (w->d_ff_shared > 0) {
+  if (w->d_ff_shared > 0 && l.gemm_shared) {
+    ys = at<float>(scratch, l.ys);
+    _Float16* hs16 = at<_Float16>(scratch, l.hs16);
+    GemmArgs g{};
+    g.A = x16;
+    g.T = T;
+    g.W0 = w->gate_shared;
+    g.W1 = w->up_shared;
+    g.type = w->gate_shared_type;
+    g.row_bytes = row_bytes(w->gate_shared_type, d);
+    g.N = w->d_ff_shared;
+    g.K = d;
+    g.out_h = hs16;
+    const int mt = (T + 127) / 128;
+    if ((s = launch_gemm(g, true, mt, st))) return s;
+    g.A = hs16;
+    g.W0 = w->down_shared;
+    g.W1 = nullptr;
+    g.type = w->down_shared_type;
+    g.row_bytes = row_bytes(w->down_shared_type, w->d_ff_shared);
+    g.N = d;
+    g.K = w->d_ff_shared;
+    g.out_h = nullptr;
+    g.out_y = ys;
+    if ((s = launch_gemm(g, false, mt, st))) return s;
+  } else if (w->d_ff_shared > 0) {
     float* hs = at<float>(scratch, l.hs);
     ys = at<float>(scratch, l.ys);
     ProjArgs b{};

@@ -1,0 +1,340 @@
+// Grouped expert GEMM of the MoE FFN for prefill-sized batches, on CDNA4 MFMA.
+//
+// For every expert segment (the tokens routed to one expert, contiguous in the dispatch order) and
+// every output tile: gate/up:  h[p][n] = silu(x_p . Wg[n]) * (x_p . Wu[n])   (x rows gathered via perm)
+//                    down:     y[p][n] = h_p . Wd[n]
+// with W rows in their ggml encoding. The reference computes the same products as FP64 dots over
+// weights dequantized to F32 at load (utils.cpp:735-747, weight_management.cpp:802-877).
+//
+// Numerics: weights are decoded to fp16 while they are staged into LDS (Q8_0: d*q with one rounding;
+// Q4_K: (d*sc)*q - dmin*m by one fused multiply-add of the fp16-rounded factors; BF16: RNE to fp16),
+// activations are fp16, products accumulate in fp32 on v_mfma_f32_32x32x16_f16. The relative error
+// of a layer is ~4e-4 (rel-L2), inside the 2e-3 bar for quantized stacks. F32 stacks never take this
+// path (their bar is 1e-5).
+//
+// Tiling: 256 threads = 4 waves in a 2x2 arrangement, BM = 128 tokens, K tiles of 64. gate/up:
+// BN = 128 columns of h (256 rows of W: 128 gate + 128 up), each wave 64x64 of both; down: BN = 256,
+// each wave 64x128. Tiles (expert, first token) come from a table the dispatch step writes, so
+// grid.x over-provisions m-tiles and extra blocks exit at once; grid.y covers N. Global loads of the
+// next K tile are issued before the MFMAs of the current one.
+#include "moe_internal.hpp"
+
+namespace ember_moe {
+using namespace ember_math;
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef u32x4 u32x4_a4 __attribute__((aligned(4)));
+
+constexpr int GBM = 128, GBK = 64, LDK = GBK + 8;  // LDS rows padded by 16 bytes
+
+__device__ inline half2_t h2(uint32_t v) { return __builtin_bit_cast(half2_t, v); }
+__device__ inline uint32_t u32(half2_t v) { return __builtin_bit_cast(uint32_t, v); }
+
+// (1024 + byte) as fp16 for bytes 0,1 (hi = 0) or 2,3 (hi = 1) of w: exact integers 1024..1279.
+__device__ inline half2_t magic_pair(uint32_t w, int hi) {
+  return h2(__builtin_amdgcn_perm(0x64646464u, w, hi ? 0x04030402u : 0x04010400u));
+}
+
+// Decodes the 64-element chunk `c` of a weight row into 32 dwords of fp16 pairs.
+template <int FMT>
+struct Deq;
+
+template <>
+struct Deq<EMBER_TYPE_Q8_0> {
+  static constexpr int NW = 17;
+  __device__ static void load(const uint8_t* row, int c, uint32_t* raw) {
+    const uint8_t* p = row + (size_t)c * 68;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const u32x4 q = *reinterpret_cast<const u32x4_a4*>(p + 16 * v);
+      raw[4 * v] = q.x; raw[4 * v + 1] = q.y; raw[4 * v + 2] = q.z; raw[4 * v + 3] = q.w;
+    }
+    raw[16] = *reinterpret_cast<const uint32_t*>(p + 64);
+  }
+  __device__ static void decode(const uint32_t* raw, int, uint32_t* out) {
+    const half2_t dA = h2((raw[0] & 0xffffu) * 0x10001u), dB = h2((raw[8] >> 16) * 0x10001u);
+    const half2_t off = h2(0xe480e480u);  // -1152 = -(1024 + 128) in each half
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const half2_t qa = magic_pair(raw[(1 + j) >> 1] ^ 0x80808080u, (1 + j) & 1) + off;
+      const half2_t qb = magic_pair(raw[9 + (j >> 1)] ^ 0x80808080u, j & 1) + off;
+      out[j] = u32(qa * dA);
+      out[16 + j] = u32(qb * dB);
+    }
+  }
+};
+
+template <>
+struct Deq<EMBER_TYPE_Q4_K> {
+  static constexpr int NW = 12;
+  __device__ static void load(const uint8_t* row, int c, uint32_t* raw) {
+    const uint8_t* sb = row + (size_t)(c >> 2) * 144;
+    const u32x4 h = *reinterpret_cast<const u32x4*>(sb);
+    const u32x4 q0 = *reinterpret_cast<const u32x4*>(sb + 16 + 32 * (c & 3));
+    const u32x4 q1 = *reinterpret_cast<const u32x4*>(sb + 32 + 32 * (c & 3));
+    raw[0] = h.x; raw[1] = h.y; raw[2] = h.z; raw[3] = h.w;
+    raw[4] = q0.x; raw[5] = q0.y; raw[6] = q0.z; raw[7] = q0.w;
+    raw[8] = q1.x; raw[9] = q1.y; raw[10] = q1.z; raw[11] = q1.w;
+  }
+  __device__ static int ubyte(const uint32_t* raw, int b) { return (int)((raw[b >> 2] >> (8 * (b & 3))) & 0xff); }
+  __device__ static void scale_min(const uint32_t* raw, int j, int* sc, int* mn) {  // quantization.cpp:145-155
+    if (j < 4) {
+      *sc = ubyte(raw, 4 + j) & 63;
+      *mn = ubyte(raw, 8 + j) & 63;
+    } else {
+      *sc = (ubyte(raw, 8 + j) & 0xf) | ((ubyte(raw, j) >> 6) << 4);
+      *mn = (ubyte(raw, 8 + j) >> 4) | ((ubyte(raw, 4 + j) >> 6) << 4);
+    }
+  }
+  __device__ static void decode(const uint32_t* raw, int c, uint32_t* out) {
+    const float d = half_bits_to_float(raw[0] & 0xffff), dmin = half_bits_to_float(raw[0] >> 16);
+    int scA, mA, scB, mB;
+    scale_min(raw, 2 * (c & 3), &scA, &mA);
+    scale_min(raw, 2 * (c & 3) + 1, &scB, &mB);
+    const _Float16 fdA = (_Float16)(d * (float)scA), fmA = (_Float16)(-(dmin * (float)mA));
+    const _Float16 fdB = (_Float16)(d * (float)scB), fmB = (_Float16)(-(dmin * (float)mB));
+    const half2_t dA = {fdA, fdA}, mA2 = {fmA, fmA}, dB = {fdB, fdB}, mB2 = {fmB, fmB};
+    const half2_t off = h2(0xe400e400u);  // -1024
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t w = raw[4 + k];
+      const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+      out[2 * k] = u32(__builtin_elementwise_fma(magic_pair(lo, 0) + off, dA, mA2));
+      out[2 * k + 1] = u32(__builtin_elementwise_fma(magic_pair(lo, 1) + off, dA, mA2));
+      out[16 + 2 * k] = u32(__builtin_elementwise_fma(magic_pair(hi, 0) + off, dB, mB2));
+      out[16 + 2 * k + 1] = u32(__builtin_elementwise_fma(magic_pair(hi, 1) + off, dB, mB2));
+    }
+  }
+};
+
+template <int FMT>
+struct DeqHalf {
+  static constexpr int NW = 32;
+  __device__ static void load(const uint8_t* row, int c, uint32_t* raw) {
+    const u32x4* p = reinterpret_cast<const u32x4*>(row + (size_t)c * 128);
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      const u32x4 q = p[v];
+      raw[4 * v] = q.x; raw[4 * v + 1] = q.y; raw[4 * v + 2] = q.z; raw[4 * v + 3] = q.w;
+    }
+  }
+  __device__ static void decode(const uint32_t* raw, int, uint32_t* out) {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      if (FMT == EMBER_TYPE_F16) {
+        out[i] = raw[i];
+      } else {
+        const half2_t v = {(_Float16)as_f32(raw[i] << 16), (_Float16)as_f32(raw[i] & 0xffff0000u)};
+        out[i] = u32(v);
+      }
+    }
+  }
+};
+template <>
+struct Deq<EMBER_TYPE_F16> : DeqHalf<EMBER_TYPE_F16> {};
+template <>
+struct Deq<EMBER_TYPE_BF16> : DeqHalf<EMBER_TYPE_BF16> {};
+
+__device__ inline float swiglu_g(float g, float u) { return g * (1.0f / (1.0f + expf_glibc(-g))) * u; }
+
+template <int FMT, bool GATED>
+__global__ void __launch_bounds__(256) gemm_kernel(GemmArgs g) {
+  using D = Deq<FMT>;
+  constexpr int BN = GATED ? 128 : 256;  // output columns per block
+  constexpr int WN = GATED ? 2 : 4;      // 32-column subtiles per wave (per matrix)
+  constexpr int G = GATED ? 2 : 1;
+  __shared__ __align__(16) _Float16 As[GBM][LDK];
+  __shared__ __align__(16) _Float16 Bs[256][LDK];
+
+  // ---- the tile: expert segment, first token, rows
+  int e = 0, p0 = 0, rows = 0;
+  if (g.tiles) {
+    if ((int)blockIdx.x >= *g.n_tiles) return;
+    e = g.tiles[2 * blockIdx.x];
+    const int m0 = g.tiles[2 * blockIdx.x + 1];
+    p0 = g.offsets[e] + m0;
+    rows = min(GBM, g.offsets[e + 1] - p0);
+  } else {
+    p0 = blockIdx.x * GBM;
+    if (p0 >= g.T) return;
+    rows = min(GBM, g.T - p0);
+  }
+  const int n0 = blockIdx.y * BN;
+  const int K = g.K, N = g.N;
+  const int nk = K / GBK;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // ---- global load assignments
+  // A: thread -> token row tid/2, 32-element half (tid & 1) of the K tile
+  const int a_r = tid >> 1, a_h = tid & 1;
+  const _Float16* a_src = nullptr;
+  if (a_r < rows) {
+    const int p = p0 + a_r;
+    const int src_row = g.perm ? g.perm[p] / g.k : p;
+    a_src = g.A + (size_t)src_row * K + a_h * 32;
+  }
+  // B: thread -> weight row tid (gated: tid < 128 gate rows, else up rows)
+  const int b_g = GATED ? (tid >> 7) : 0;
+  const int b_n = n0 + (GATED ? (tid & 127) : tid);
+  const uint8_t* b_row = nullptr;
+  if (b_n < N) {
+    const uint8_t* base = static_cast<const uint8_t*>(b_g ? g.W1 : g.W0) + (int64_t)e * g.expert_stride;
+    b_row = base + (int64_t)b_n * g.row_bytes;
+  }
+
+  u32x4 a_reg[4];
+  uint32_t b_raw[D::NW];
+  auto fetch = [&](int kt) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      a_reg[v] = a_src ? *reinterpret_cast<const u32x4*>(a_src + (size_t)kt * GBK + 8 * v) : u32x4{0, 0, 0, 0};
+    if (b_row) {
+      D::load(b_row, kt, b_raw);
+    } else {
+#pragma unroll
+      for (int w = 0; w < D::NW; ++w) b_raw[w] = 0u;
+    }
+  };
+
+  floatx16 acc[G][2][WN];
+#pragma unroll
+  for (int q = 0; q < G; ++q)
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < WN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[q][i][j][r] = 0.0f;
+
+  fetch(0);
+  for (int kt = 0; kt < nk; ++kt) {
+    __syncthreads();  // the previous tile's MFMAs are done with LDS
+#pragma unroll
+    for (int v = 0; v < 4; ++v) *reinterpret_cast<u32x4*>(&As[a_r][a_h * 32 + 8 * v]) = a_reg[v];
+    {
+      uint32_t dq[32];
+      if (b_row) {
+        D::decode(b_raw, kt, dq);
+      } else {
+#pragma unroll
+        for (int w = 0; w < 32; ++w) dq[w] = 0u;
+      }
+#pragma unroll
+      for (int v = 0; v < 8; ++v)
+        *reinterpret_cast<u32x4*>(&Bs[tid][8 * v]) = u32x4{dq[4 * v], dq[4 * v + 1], dq[4 * v + 2], dq[4 * v + 3]};
+    }
+    __syncthreads();
+    if (kt + 1 < nk) fetch(kt + 1);
+#pragma unroll
+    for (int ks = 0; ks < GBK / 16; ++ks) {
+      const int kk = ks * 16 + 8 * (lane >> 5);
+      half8 af[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) af[i] = *reinterpret_cast<const half8*>(&As[wm * 64 + 32 * i + (lane & 31)][kk]);
+#pragma unroll
+      for (int q = 0; q < G; ++q)
+#pragma unroll
+        for (int j = 0; j < WN; ++j) {
+          const int brow = (GATED ? q * 128 : 0) + wn * (WN * 32) + 32 * j + (lane & 31);
+          const half8 bf = *reinterpret_cast<const half8*>(&Bs[brow][kk]);
+#pragma unroll
+          for (int i = 0; i < 2; ++i) acc[q][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf, acc[q][i][j], 0, 0, 0);
+        }
+    }
+  }
+
+  // ---- epilogue: lane holds column (lane & 31) of each 32x32 subtile, rows 8*ii + 4*(lane>>5) + jj
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < WN; ++j) {
+      const int n = n0 + wn * (WN * 32) + 32 * j + (lane & 31);
+      if (n >= N) continue;
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int m = wm * 64 + 32 * i + 8 * ii + 4 * (lane >> 5) + jj;
+          if (m >= rows) continue;
+          const size_t o = (size_t)(p0 + m) * N + n;
+          if constexpr (GATED) {
+            g.out_h[o] = (_Float16)swiglu_g(acc[0][i][j][4 * ii + jj], acc[1][i][j][4 * ii + jj]);
+          } else {
+            g.out_y[o] = acc[0][i][j][4 * ii + jj];
+          }
+        }
+    }
+}
+
+bool gemm_supported(int type, int K) {
+  return (type == EMBER_TYPE_Q8_0 || type == EMBER_TYPE_Q4_K || type == EMBER_TYPE_BF16 || type == EMBER_TYPE_F16) &&
+         K % GBK == 0;
+}
+
+int gemm_max_tiles(int T, int k, int E) { return (T * k + GBM - 1) / GBM + std::min(E, T * k); }
+
+template <bool GATED>
+int launch_gemm_t(const GemmArgs& g, int max_mtiles, hipStream_t st) {
+  constexpr int BN = GATED ? 128 : 256;
+  dim3 grid(max_mtiles, (g.N + BN - 1) / BN);
+  if (grid.x == 0 || grid.y == 0) return EMBER_OK;
+  switch (g.type) {
+    case EMBER_TYPE_Q8_0: gemm_kernel<EMBER_TYPE_Q8_0, GATED><<<grid, 256, 0, st>>>(g); break;
+    case EMBER_TYPE_Q4_K: gemm_kernel<EMBER_TYPE_Q4_K, GATED><<<grid, 256, 0, st>>>(g); break;
+    case EMBER_TYPE_BF16: gemm_kernel<EMBER_TYPE_BF16, GATED><<<grid, 256, 0, st>>>(g); break;
+    case EMBER_TYPE_F16: gemm_kernel<EMBER_TYPE_F16, GATED><<<grid, 256, 0, st>>>(g); break;
+    default: return EMBER_ERR_TYPE;
+  }
+  return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
+}
+
+int launch_gemm(const GemmArgs& g, bool gated, int max_mtiles, hipStream_t st) {
+  return gated ? launch_gemm_t<true>(g, max_mtiles, st) : launch_gemm_t<false>(g, max_mtiles, st);
+}
+
+// x (f32) -> fp16, RNE, elementwise.
+__global__ void __launch_bounds__(256) to_f16_kernel(const float* __restrict__ x, int64_t n, _Float16* __restrict__ y) {
+  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (i + 3 < n) {
+    const float4 v = *reinterpret_cast<const float4*>(x + i);
+    const half2_t a = {(_Float16)v.x, (_Float16)v.y}, b = {(_Float16)v.z, (_Float16)v.w};
+    *reinterpret_cast<uint2*>(y + i) = make_uint2(u32(a), u32(b));
+  } else {
+    for (int64_t j = i; j < n; ++j) y[j] = (_Float16)x[j];
+  }
+}
+
+int launch_to_f16(const float* x, int64_t n, _Float16* y, hipStream_t st) {
+  if (n <= 0) return EMBER_OK;
+  const int64_t threads = (n + 3) / 4;
+  to_f16_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, st>>>(x, n, y);
+  return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
+}
+
+// Tile table for the grouped GEMM: (expert, first token) of every 128-token tile of every expert
+// segment with tokens, ascending by expert. One thread; E entries of offsets.
+__global__ void build_tiles_kernel(const int32_t* __restrict__ offsets, int E, int32_t* __restrict__ tiles,
+                                   int32_t* __restrict__ n_tiles) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  int n = 0;
+  for (int e = 0; e < E; ++e) {
+    const int cnt = offsets[e + 1] - offsets[e];
+    for (int m0 = 0; m0 < cnt; m0 += GBM) {
+      tiles[2 * n] = e;
+      tiles[2 * n + 1] = m0;
+      ++n;
+    }
+  }
+  *n_tiles = n;
+}
+
+int launch_build_tiles(const int32_t* offsets, int E, int32_t* tiles, int32_t* n_tiles, hipStream_t st) {
+  build_tiles_kernel<<<1, 64, 0, st>>>(offsets, E, tiles, n_tiles);
+  return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
+}
+
+}  // namespace ember_moe

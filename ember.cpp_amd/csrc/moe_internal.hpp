@@ -84,6 +84,30 @@ struct ProjArgs {
 
 int launch_projection(const ProjArgs& a, hipStream_t st);
 
+// Grouped MFMA GEMM (prefill). Tiles come from `tiles` (pairs expert, first token; *n_tiles valid)
+// over expert segments of the dispatch order, or, when tiles is null, cover T rows of one matrix.
+struct GemmArgs {
+  const _Float16* A;       // activation rows, fp16 [*][K]
+  const int32_t* perm;     // non-null: row of sorted position p is perm[p] / k
+  int k, T;
+  const void* W0;          // gate (or the only) stack
+  const void* W1;          // up stack (gated) or null
+  int64_t expert_stride;   // bytes between experts' matrices
+  int64_t row_bytes;       // bytes of one weight row of K elements
+  int type;
+  int N, K;
+  const int32_t* tiles;
+  const int32_t* n_tiles;
+  const int32_t* offsets;
+  _Float16* out_h;         // gated: silu(gate) * up as fp16 [pos][N]
+  float* out_y;            // plain: f32 [pos][N]
+};
+bool gemm_supported(int type, int K);
+int gemm_max_tiles(int T, int k, int E);
+int launch_gemm(const GemmArgs& g, bool gated, int max_mtiles, hipStream_t st);
+int launch_to_f16(const float* x, int64_t n, _Float16* y, hipStream_t st);
+int launch_build_tiles(const int32_t* offsets, int E, int32_t* tiles, int32_t* n_tiles, hipStream_t st);
+
 int launch_combine(const float* y, const float* gates, const int32_t* pos, const float* y_shared, float scale, int T,
                    int k, int d, float* out, hipStream_t st);
 

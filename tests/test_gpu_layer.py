@@ -69,6 +69,18 @@ def test_deepseek_shared_bias_scale(gpu, T):
                        seed=7), T)
 
 
+@pytest.mark.parametrize("wtype,T", [(em.Q8_0, 64), (em.Q8_0, 300), (em.Q4_K, 200), (em.BF16, 130), (em.F16, 96)])
+def test_grouped_gemm_path(gpu, wtype, T):
+    """T >= 32 runs the MFMA grouped GEMM; skewed routing (E 32, top-8) leaves ragged expert tiles."""
+    check(em.LayerSpec(d=512, d_ff=768, E=32, k=8, wtype=wtype, seed=11), T)
+
+
+@pytest.mark.parametrize("T", [64, 257])
+def test_grouped_gemm_shared_bias(gpu, T):
+    check(em.LayerSpec(d=256, d_ff=192, E=16, k=6, wtype=em.BF16, bias_std=2.0, d_ff_shared=384, out_scale=2.5,
+                       seed=7), T)
+
+
 @pytest.mark.parametrize("T", [1, 6])
 def test_sigmoid_groups(gpu, T):
     check(em.LayerSpec(d=128, d_ff=256, E=32, k=4, wtype=em.Q8_0, scoring=em.SCORE_SIGMOID, bias_std=0.5, groups_n=8,
