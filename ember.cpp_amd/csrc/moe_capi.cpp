@@ -326,7 +326,7 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     g.N = w->d_ff_shared;
     g.K = d;
     g.out_h = hs16;
-    const int mt = (T + 127) / 128;
+    const int mt = gemm_max_tiles(T, 1, 0);  // one dense segment of T rows
     if ((s = launch_gemm(g, true, mt, st))) return s;
     g.A = hs16;
     g.W0 = w->down_shared;

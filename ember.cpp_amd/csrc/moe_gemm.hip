@@ -28,7 +28,7 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef u32x4 u32x4_a4 __attribute__((aligned(4)));
 
-constexpr int GBM = 128, GBK = 64, LDK = GBK + 8;  // LDS rows padded by 16 bytes
+constexpr int GBM = 256, GBK = 64, LDK = GBK + 8;  // LDS rows padded by 16 bytes
 
 __device__ inline half2_t h2(uint32_t v) { return __builtin_bit_cast(half2_t, v); }
 __device__ inline uint32_t u32(half2_t v) { return __builtin_bit_cast(uint32_t, v); }
@@ -38,10 +38,12 @@ __device__ inline half2_t magic_pair(uint32_t w, int hi) {
   return h2(__builtin_amdgcn_perm(0x64646464u, w, hi ? 0x04030402u : 0x04010400u));
 }
 
-// Decodes the 64-element chunk `c` of a weight row into 32 dwords of fp16 pairs.
+// Row-chunk decoders: the 64 elements [64*kt, +64) of a weight row into 32 dwords of fp16 pairs.
 template <int FMT>
 struct Deq;
 
+// Q8_0: two 34-byte blocks, 68 bytes from a 4-byte boundary (rows are whole 64-element chunks).
+// Dword 0 = {d_A, q0, q1}; 1..7 = q2..q29; 8 = {q30, q31, d_B}; 9..16 = block B's q0..q31.
 template <>
 struct Deq<EMBER_TYPE_Q8_0> {
   static constexpr int NW = 17;
@@ -67,15 +69,17 @@ struct Deq<EMBER_TYPE_Q8_0> {
   }
 };
 
+// Q4_K: quarter kt%4 of super-block kt/4: the 16-byte header and the quarter's 32 nibble bytes
+// (low nibbles: group 2q, high nibbles: group 2q+1).
 template <>
 struct Deq<EMBER_TYPE_Q4_K> {
   static constexpr int NW = 12;
   __device__ static void load(const uint8_t* row, int c, uint32_t* raw) {
     const uint8_t* sb = row + (size_t)(c >> 2) * 144;
-    const u32x4 h = *reinterpret_cast<const u32x4*>(sb);
+    const u32x4 hd = *reinterpret_cast<const u32x4*>(sb);
     const u32x4 q0 = *reinterpret_cast<const u32x4*>(sb + 16 + 32 * (c & 3));
     const u32x4 q1 = *reinterpret_cast<const u32x4*>(sb + 32 + 32 * (c & 3));
-    raw[0] = h.x; raw[1] = h.y; raw[2] = h.z; raw[3] = h.w;
+    raw[0] = hd.x; raw[1] = hd.y; raw[2] = hd.z; raw[3] = hd.w;
     raw[4] = q0.x; raw[5] = q0.y; raw[6] = q0.z; raw[7] = q0.w;
     raw[8] = q1.x; raw[9] = q1.y; raw[10] = q1.z; raw[11] = q1.w;
   }
@@ -138,59 +142,70 @@ struct Deq<EMBER_TYPE_F16> : DeqHalf<EMBER_TYPE_F16> {};
 template <>
 struct Deq<EMBER_TYPE_BF16> : DeqHalf<EMBER_TYPE_BF16> {};
 
-__device__ inline float swiglu_g(float g, float u) { return g * (1.0f / (1.0f + expf_glibc(-g))) * u; }
+// The GEMM path carries ~4e-4 relative error from fp16 operands, so SwiGLU uses the hardware exp here.
+__device__ inline float swiglu_g(float g, float u) { return g * __frcp_rn(1.0f + __expf(-g)) * u; }
+
+// Blocks are laid out XCD-aware: the hardware hands block b to XCD b % 8, and block b works on
+// m-tile (b % 8) + 8 * ((b / 8) / NT) and n-tile (b / 8) % NT, so the blocks resident on one XCD at a
+// time share one m-tile of activations (read into that XCD's L2 once) while consecutive m-tiles of an
+// expert run on neighbouring XCDs at the same time (their weight tiles meet in the shared MALL).
+//
+// 256 threads = 4 waves in a 2 (M) x 2 (N) arrangement, each wave a 128 x 128 tile of MFMA
+// accumulators (in AGPRs); every thread loads one activation row and decodes one weight row per K tile.
+// Per K tile: issue the global loads of tile k+1, run the MFMAs of tile k from one LDS stage, then
+// store / decode tile k+1 into the other stage, barrier.
+constexpr int kGemmThreads = 256;
+constexpr int kStageHalves = (GBM + 256) * LDK;
+constexpr size_t kGemmLds = 2 * kStageHalves * sizeof(_Float16);
 
 template <int FMT, bool GATED>
-__global__ void __launch_bounds__(256) gemm_kernel(GemmArgs g) {
+__global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs g, int NT) {
   using D = Deq<FMT>;
   constexpr int BN = GATED ? 128 : 256;  // output columns per block
   constexpr int WN = GATED ? 2 : 4;      // 32-column subtiles per wave (per matrix)
+  constexpr int WM = 4;                  // 32-row subtiles per wave
   constexpr int G = GATED ? 2 : 1;
-  __shared__ __align__(16) _Float16 As[GBM][LDK];
-  __shared__ __align__(16) _Float16 Bs[256][LDK];
+  extern __shared__ __align__(16) _Float16 smem[];
 
-  // ---- the tile: expert segment, first token, rows
+  // ---- the tile
+  const int xcd = blockIdx.x % 8, j = blockIdx.x / 8;
+  const int mt = xcd + 8 * (j / NT), nt = j % NT;
   int e = 0, p0 = 0, rows = 0;
   if (g.tiles) {
-    if ((int)blockIdx.x >= *g.n_tiles) return;
-    e = g.tiles[2 * blockIdx.x];
-    const int m0 = g.tiles[2 * blockIdx.x + 1];
+    if (mt >= *g.n_tiles) return;
+    e = g.tiles[2 * mt];
+    const int m0 = g.tiles[2 * mt + 1];
     p0 = g.offsets[e] + m0;
     rows = min(GBM, g.offsets[e + 1] - p0);
   } else {
-    p0 = blockIdx.x * GBM;
+    p0 = mt * GBM;
     if (p0 >= g.T) return;
     rows = min(GBM, g.T - p0);
   }
-  const int n0 = blockIdx.y * BN;
+  const int n0 = nt * BN;
   const int K = g.K, N = g.N;
   const int nk = K / GBK;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
-  // ---- global load assignments
-  // A: thread -> token row tid/2, 32-element half (tid & 1) of the K tile
-  const int a_r = tid >> 1, a_h = tid & 1;
   const _Float16* a_src = nullptr;
-  if (a_r < rows) {
-    const int p = p0 + a_r;
-    const int src_row = g.perm ? g.perm[p] / g.k : p;
-    a_src = g.A + (size_t)src_row * K + a_h * 32;
+  if (tid < rows) {
+    const int p = p0 + tid;
+    a_src = g.A + (size_t)(g.perm ? g.perm[p] / g.k : p) * K;
   }
-  // B: thread -> weight row tid (gated: tid < 128 gate rows, else up rows)
-  const int b_g = GATED ? (tid >> 7) : 0;
-  const int b_n = n0 + (GATED ? (tid & 127) : tid);
   const uint8_t* b_row = nullptr;
-  if (b_n < N) {
-    const uint8_t* base = static_cast<const uint8_t*>(b_g ? g.W1 : g.W0) + (int64_t)e * g.expert_stride;
-    b_row = base + (int64_t)b_n * g.row_bytes;
+  {
+    const int b_g = GATED ? (tid >> 7) : 0;
+    const int b_n = n0 + (GATED ? (tid & 127) : tid);
+    if (b_n < N)
+      b_row = static_cast<const uint8_t*>(b_g ? g.W1 : g.W0) + (int64_t)e * g.expert_stride + (int64_t)b_n * g.row_bytes;
   }
 
-  u32x4 a_reg[4];
+  u32x4 a_reg[8];
   uint32_t b_raw[D::NW];
   auto fetch = [&](int kt) {
 #pragma unroll
-    for (int v = 0; v < 4; ++v)
+    for (int v = 0; v < 8; ++v)
       a_reg[v] = a_src ? *reinterpret_cast<const u32x4*>(a_src + (size_t)kt * GBK + 8 * v) : u32x4{0, 0, 0, 0};
     if (b_row) {
       D::load(b_row, kt, b_raw);
@@ -199,72 +214,78 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs g) {
       for (int w = 0; w < D::NW; ++w) b_raw[w] = 0u;
     }
   };
+  auto stage_in = [&](int kt, int stage) {
+    _Float16* As = smem + stage * kStageHalves;
+    _Float16* Bs = As + GBM * LDK;
+#pragma unroll
+    for (int v = 0; v < 8; ++v) *reinterpret_cast<u32x4*>(&As[tid * LDK + 8 * v]) = a_reg[v];
+    uint32_t dq[32];
+    D::decode(b_raw, kt, dq);
+#pragma unroll
+    for (int v = 0; v < 8; ++v)
+      *reinterpret_cast<u32x4*>(&Bs[tid * LDK + 8 * v]) = u32x4{dq[4 * v], dq[4 * v + 1], dq[4 * v + 2], dq[4 * v + 3]};
+  };
 
-  floatx16 acc[G][2][WN];
+  floatx16 acc[G][WM][WN];
 #pragma unroll
   for (int q = 0; q < G; ++q)
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < WM; ++i)
 #pragma unroll
-      for (int j = 0; j < WN; ++j)
+      for (int jn = 0; jn < WN; ++jn)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[q][i][j][r] = 0.0f;
+        for (int r = 0; r < 16; ++r) acc[q][i][jn][r] = 0.0f;
 
-  fetch(0);
-  for (int kt = 0; kt < nk; ++kt) {
-    __syncthreads();  // the previous tile's MFMAs are done with LDS
-#pragma unroll
-    for (int v = 0; v < 4; ++v) *reinterpret_cast<u32x4*>(&As[a_r][a_h * 32 + 8 * v]) = a_reg[v];
-    {
-      uint32_t dq[32];
-      if (b_row) {
-        D::decode(b_raw, kt, dq);
-      } else {
-#pragma unroll
-        for (int w = 0; w < 32; ++w) dq[w] = 0u;
-      }
-#pragma unroll
-      for (int v = 0; v < 8; ++v)
-        *reinterpret_cast<u32x4*>(&Bs[tid][8 * v]) = u32x4{dq[4 * v], dq[4 * v + 1], dq[4 * v + 2], dq[4 * v + 3]};
-    }
-    __syncthreads();
-    if (kt + 1 < nk) fetch(kt + 1);
+  auto mfma_stage = [&](int stage) {
+    const _Float16* As = smem + stage * kStageHalves;
+    const _Float16* Bs = As + GBM * LDK;
 #pragma unroll
     for (int ks = 0; ks < GBK / 16; ++ks) {
       const int kk = ks * 16 + 8 * (lane >> 5);
-      half8 af[2];
+      half8 af[WM];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) af[i] = *reinterpret_cast<const half8*>(&As[wm * 64 + 32 * i + (lane & 31)][kk]);
+      for (int i = 0; i < WM; ++i) af[i] = *reinterpret_cast<const half8*>(&As[(wm * 128 + 32 * i + (lane & 31)) * LDK + kk]);
 #pragma unroll
       for (int q = 0; q < G; ++q)
 #pragma unroll
-        for (int j = 0; j < WN; ++j) {
-          const int brow = (GATED ? q * 128 : 0) + wn * (WN * 32) + 32 * j + (lane & 31);
-          const half8 bf = *reinterpret_cast<const half8*>(&Bs[brow][kk]);
+        for (int jn = 0; jn < WN; ++jn) {
+          const int brow = (GATED ? q * 128 : 0) + wn * (WN * 32) + 32 * jn + (lane & 31);
+          const half8 bf = *reinterpret_cast<const half8*>(&Bs[brow * LDK + kk]);
 #pragma unroll
-          for (int i = 0; i < 2; ++i) acc[q][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf, acc[q][i][j], 0, 0, 0);
+          for (int i = 0; i < WM; ++i)
+            acc[q][i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf, acc[q][i][jn], 0, 0, 0);
         }
     }
+  };
+
+  fetch(0);
+  stage_in(0, 0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    if (kt + 1 < nk) fetch(kt + 1);  // in flight during the MFMAs below
+    mfma_stage(kt & 1);
+    if (kt + 1 < nk) stage_in(kt + 1, (kt + 1) & 1);
+    __syncthreads();
   }
 
   // ---- epilogue: lane holds column (lane & 31) of each 32x32 subtile, rows 8*ii + 4*(lane>>5) + jj
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < WM; ++i)
 #pragma unroll
-    for (int j = 0; j < WN; ++j) {
-      const int n = n0 + wn * (WN * 32) + 32 * j + (lane & 31);
+    for (int jn = 0; jn < WN; ++jn) {
+      const int n = n0 + wn * (WN * 32) + 32 * jn + (lane & 31);
       if (n >= N) continue;
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii)
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-          const int m = wm * 64 + 32 * i + 8 * ii + 4 * (lane >> 5) + jj;
+          const int m = wm * 128 + 32 * i + 8 * ii + 4 * (lane >> 5) + jj;
           if (m >= rows) continue;
           const size_t o = (size_t)(p0 + m) * N + n;
           if constexpr (GATED) {
-            g.out_h[o] = (_Float16)swiglu_g(acc[0][i][j][4 * ii + jj], acc[1][i][j][4 * ii + jj]);
+            g.out_h[o] = (_Float16)swiglu_g(acc[0][i][jn][4 * ii + jj], acc[1][i][jn][4 * ii + jj]);
           } else {
-            g.out_y[o] = acc[0][i][j][4 * ii + jj];
+            g.out_y[o] = acc[0][i][jn][4 * ii + jj];
           }
         }
     }
@@ -277,19 +298,30 @@ bool gemm_supported(int type, int K) {
 
 int gemm_max_tiles(int T, int k, int E) { return (T * k + GBM - 1) / GBM + std::min(E, T * k); }
 
+template <int FMT, bool GATED>
+int launch_gemm_fmt(const GemmArgs& g, int max_mtiles, hipStream_t st) {
+  constexpr int BN = GATED ? 128 : 256;
+  static const bool lds_ok =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<FMT, GATED>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemmLds) == hipSuccess;
+  if (!lds_ok) return EMBER_ERR_LAUNCH;
+  const int NT = (g.N + BN - 1) / BN;
+  const int mgroups = (max_mtiles + 7) / 8;
+  const unsigned blocks = (unsigned)(8 * mgroups * NT);
+  if (max_mtiles == 0 || NT == 0) return EMBER_OK;
+  gemm_kernel<FMT, GATED><<<blocks, kGemmThreads, kGemmLds, st>>>(g, NT);
+  return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
+}
+
 template <bool GATED>
 int launch_gemm_t(const GemmArgs& g, int max_mtiles, hipStream_t st) {
-  constexpr int BN = GATED ? 128 : 256;
-  dim3 grid(max_mtiles, (g.N + BN - 1) / BN);
-  if (grid.x == 0 || grid.y == 0) return EMBER_OK;
   switch (g.type) {
-    case EMBER_TYPE_Q8_0: gemm_kernel<EMBER_TYPE_Q8_0, GATED><<<grid, 256, 0, st>>>(g); break;
-    case EMBER_TYPE_Q4_K: gemm_kernel<EMBER_TYPE_Q4_K, GATED><<<grid, 256, 0, st>>>(g); break;
-    case EMBER_TYPE_BF16: gemm_kernel<EMBER_TYPE_BF16, GATED><<<grid, 256, 0, st>>>(g); break;
-    case EMBER_TYPE_F16: gemm_kernel<EMBER_TYPE_F16, GATED><<<grid, 256, 0, st>>>(g); break;
+    case EMBER_TYPE_Q8_0: return launch_gemm_fmt<EMBER_TYPE_Q8_0, GATED>(g, max_mtiles, st);
+    case EMBER_TYPE_Q4_K: return launch_gemm_fmt<EMBER_TYPE_Q4_K, GATED>(g, max_mtiles, st);
+    case EMBER_TYPE_BF16: return launch_gemm_fmt<EMBER_TYPE_BF16, GATED>(g, max_mtiles, st);
+    case EMBER_TYPE_F16: return launch_gemm_fmt<EMBER_TYPE_F16, GATED>(g, max_mtiles, st);
     default: return EMBER_ERR_TYPE;
   }
-  return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
 }
 
 int launch_gemm(const GemmArgs& g, bool gated, int max_mtiles, hipStream_t st) {

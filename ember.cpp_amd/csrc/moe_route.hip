@@ -91,6 +91,79 @@ __global__ void __launch_bounds__(256) router_logits_lds(const float* __restrict
   }
 }
 
+// Router logits, many tokens: a block of TT tokens x TE experts (TT * TE = 256 threads, one per
+// pair) walks K in tiles of 512 staged in LDS; each thread keeps the pair's eight FP64 chains as
+// independent accumulators (8-way ILP), element 8q + c going to chain c in increasing q, exactly the
+// reference's order.
+constexpr int RP_KT = 256;
+template <int TT, int TE>
+__global__ void __launch_bounds__(256) router_logits_pt(const float* __restrict__ x, const float* __restrict__ R,
+                                                        float* __restrict__ logits, int T, int d, int E) {
+  extern __shared__ __align__(16) float rp_lds[];
+  constexpr int LD = RP_KT + 4;
+  constexpr int ROWS = TT + TE;
+  constexpr int Q4 = RP_KT / 4;                    // float4 granules per row of a full tile
+  constexpr int PER = (ROWS * Q4 + 255) / 256;     // granules per thread per tile
+  const int t0 = blockIdx.x * TT, e0 = blockIdx.y * TE;
+  const int tl = threadIdx.x / TE, el = threadIdx.x % TE;
+  const int n8 = d - d % 8;
+  const int ntiles = (n8 + RP_KT - 1) / RP_KT;
+  float4 pre[PER];
+  // all of a tile's loads are issued before any is used; the next tile's are in flight while this
+  // tile's chains run
+  auto fetch = [&](int kt) {
+    const int k0 = kt * RP_KT, kn = min(RP_KT, n8 - k0);
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const int i = threadIdx.x + u * 256;
+      const int row = i / Q4, col = i % Q4;
+      pre[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (row < ROWS && 4 * col < kn) {
+        if (row < TT) {
+          if (t0 + row < T) pre[u] = *reinterpret_cast<const float4*>(x + (size_t)(t0 + row) * d + k0 + 4 * col);
+        } else if (e0 + row - TT < E) {
+          pre[u] = *reinterpret_cast<const float4*>(R + (size_t)(e0 + row - TT) * d + k0 + 4 * col);
+        }
+      }
+    }
+  };
+  double a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (ntiles > 0) fetch(0);
+  for (int kt = 0; kt < ntiles; ++kt) {
+    const int kn = min(RP_KT, n8 - kt * RP_KT);
+    float* buf = rp_lds + (kt & 1) * ROWS * LD;
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const int i = threadIdx.x + u * 256;
+      if (i < ROWS * Q4) *reinterpret_cast<float4*>(buf + (i / Q4) * LD + 4 * (i % Q4)) = pre[u];
+    }
+    __syncthreads();
+    if (kt + 1 < ntiles) fetch(kt + 1);
+    const float* xr = buf + tl * LD;
+    const float* rr = buf + (TT + el) * LD;
+    for (int i = 0; i < kn; i += 8) {
+      const float4 x0 = *reinterpret_cast<const float4*>(xr + i), x1 = *reinterpret_cast<const float4*>(xr + i + 4);
+      const float4 r0 = *reinterpret_cast<const float4*>(rr + i), r1 = *reinterpret_cast<const float4*>(rr + i + 4);
+      a[0] = a[0] + (double)r0.x * (double)x0.x;
+      a[1] = a[1] + (double)r0.y * (double)x0.y;
+      a[2] = a[2] + (double)r0.z * (double)x0.z;
+      a[3] = a[3] + (double)r0.w * (double)x0.w;
+      a[4] = a[4] + (double)r1.x * (double)x1.x;
+      a[5] = a[5] + (double)r1.y * (double)x1.y;
+      a[6] = a[6] + (double)r1.z * (double)x1.z;
+      a[7] = a[7] + (double)r1.w * (double)x1.w;
+    }
+    // two LDS buffers alternate, so one barrier per tile keeps a buffer from being overwritten
+    // while another wave still reads it
+  }
+  const int t = t0 + tl, e = e0 + el;
+  if (t >= T || e >= E) return;
+  double tail = 0.0;
+  for (int i = n8; i < d; ++i) tail = tail + (double)R[(size_t)e * d + i] * (double)x[(size_t)t * d + i];
+  const double v = (((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]))) + tail;
+  logits[(size_t)t * E + e] = (float)v;
+}
+
 // Router logits, large T: a 32-token x 16-expert tile per 256-thread block. Thread (chain c, group g)
 // keeps 4 tokens x 4 experts of chain c; x and R stream through LDS in 64-element K tiles, and each
 // chain visits its elements in increasing index order, so the sums are the reference's exactly.
@@ -528,6 +601,21 @@ int launch_router_logits(const float* x, int T, int d, int E, const float* R, fl
     const int EG = router_lds_rows(d);
     dim3 grid((E + EG - 1) / EG, T);
     router_logits_lds<<<grid, 256, (size_t)(EG + 1) * (d + 8) * sizeof(float), st>>>(x, R, logits, T, d, E);
+  } else if (d % 4 == 0) {
+    static const bool lds_ok =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&router_logits_pt<32, 8>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, 2 * 40 * (RP_KT + 4) * (int)sizeof(float)) ==
+        hipSuccess;
+    if (!lds_ok) return EMBER_ERR_LAUNCH;
+    if (E <= 8) {
+      dim3 grid((T + 31) / 32, (E + 7) / 8);
+      router_logits_pt<32, 8><<<grid, 256, (size_t)2 * (32 + 8) * (RP_KT + 4) * sizeof(float), st>>>(x, R, logits, T,
+                                                                                                   d, E);
+    } else {
+      dim3 grid((T + 15) / 16, (E + 15) / 16);
+      router_logits_pt<16, 16><<<grid, 256, (size_t)2 * (16 + 16) * (RP_KT + 4) * sizeof(float), st>>>(x, R, logits,
+                                                                                                     T, d, E);
+    }
   } else if (T >= 32 && E >= 8) {
     dim3 grid((T + RL_TT - 1) / RL_TT, (E + RL_TE - 1) / RL_TE);
     router_logits_tiled<<<grid, 256, 0, st>>>(x, R, logits, T, d, E);

@@ -19,7 +19,7 @@ def _dev(a):
     return torch.from_numpy(np.ascontiguousarray(a)).cuda()
 
 
-@pytest.mark.parametrize("T,d,E", [(1, 4096, 8), (8, 4096, 8), (3, 100, 8), (64, 2048, 128), (257, 2048, 64),
+@pytest.mark.parametrize("T,d,E", [(1, 4096, 8), (8, 4096, 8), (3, 100, 8), (64, 2048, 128), (257, 2048, 64), (2048, 4096, 8),
                                    (40, 256, 8), (31, 20, 5)])
 def test_router_logits_bit_exact(gpu, T, d, E):
     import torch
