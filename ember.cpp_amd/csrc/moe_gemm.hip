@@ -56,6 +56,28 @@ struct Deq<EMBER_TYPE_Q8_0> {
     }
     raw[16] = *reinterpret_cast<const uint32_t*>(p + 64);
   }
+  // half row: block 2*kt + h, 34 bytes; odd blocks start 2 bytes past a dword boundary, so nine dwords
+  // are loaded from the boundary below (they never leave the row) and funnel-shifted
+  static constexpr int NWH = 9;
+  __device__ static void load_half(const uint8_t* row, int kt, int h, uint32_t* raw) {
+    const int blk = 2 * kt + h;
+    const uint32_t* p = reinterpret_cast<const uint32_t*>(row + (size_t)(blk * 34 & ~3));
+    const u32x4 q0 = *reinterpret_cast<const u32x4_a4*>(p), q1 = *reinterpret_cast<const u32x4_a4*>(p + 4);
+    raw[0] = q0.x; raw[1] = q0.y; raw[2] = q0.z; raw[3] = q0.w;
+    raw[4] = q1.x; raw[5] = q1.y; raw[6] = q1.z; raw[7] = q1.w;
+    raw[8] = p[8];
+  }
+  __device__ static void decode_half(const uint32_t* raw, int, int h, uint32_t* out) {
+    const uint32_t sh = h ? 16u : 0u;
+    uint32_t w[9];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w[i] = __builtin_amdgcn_alignbit(raw[i + 1], raw[i], sh);
+    w[8] = raw[8] >> sh;
+    const half2_t dd = h2((w[0] & 0xffffu) * 0x10001u);
+    const half2_t off = h2(0xe480e480u);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) out[j] = u32((magic_pair(w[(1 + j) >> 1] ^ 0x80808080u, (1 + j) & 1) + off) * dd);
+  }
   __device__ static void decode(const uint32_t* raw, int, uint32_t* out) {
     const half2_t dA = h2((raw[0] & 0xffffu) * 0x10001u), dB = h2((raw[8] >> 16) * 0x10001u);
     const half2_t off = h2(0xe480e480u);  // -1152 = -(1024 + 128) in each half
@@ -93,6 +115,24 @@ struct Deq<EMBER_TYPE_Q4_K> {
       *mn = (ubyte(raw, 8 + j) >> 4) | ((ubyte(raw, 4 + j) >> 6) << 4);
     }
   }
+  // half row: group 2*(kt%4) + h of super-block kt/4 (low nibbles for h = 0, high for h = 1)
+  static constexpr int NWH = 12;
+  __device__ static void load_half(const uint8_t* row, int kt, int, uint32_t* raw) { load(row, kt, raw); }
+  __device__ static void decode_half(const uint32_t* raw, int kt, int h, uint32_t* out) {
+    const float d = half_bits_to_float(raw[0] & 0xffff), dmin = half_bits_to_float(raw[0] >> 16);
+    int sc, mn;
+    scale_min(raw, 2 * (kt & 3) + h, &sc, &mn);
+    const _Float16 fd = (_Float16)(d * (float)sc), fm = (_Float16)(-(dmin * (float)mn));
+    const half2_t dd = {fd, fd}, mm = {fm, fm};
+    const half2_t off = h2(0xe400e400u);
+    const uint32_t sh = h ? 4u : 0u;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t nib = (raw[4 + k] >> sh) & 0x0f0f0f0fu;
+      out[2 * k] = u32(__builtin_elementwise_fma(magic_pair(nib, 0) + off, dd, mm));
+      out[2 * k + 1] = u32(__builtin_elementwise_fma(magic_pair(nib, 1) + off, dd, mm));
+    }
+  }
   __device__ static void decode(const uint32_t* raw, int c, uint32_t* out) {
     const float d = half_bits_to_float(raw[0] & 0xffff), dmin = half_bits_to_float(raw[0] >> 16);
     int scA, mA, scB, mB;
@@ -116,7 +156,26 @@ struct Deq<EMBER_TYPE_Q4_K> {
 
 template <int FMT>
 struct DeqHalf {
-  static constexpr int NW = 32;
+  static constexpr int NW = 32, NWH = 16;
+  __device__ static void load_half(const uint8_t* row, int kt, int h, uint32_t* raw) {
+    const u32x4* p = reinterpret_cast<const u32x4*>(row + (size_t)kt * 128 + 64 * h);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const u32x4 q = p[v];
+      raw[4 * v] = q.x; raw[4 * v + 1] = q.y; raw[4 * v + 2] = q.z; raw[4 * v + 3] = q.w;
+    }
+  }
+  __device__ static void decode_half(const uint32_t* raw, int, int, uint32_t* out) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (FMT == EMBER_TYPE_F16) {
+        out[i] = raw[i];
+      } else {
+        const half2_t v = {(_Float16)as_f32(raw[i] << 16), (_Float16)as_f32(raw[i] & 0xffff0000u)};
+        out[i] = u32(v);
+      }
+    }
+  }
   __device__ static void load(const uint8_t* row, int c, uint32_t* raw) {
     const u32x4* p = reinterpret_cast<const u32x4*>(row + (size_t)c * 128);
 #pragma unroll
@@ -150,11 +209,12 @@ __device__ inline float swiglu_g(float g, float u) { return g * __frcp_rn(1.0f +
 // time share one m-tile of activations (read into that XCD's L2 once) while consecutive m-tiles of an
 // expert run on neighbouring XCDs at the same time (their weight tiles meet in the shared MALL).
 //
-// 256 threads = 4 waves in a 2 (M) x 2 (N) arrangement, each wave a 128 x 128 tile of MFMA
-// accumulators (in AGPRs); every thread loads one activation row and decodes one weight row per K tile.
-// Per K tile: issue the global loads of tile k+1, run the MFMAs of tile k from one LDS stage, then
-// store / decode tile k+1 into the other stage, barrier.
-constexpr int kGemmThreads = 256;
+// 512 threads = 8 waves in a 4 (M) x 2 (N) arrangement (two waves per SIMD, so one wave's waits and
+// decode overlap the other's MFMAs), each wave a 64 x 128 tile of accumulators; every thread loads
+// half of one activation row and decodes half of one weight row per K tile. Per K tile: issue the
+// global loads of tile k+1, run the MFMAs of tile k from one LDS stage, store / decode tile k+1 into
+// the other stage, barrier.
+constexpr int kGemmThreads = 512;
 constexpr int kStageHalves = (GBM + 256) * LDK;
 constexpr size_t kGemmLds = 2 * kStageHalves * sizeof(_Float16);
 
@@ -163,7 +223,7 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs g, int NT) 
   using D = Deq<FMT>;
   constexpr int BN = GATED ? 128 : 256;  // output columns per block
   constexpr int WN = GATED ? 2 : 4;      // 32-column subtiles per wave (per matrix)
-  constexpr int WM = 4;                  // 32-row subtiles per wave
+  constexpr int WM = 2;                  // 32-row subtiles per wave
   constexpr int G = GATED ? 2 : 1;
   extern __shared__ __align__(16) _Float16 smem[];
 
@@ -187,43 +247,49 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs g, int NT) 
   const int nk = K / GBK;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
+  const int lr = tid >> 1, lh = tid & 1;  // this thread's row (of A and of W) and half of the K tile
 
   const _Float16* a_src = nullptr;
-  if (tid < rows) {
-    const int p = p0 + tid;
-    a_src = g.A + (size_t)(g.perm ? g.perm[p] / g.k : p) * K;
+  if (lr < rows) {
+    const int p = p0 + lr;
+    a_src = g.A + (size_t)(g.perm ? g.perm[p] / g.k : p) * K + 32 * lh;
   }
   const uint8_t* b_row = nullptr;
   {
-    const int b_g = GATED ? (tid >> 7) : 0;
-    const int b_n = n0 + (GATED ? (tid & 127) : tid);
+    const int b_g = GATED ? (lr >> 7) : 0;
+    const int b_n = n0 + (GATED ? (lr & 127) : lr);
     if (b_n < N)
       b_row = static_cast<const uint8_t*>(b_g ? g.W1 : g.W0) + (int64_t)e * g.expert_stride + (int64_t)b_n * g.row_bytes;
   }
 
-  u32x4 a_reg[8];
-  uint32_t b_raw[D::NW];
+  u32x4 a_reg[4];
+  uint32_t b_raw[D::NWH];
   auto fetch = [&](int kt) {
 #pragma unroll
-    for (int v = 0; v < 8; ++v)
+    for (int v = 0; v < 4; ++v)
       a_reg[v] = a_src ? *reinterpret_cast<const u32x4*>(a_src + (size_t)kt * GBK + 8 * v) : u32x4{0, 0, 0, 0};
     if (b_row) {
-      D::load(b_row, kt, b_raw);
+      D::load_half(b_row, kt, lh, b_raw);
     } else {
 #pragma unroll
-      for (int w = 0; w < D::NW; ++w) b_raw[w] = 0u;
+      for (int w = 0; w < D::NWH; ++w) b_raw[w] = 0u;
     }
   };
   auto stage_in = [&](int kt, int stage) {
     _Float16* As = smem + stage * kStageHalves;
     _Float16* Bs = As + GBM * LDK;
 #pragma unroll
-    for (int v = 0; v < 8; ++v) *reinterpret_cast<u32x4*>(&As[tid * LDK + 8 * v]) = a_reg[v];
-    uint32_t dq[32];
-    D::decode(b_raw, kt, dq);
+    for (int v = 0; v < 4; ++v) *reinterpret_cast<u32x4*>(&As[lr * LDK + 32 * lh + 8 * v]) = a_reg[v];
+    uint32_t dq[16];
+    if (b_row) {
+      D::decode_half(b_raw, kt, lh, dq);
+    } else {
 #pragma unroll
-    for (int v = 0; v < 8; ++v)
-      *reinterpret_cast<u32x4*>(&Bs[tid * LDK + 8 * v]) = u32x4{dq[4 * v], dq[4 * v + 1], dq[4 * v + 2], dq[4 * v + 3]};
+      for (int w = 0; w < 16; ++w) dq[w] = 0u;
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      *reinterpret_cast<u32x4*>(&Bs[lr * LDK + 32 * lh + 8 * v]) = u32x4{dq[4 * v], dq[4 * v + 1], dq[4 * v + 2], dq[4 * v + 3]};
   };
 
   floatx16 acc[G][WM][WN];
@@ -244,7 +310,7 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs g, int NT) 
       const int kk = ks * 16 + 8 * (lane >> 5);
       half8 af[WM];
 #pragma unroll
-      for (int i = 0; i < WM; ++i) af[i] = *reinterpret_cast<const half8*>(&As[(wm * 128 + 32 * i + (lane & 31)) * LDK + kk]);
+      for (int i = 0; i < WM; ++i) af[i] = *reinterpret_cast<const half8*>(&As[(wm * 64 + 32 * i + (lane & 31)) * LDK + kk]);
 #pragma unroll
       for (int q = 0; q < G; ++q)
 #pragma unroll
@@ -279,7 +345,7 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs g, int NT) 
       for (int ii = 0; ii < 4; ++ii)
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-          const int m = wm * 128 + 32 * i + 8 * ii + 4 * (lane >> 5) + jj;
+          const int m = wm * 64 + 32 * i + 8 * ii + 4 * (lane >> 5) + jj;
           if (m >= rows) continue;
           const size_t o = (size_t)(p0 + m) * N + n;
           if constexpr (GATED) {
