@@ -33,6 +33,8 @@ int check_matrix(const void* p, int type, int K) {
   const int64_t rb = row_bytes(type, K);
   if (rb == -2) return EMBER_ERR_TYPE;
   if (rb < 0) return EMBER_ERR_SHAPE;
+  // the decode kernel stages one activation row of K elements per token in 64 KiB of LDS
+  if ((type_quantizes_activations(type) ? (int64_t)K * 2 + K / 32 * 8 : (int64_t)K * 4) > 65536) return EMBER_ERR_SHAPE;
   if (reinterpret_cast<uintptr_t>(p) % 16) return EMBER_ERR_ALIGN;
   return EMBER_OK;
 }
