@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdlib>
+#include <string>
 
 #include "moe_internal.hpp"
 
@@ -13,7 +15,22 @@ namespace {
 
 constexpr int kMaxE = 512;  // route_kernel keeps one bit per (lane, 64-expert stripe) and LDS rows of E
 constexpr int kMaxK = 64;   // picks live in a 64-entry LDS array per wave
-constexpr int kGemmMinT = 32;  // from this many tokens the expert products run on the MFMA grouped GEMM
+// Expert-product kernels by tokens per expert (M): the int16-dot GEMV while M is at most a few tokens,
+// the skinny MFMA GEMM (64-token tiles) for up to ~100, the 256-token-tile MFMA GEMM beyond.
+enum PathMode { kGemv = 0, kSkinny = 1, kGemm = 2 };
+int path_mode(int type_in, int K_in, int type_out, int K_out, double avg_m) {
+  if (!gemm_supported(type_in, K_in) || !gemm_supported(type_out, K_out)) return kGemv;
+  static const int forced = [] {
+    const char* v = std::getenv("EMBER_MOE_PATH");  // tuning override: gemv | skinny | gemm
+    if (!v) return -1;
+    const std::string s(v);
+    return s == "gemv" ? kGemv : s == "skinny" ? kSkinny : s == "gemm" ? kGemm : -1;
+  }();
+  if (forced >= 0) return forced;
+  if (avg_m <= 2.0) return kGemv;
+  if (avg_m <= 96.0) return kSkinny;
+  return kGemm;
+}
 
 size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
 
@@ -95,8 +112,8 @@ struct ActLayout {
 };
 struct Layout {
   size_t logits, idx, gates, offsets, perm, h, y, hs, ys;
-  size_t x16, h16, hs16, tiles, n_tiles;  // MFMA path
-  bool gemm, gemm_shared;
+  size_t x16, h16, hs16, tiles, n_tiles;  // MFMA paths
+  int mode, mode_shared;                  // PathMode of the routed experts and of the shared expert
   ActLayout xq, hq, hsq;  // int16 activations of x, h and the shared expert's h (quantized formats)
   RouteLayout r;
   size_t end;
@@ -127,13 +144,17 @@ Layout layout(const ember_moe_layer* w, int T) {
   o = act_layout(o, T, w->d, qx, &l.xq);
   o = act_layout(o, slots, w->d_ff, type_quantizes_activations(w->down_type), &l.hq);
   o = act_layout(o, T, w->d_ff_shared, w->d_ff_shared > 0 && type_quantizes_activations(w->down_shared_type), &l.hsq);
-  l.gemm = T >= kGemmMinT && gemm_supported(w->gate_type, w->d) && gemm_supported(w->down_type, w->d_ff);
-  l.gemm_shared = w->d_ff_shared > 0 && T >= kGemmMinT && gemm_supported(w->gate_shared_type, w->d) &&
-                  gemm_supported(w->down_shared_type, w->d_ff_shared);
-  const size_t tiles = l.gemm ? (size_t)gemm_max_tiles(T, w->k, w->E) : 0;
-  l.x16 = o; o = align_up(o + (l.gemm || l.gemm_shared ? (size_t)T * w->d * 2 : 0));
-  l.h16 = o; o = align_up(o + (l.gemm ? slots * w->d_ff * 2 : 0));
-  l.hs16 = o; o = align_up(o + (l.gemm_shared ? (size_t)T * w->d_ff_shared * 2 : 0));
+  l.mode = path_mode(w->gate_type, w->d, w->down_type, w->d_ff, (double)T * w->k / w->E);
+  l.mode_shared = w->d_ff_shared > 0
+                      ? path_mode(w->gate_shared_type, w->d, w->down_shared_type, w->d_ff_shared, (double)T)
+                      : kGemv;
+  const size_t tiles = l.mode == kGemm     ? (size_t)gemm_max_tiles(T, w->k, w->E)
+                       : l.mode == kSkinny ? (size_t)gemm_skinny_max_tiles(T, w->k, w->E)
+                                           : 0;
+  const bool mfma = l.mode != kGemv, mfma_sh = w->d_ff_shared > 0 && l.mode_shared != kGemv;
+  l.x16 = o; o = align_up(o + (mfma || mfma_sh ? (size_t)T * w->d * 2 : 0));
+  l.h16 = o; o = align_up(o + (mfma ? slots * w->d_ff * 2 : 0));
+  l.hs16 = o; o = align_up(o + (mfma_sh ? (size_t)T * w->d_ff_shared * 2 : 0));
   l.tiles = o; o = align_up(o + tiles * 8);
   l.n_tiles = o; o = align_up(o + 4);
   l.end = o;
@@ -226,18 +247,23 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
   mark(ev, 3, st);
 
   const ActQ xq = act_at(scratch, l.xq, d);
-  const bool gemv_x = (!l.gemm && type_quantizes_activations(w->gate_type)) ||
-                      (w->d_ff_shared > 0 && !l.gemm_shared && type_quantizes_activations(w->gate_shared_type));
+  const bool shared_mfma = w->d_ff_shared > 0 && l.mode_shared != kGemv;
+  const bool gemv_x = (l.mode == kGemv && type_quantizes_activations(w->gate_type)) ||
+                      (w->d_ff_shared > 0 && !shared_mfma && type_quantizes_activations(w->gate_shared_type));
   if (gemv_x)
     if ((s = launch_quantize_act(x, T, d, xq, st))) return s;
   _Float16* x16 = at<_Float16>(scratch, l.x16);
-  if (l.gemm || l.gemm_shared)
+  if (l.mode != kGemv || shared_mfma)
     if ((s = launch_to_f16(x, (int64_t)T * d, x16, st))) return s;
 
-  if (l.gemm) {
+  if (l.mode != kGemv) {
+    const bool skinny = l.mode == kSkinny;
+    auto gemm = [&](const GemmArgs& g, bool gated, int mt) {
+      return skinny ? launch_gemm_skinny(g, gated, mt, st) : launch_gemm(g, gated, mt, st);
+    };
     int32_t* tiles = at<int32_t>(scratch, l.tiles);
     int32_t* n_tiles = at<int32_t>(scratch, l.n_tiles);
-    if ((s = launch_build_tiles(offsets, E, tiles, n_tiles, st))) return s;
+    if ((s = launch_build_tiles(offsets, E, skinny, tiles, n_tiles, st))) return s;
     _Float16* h16 = at<_Float16>(scratch, l.h16);
     GemmArgs g{};
     g.A = x16;
@@ -255,8 +281,8 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     g.n_tiles = n_tiles;
     g.offsets = offsets;
     g.out_h = h16;
-    const int mt = gemm_max_tiles(T, k, E);
-    if ((s = launch_gemm(g, true, mt, st))) return s;
+    const int mt = skinny ? gemm_skinny_max_tiles(T, k, E) : gemm_max_tiles(T, k, E);
+    if ((s = gemm(g, true, mt))) return s;
     mark(ev, 4, st);
     g.A = h16;
     g.perm = nullptr;
@@ -269,7 +295,7 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     g.K = d_ff;
     g.out_h = nullptr;
     g.out_y = y;
-    if ((s = launch_gemm(g, false, mt, st))) return s;
+    if ((s = gemm(g, false, mt))) return s;
     mark(ev, 5, st);
   } else {
 
@@ -315,7 +341,7 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
 
   }
   float* ys = nullptr;
-  if (w->d_ff_shared > 0 && l.gemm_shared) {
+  if (shared_mfma) {
     ys = at<float>(scratch, l.ys);
     _Float16* hs16 = at<_Float16>(scratch, l.hs16);
     GemmArgs g{};
@@ -328,8 +354,9 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     g.N = w->d_ff_shared;
     g.K = d;
     g.out_h = hs16;
-    const int mt = gemm_max_tiles(T, 1, 0);  // one dense segment of T rows
-    if ((s = launch_gemm(g, true, mt, st))) return s;
+    const bool skinny = l.mode_shared == kSkinny;  // one dense segment of T rows
+    const int mt = skinny ? gemm_skinny_max_tiles(T, 1, 0) : gemm_max_tiles(T, 1, 0);
+    if ((s = skinny ? launch_gemm_skinny(g, true, mt, st) : launch_gemm(g, true, mt, st))) return s;
     g.A = hs16;
     g.W0 = w->down_shared;
     g.W1 = nullptr;
@@ -339,7 +366,7 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     g.K = w->d_ff_shared;
     g.out_h = nullptr;
     g.out_y = ys;
-    if ((s = launch_gemm(g, false, mt, st))) return s;
+    if ((s = skinny ? launch_gemm_skinny(g, false, mt, st) : launch_gemm(g, false, mt, st))) return s;
   } else if (w->d_ff_shared > 0) {
     float* hs = at<float>(scratch, l.hs);
     ys = at<float>(scratch, l.ys);

@@ -357,6 +357,148 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs g, int NT) 
     }
 }
 
+// Skinny grouped GEMM for segments of a few dozen tokens (decode batches of 8+ tokens, short prefills):
+// 64-token tiles, 256 threads. Each wave owns 32 output columns (gate/up: 32 gate + 32 up rows; down:
+// 64 rows) and decodes its own weight rows straight into MFMA B operands: lane (n = lane % 32,
+// h = lane / 32) decodes the 32 elements [32h, 32h + 32) of its row's K tile (one Q8_0 block, one
+// Q4_K group), which are exactly its four 8-element fragments of the tile's four K steps (the A
+// operand uses the same K order). Weights never touch LDS; activations are staged in LDS, two stages.
+constexpr int SBM = 64;
+
+template <int FMT, bool GATED>
+__global__ void __launch_bounds__(256) gemm_skinny_kernel(GemmArgs g, int NT) {
+  using D = Deq<FMT>;
+  constexpr int G = GATED ? 2 : 1;
+  constexpr int WN = GATED ? 1 : 2;     // 32-row subtiles per matrix per wave
+  constexpr int BN = GATED ? 128 : 256; // output columns per block
+  __shared__ __align__(16) _Float16 As[2][SBM][LDK];
+
+  const int mt = blockIdx.x % g.max_mt, nt = blockIdx.x / g.max_mt;
+  int e = 0, p0 = 0, rows = 0;
+  if (g.tiles) {
+    if (mt >= *g.n_tiles) return;
+    e = g.tiles[2 * mt];
+    const int m0 = g.tiles[2 * mt + 1];
+    p0 = g.offsets[e] + m0;
+    rows = min(SBM, g.offsets[e + 1] - p0);
+  } else {
+    p0 = mt * SBM;
+    if (p0 >= g.T) return;
+    rows = min(SBM, g.T - p0);
+  }
+  (void)NT;
+  const int K = g.K, N = g.N, nk = K / GBK;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = lane >> 5, nl = lane & 31;
+  const int ncol0 = nt * BN + wave * (GATED ? 32 : 64);  // first output column of this wave
+
+  // A loads: thread -> token row tid / 4, 16-element quarter (tid & 3) of the K tile
+  const int a_r = tid >> 2, a_q = tid & 3;
+  const _Float16* a_src = nullptr;
+  if (a_r < rows) {
+    const int p = p0 + a_r;
+    a_src = g.A + (size_t)(g.perm ? g.perm[p] / g.k : p) * K + 16 * a_q;
+  }
+  // B rows of this lane: per matrix q and subtile j, row ncol0 + 32 j + nl
+  const uint8_t* b_row[G][WN];
+#pragma unroll
+  for (int q = 0; q < G; ++q)
+#pragma unroll
+    for (int j = 0; j < WN; ++j) {
+      const int n = ncol0 + 32 * j + nl;
+      b_row[q][j] = n < N ? static_cast<const uint8_t*>(q ? g.W1 : g.W0) + (int64_t)e * g.expert_stride +
+                                (int64_t)n * g.row_bytes
+                          : nullptr;
+    }
+
+  u32x4 a_reg[2];
+  uint32_t b_raw[G][WN][D::NWH];
+  auto fetch = [&](int kt) {
+#pragma unroll
+    for (int v = 0; v < 2; ++v)
+      a_reg[v] = a_src ? *reinterpret_cast<const u32x4*>(a_src + (size_t)kt * GBK + 8 * v) : u32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int q = 0; q < G; ++q)
+#pragma unroll
+      for (int j = 0; j < WN; ++j) {
+        if (b_row[q][j]) {
+          D::load_half(b_row[q][j], kt, h, b_raw[q][j]);
+        } else {
+#pragma unroll
+          for (int w = 0; w < D::NWH; ++w) b_raw[q][j][w] = 0u;
+        }
+      }
+  };
+
+  floatx16 acc[G][2][WN];
+#pragma unroll
+  for (int q = 0; q < G; ++q)
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < WN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[q][i][j][r] = 0.0f;
+
+  fetch(0);
+#pragma unroll
+  for (int v = 0; v < 2; ++v) *reinterpret_cast<u32x4*>(&As[0][a_r][16 * a_q + 8 * v]) = a_reg[v];
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int st = kt & 1;
+    // decode this tile's weights (registers loaded in the previous iteration) before the loads of
+    // the next tile overwrite them
+    uint32_t bq[G][WN][16];
+#pragma unroll
+    for (int q = 0; q < G; ++q)
+#pragma unroll
+      for (int j = 0; j < WN; ++j) D::decode_half(b_raw[q][j], kt, h, bq[q][j]);
+    if (kt + 1 < nk) fetch(kt + 1);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      half8 af[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) af[i] = *reinterpret_cast<const half8*>(&As[st][32 * i + nl][32 * h + 8 * s]);
+#pragma unroll
+      for (int q = 0; q < G; ++q)
+#pragma unroll
+        for (int j = 0; j < WN; ++j) {
+          const half8 bf = __builtin_bit_cast(half8, u32x4{bq[q][j][4 * s], bq[q][j][4 * s + 1], bq[q][j][4 * s + 2],
+                                                          bq[q][j][4 * s + 3]});
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+            acc[q][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf, acc[q][i][j], 0, 0, 0);
+        }
+    }
+    if (kt + 1 < nk) {
+#pragma unroll
+      for (int v = 0; v < 2; ++v) *reinterpret_cast<u32x4*>(&As[st ^ 1][a_r][16 * a_q + 8 * v]) = a_reg[v];
+    }
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < WN; ++j) {
+      const int n = ncol0 + 32 * j + nl;
+      if (n >= N) continue;
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int m = 32 * i + 8 * ii + 4 * h + jj;
+          if (m >= rows) continue;
+          const size_t o = (size_t)(p0 + m) * N + n;
+          if constexpr (GATED) {
+            g.out_h[o] = (_Float16)swiglu_g(acc[0][i][j][4 * ii + jj], acc[1][i][j][4 * ii + jj]);
+          } else {
+            g.out_y[o] = acc[0][i][j][4 * ii + jj];
+          }
+        }
+    }
+}
+
 bool gemm_supported(int type, int K) {
   return (type == EMBER_TYPE_Q8_0 || type == EMBER_TYPE_Q4_K || type == EMBER_TYPE_BF16 || type == EMBER_TYPE_F16) &&
          K % GBK == 0;
@@ -394,6 +536,33 @@ int launch_gemm(const GemmArgs& g, bool gated, int max_mtiles, hipStream_t st) {
   return gated ? launch_gemm_t<true>(g, max_mtiles, st) : launch_gemm_t<false>(g, max_mtiles, st);
 }
 
+template <int FMT, bool GATED>
+int launch_skinny_fmt(GemmArgs g, int max_mtiles, hipStream_t st) {
+  constexpr int BN = GATED ? 128 : 256;
+  const int NT = (g.N + BN - 1) / BN;
+  if (max_mtiles == 0 || NT == 0) return EMBER_OK;
+  g.max_mt = max_mtiles;
+  gemm_skinny_kernel<FMT, GATED><<<(unsigned)(max_mtiles * NT), 256, 0, st>>>(g, NT);
+  return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
+}
+
+template <bool GATED>
+int launch_skinny_t(const GemmArgs& g, int max_mtiles, hipStream_t st) {
+  switch (g.type) {
+    case EMBER_TYPE_Q8_0: return launch_skinny_fmt<EMBER_TYPE_Q8_0, GATED>(g, max_mtiles, st);
+    case EMBER_TYPE_Q4_K: return launch_skinny_fmt<EMBER_TYPE_Q4_K, GATED>(g, max_mtiles, st);
+    case EMBER_TYPE_BF16: return launch_skinny_fmt<EMBER_TYPE_BF16, GATED>(g, max_mtiles, st);
+    case EMBER_TYPE_F16: return launch_skinny_fmt<EMBER_TYPE_F16, GATED>(g, max_mtiles, st);
+    default: return EMBER_ERR_TYPE;
+  }
+}
+
+int launch_gemm_skinny(const GemmArgs& g, bool gated, int max_mtiles, hipStream_t st) {
+  return gated ? launch_skinny_t<true>(g, max_mtiles, st) : launch_skinny_t<false>(g, max_mtiles, st);
+}
+
+int gemm_skinny_max_tiles(int T, int k, int E) { return (T * k + SBM - 1) / SBM + std::min(E, T * k); }
+
 // x (f32) -> fp16, RNE, elementwise.
 __global__ void __launch_bounds__(256) to_f16_kernel(const float* __restrict__ x, int64_t n, _Float16* __restrict__ y) {
   const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
@@ -413,15 +582,15 @@ int launch_to_f16(const float* x, int64_t n, _Float16* y, hipStream_t st) {
   return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
 }
 
-// Tile table for the grouped GEMM: (expert, first token) of every 128-token tile of every expert
+// Tile table for the grouped GEMMs: (expert, first token) of every bm-token tile of every expert
 // segment with tokens, ascending by expert. One thread; E entries of offsets.
-__global__ void build_tiles_kernel(const int32_t* __restrict__ offsets, int E, int32_t* __restrict__ tiles,
+__global__ void build_tiles_kernel(const int32_t* __restrict__ offsets, int E, int bm, int32_t* __restrict__ tiles,
                                    int32_t* __restrict__ n_tiles) {
   if (threadIdx.x != 0 || blockIdx.x != 0) return;
   int n = 0;
   for (int e = 0; e < E; ++e) {
     const int cnt = offsets[e + 1] - offsets[e];
-    for (int m0 = 0; m0 < cnt; m0 += GBM) {
+    for (int m0 = 0; m0 < cnt; m0 += bm) {
       tiles[2 * n] = e;
       tiles[2 * n + 1] = m0;
       ++n;
@@ -430,8 +599,8 @@ __global__ void build_tiles_kernel(const int32_t* __restrict__ offsets, int E, i
   *n_tiles = n;
 }
 
-int launch_build_tiles(const int32_t* offsets, int E, int32_t* tiles, int32_t* n_tiles, hipStream_t st) {
-  build_tiles_kernel<<<1, 64, 0, st>>>(offsets, E, tiles, n_tiles);
+int launch_build_tiles(const int32_t* offsets, int E, bool skinny, int32_t* tiles, int32_t* n_tiles, hipStream_t st) {
+  build_tiles_kernel<<<1, 64, 0, st>>>(offsets, E, skinny ? SBM : GBM, tiles, n_tiles);
   return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
 }
 

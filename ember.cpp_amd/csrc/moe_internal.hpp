@@ -101,12 +101,16 @@ struct GemmArgs {
   const int32_t* offsets;
   _Float16* out_h;         // gated: silu(gate) * up as fp16 [pos][N]
   float* out_y;            // plain: f32 [pos][N]
+  int max_mt;              // m-tile slots of the launch (set by the launcher)
 };
 bool gemm_supported(int type, int K);
 int gemm_max_tiles(int T, int k, int E);
 int launch_gemm(const GemmArgs& g, bool gated, int max_mtiles, hipStream_t st);
 int launch_to_f16(const float* x, int64_t n, _Float16* y, hipStream_t st);
-int launch_build_tiles(const int32_t* offsets, int E, int32_t* tiles, int32_t* n_tiles, hipStream_t st);
+int launch_build_tiles(const int32_t* offsets, int E, bool skinny, int32_t* tiles, int32_t* n_tiles, hipStream_t st);
+// Skinny variant for segments of a few dozen tokens (64-token tiles).
+int launch_gemm_skinny(const GemmArgs& g, bool gated, int max_mtiles, hipStream_t st);
+int gemm_skinny_max_tiles(int T, int k, int E);
 
 int launch_combine(const float* y, const float* gates, const int32_t* pos, const float* y_shared, float scale, int T,
                    int k, int d, float* out, hipStream_t st);

@@ -71,11 +71,18 @@ def test_deepseek_shared_bias_scale(gpu, T):
 
 @pytest.mark.parametrize("wtype,T", [(em.Q8_0, 64), (em.Q8_0, 300), (em.Q4_K, 200), (em.BF16, 130), (em.F16, 96)])
 def test_grouped_gemm_path(gpu, wtype, T):
-    """T >= 32 runs the MFMA grouped GEMM; skewed routing (E 32, top-8) leaves ragged expert tiles."""
+    """A few dozen tokens per expert: the skinny MFMA GEMM (64-token tiles); skewed routing (E 32,
+    top-8) leaves ragged expert tiles."""
     check(em.LayerSpec(d=512, d_ff=768, E=32, k=8, wtype=wtype, seed=11), T)
 
 
-@pytest.mark.parametrize("T", [64, 257])
+@pytest.mark.parametrize("wtype,T", [(em.Q8_0, 512), (em.Q4_K, 700), (em.BF16, 450), (em.F16, 520)])
+def test_large_tile_gemm_path(gpu, wtype, T):
+    """More than ~96 tokens per expert: the 256-token-tile MFMA GEMM (ragged last tiles)."""
+    check(em.LayerSpec(d=512, d_ff=768, E=8, k=2, wtype=wtype, seed=12), T)
+
+
+@pytest.mark.parametrize("T", [64, 257, 600])
 def test_grouped_gemm_shared_bias(gpu, T):
     check(em.LayerSpec(d=256, d_ff=192, E=16, k=6, wtype=em.BF16, bias_std=2.0, d_ff_shared=384, out_scale=2.5,
                        seed=7), T)
