@@ -1,9 +1,11 @@
-"""Benchmark of the MI355X MoE FFN on BASELINE config 2: a Mixtral-8x7B-shaped MoE layer
-(d 4096, 8 experts, top-2, SwiGLU d_ff 14336) with Q8_0 expert stacks and an F32 router, seeded
-synthetic weights N(0, 0.02) (router N(0, 1/sqrt(d))) and hidden states N(0, 1).
+"""Benchmark of the MI355X MoE FFN. Default workload: BASELINE config 2, a Mixtral-8x7B-shaped MoE
+layer (d 4096, 8 experts, top-2, SwiGLU d_ff 14336) with Q8_0 expert stacks and an F32 router, seeded
+synthetic weights N(0, 0.02) (router N(0, 1/sqrt(d))) and hidden states N(0, 1); --config c1/c3/c4
+selects the other single-layer configs.
 
 One step = one ember_moe_ffn call over one batch of T tokens resident in HBM (the headline T is
---tokens, default 1 = decode). Prints ONE JSON line. Besides the contract fields it carries:
+--tokens, default the config's first = decode). Prints ONE JSON line. Besides the contract fields it
+carries:
   roofline      the dominant kernel (gate/up + SwiGLU, HBM-bound): algorithmic bytes per launch over
                 its average duration from HIP events recorded around it on the launch stream
   cpu_baseline  the reference's CPU MoE path (oracle/_ref, compiled from the reference's own sources
@@ -11,7 +13,7 @@ One step = one ember_moe_ffn call over one batch of T tokens resident in HBM (th
                 token sample of the same layer
   sweep         the other token counts of config 2 (µs/layer, tokens/s, roofline fractions)
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--tokens 1] [--sweep 1,8,128,2048]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--config c2] [--tokens 1] [--sweep 1,8,128,2048]
 """
 import argparse
 import json
@@ -25,18 +27,34 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path[:0] = [ROOT, os.path.join(ROOT, "ember.cpp_amd")]
 
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, 8 TB/s
-MFMA_PEAK = {"bf16": 2500.0, "int8": 5000.0, "fp32": 157.3}  # dense TFLOP/s (TOP/s for int8)
-Q8_0_BPW = 34.0 / 32.0
+MFMA_PEAK_TFLOPS = 2500.0    # dense fp16 / bf16 MFMA, the prefill kernels' operand type
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def layer_spec():
+CONFIGS = {
+    # (description, spec kwargs, token counts)
+    "c1": ("config 1: toy F32 layer, d 256, E 8, top-2, d_ff 688",
+           dict(d=256, d_ff=688, E=8, k=2, wtype="f32"), [1, 64]),
+    "c2": ("config 2: Mixtral-8x7B-shaped MoE layer, d 4096, E 8, top-2, d_ff 14336, Q8_0 experts",
+           dict(d=4096, d_ff=14336, E=8, k=2, wtype="q8_0"), [1, 8, 128, 2048]),
+    "c3": ("config 3: Qwen3-30B-A3B-shaped layer, d 2048, E 128, top-8 renorm, d_ff 768, Q4_K experts",
+           dict(d=2048, d_ff=768, E=128, k=8, wtype="q4_k"), [1, 32, 4096]),
+    "c4": ("config 4: DeepSeek-style layer, d 2048, 64 routed + 2 shared experts (d_ff_shared 2816), top-6, "
+           "d_ff 1408, BF16 experts, seeded N(0,2) selection bias",
+           dict(d=2048, d_ff=1408, E=64, k=6, wtype="bf16", bias_std=2.0, d_ff_shared=2816), [1, 2048]),
+}
+BPW = {"f32": 4.0, "f16": 2.0, "bf16": 2.0, "q8_0": 34.0 / 32.0, "q4_k": 144.0 / 256.0}
+
+
+def layer_spec(name="c2"):
     import ember_moe as em
 
-    return em.LayerSpec(d=4096, d_ff=14336, E=8, k=2, wtype=em.Q8_0, seed=0)
+    kw = dict(CONFIGS[name][1])
+    kw["wtype"] = em.TYPE_IDS[kw["wtype"]]
+    return em.LayerSpec(seed=0, **kw)
 
 
 def realised_experts(em, dl, x, T):
@@ -51,17 +69,24 @@ def realised_experts(em, dl, x, T):
     offsets = torch.empty(s.E + 1, dtype=torch.int32, device="cuda")
     perm = torch.empty(T * s.k, dtype=torch.int32, device="cuda")
     scr = torch.empty(em.route_scratch_bytes(T, s.E, s.k), dtype=torch.uint8, device="cuda")
-    assert em.route(lg, T, s.E, s.k, s.renorm, s.scoring, None, 1, 1, idx, gates, offsets, perm, scr) == 0
+    bias = dl.tensors.get("bias")
+    assert em.route(lg, T, s.E, s.k, s.renorm, s.scoring, bias, s.groups_n, s.groups_top, idx, gates, offsets, perm,
+                    scr) == 0
     torch.cuda.synchronize()
     return int(np.unique(idx.cpu().numpy()).size)
 
 
 def algorithmic(spec, T, U):
-    """Algorithmic HBM bytes of the gate/up launch and of the whole layer, and the layer's flops."""
+    """Algorithmic HBM bytes of the gate/up launch and of the whole layer (U = realised experts hit,
+    shared expert included), and the layer's flops (routed rows only)."""
+    import ember_moe as em
+
     d, dff, k, E = spec.d, spec.d_ff, spec.k, spec.E
-    gu = U * 2 * d * dff * Q8_0_BPW + T * k * d * 4 + T * k * dff * 4
-    layer = U * 3 * d * dff * Q8_0_BPW + E * d * 4 + 2 * T * d * 4
-    flops = 2.0 * T * k * 3 * d * dff + 2.0 * T * E * d
+    bpw = BPW[em.TYPE_NAMES[spec.wtype]]
+    dsh = spec.d_ff_shared
+    gu = U * 2 * d * dff * bpw + T * k * d * 4 + T * k * dff * 4
+    layer = (U * 3 * d * dff + 3 * d * dsh) * bpw + E * d * 4 + 2 * T * d * 4
+    flops = 2.0 * T * (k * 3 * d * dff + 3 * d * dsh) + 2.0 * T * E * d
     return gu, layer, flops
 
 
@@ -133,7 +158,12 @@ def cpu_baseline(hl, x_host, T_headline, max_seconds=20.0):
     R = hl.router
     G, U, D = (hl.dequantized(n) for n in ("gate", "up", "down"))
     log(f"[bench] cpu baseline: dequantized F32 stacks in {time.time() - t0:.1f}s")
-    use_ref = O.ref_available()
+    plain = s.bias_std == 0 and s.d_ff_shared == 0 and s.scoring == 0 and s.groups_n <= 1 and s.out_scale == 1.0
+    use_ref = O.ref_available() and plain
+    sh = {}
+    if s.d_ff_shared:
+        sh = dict(d_ff_sh=s.d_ff_shared, Gs=hl.dequantized("gate_sh"), Us=hl.dequantized("up_sh"),
+                  Ds=hl.dequantized("down_sh"))
     out = np.empty((1, s.d), np.float32)
     done, t_start = 0, time.time()
     while done < x_host.shape[0] and (time.time() - t_start) < max_seconds:
@@ -142,13 +172,13 @@ def cpu_baseline(hl, x_host, T_headline, max_seconds=20.0):
             O.ref().ref_moe_ffn_f32(xt.ctypes.data, 1, s.d, s.d_ff, s.E, s.k, R.ctypes.data, G.ctypes.data,
                                     U.ctypes.data, D.ctypes.data, out.ctypes.data, int(s.renorm))
         else:
-            out[:] = O.moe_layer(xt, R, G, U, D, s.d_ff, s.E, s.k, renorm=s.renorm, nthreads=1)
+            out[:] = O.moe_layer(xt, R, G, U, D, s.d_ff, s.E, s.k, renorm=s.renorm, bias=hl.bias, nthreads=1, **sh)
         done += 1
     el = time.time() - t_start
     return {"value": done / el, "unit": "tokens/s", "cores": 1,
             "kind": "reference" if use_ref else "port",
-            "sample": f"{done} decode tokens (T=1 calls) of the config-2 layer on F32 stacks dequantized from the "
-                      f"same Q8_0 bytes, single thread, {el:.1f}s"}
+            "sample": f"{done} decode tokens (T=1 calls) of the same layer on F32 stacks dequantized from the "
+                      f"same encoded bytes, single thread, {el:.1f}s"}
 
 
 def main():
@@ -156,8 +186,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--tokens", type=int, default=1)
-    ap.add_argument("--sweep", type=str, default="1,8,128,2048")
+    ap.add_argument("--config", type=str, default="c2", choices=sorted(CONFIGS))
+    ap.add_argument("--tokens", type=int, default=None, help="headline token count (default: the config's first)")
+    ap.add_argument("--sweep", type=str, default=None, help="comma-separated token counts (default: the config's)")
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -170,7 +201,12 @@ def main():
     import ember_moe as em
 
     em.lib()
-    spec = layer_spec()
+    desc, _, tokens = CONFIGS[args.config]
+    if args.tokens is None:
+        args.tokens = tokens[0]
+    if args.sweep is None:
+        args.sweep = ",".join(str(t) for t in tokens)
+    spec = layer_spec(args.config)
     t0 = time.time()
     hl = em.make_host_layer(spec)
     log(f"[bench] generated + quantized the Q8_0 layer in {time.time() - t0:.1f}s")
@@ -188,6 +224,7 @@ def main():
         gu_bytes, layer_bytes, flops = algorithmic(spec, T, U)
         gu_ms = phases["gate_up"]
         results[T] = dict(T=T, experts_hit=U, us_per_layer=best_ms * 1e3, eager_us=eager_ms * 1e3,
+                          layer_mfma_frac=flops / (best_ms * 1e-3) / (MFMA_PEAK_TFLOPS * 1e12),
                           graph_us=None if graph_ms is None else graph_ms * 1e3, tokens_per_s=T / (best_ms * 1e-3),
                           layer_hbm_frac=layer_bytes / (best_ms * 1e-3) / (HBM_PEAK_GBS * 1e9),
                           gate_up_us=gu_ms * 1e3, gate_up_gbs=gu_bytes / (gu_ms * 1e-3) / 1e9,
@@ -196,9 +233,9 @@ def main():
         log(f"[bench] T={T}: {json.dumps(results[T])}")
 
     h = results[args.tokens]
-    gu_bytes, _, _ = algorithmic(spec, args.tokens, h["experts_hit"])
+    gu_bytes, _, flops = algorithmic(spec, args.tokens, h["experts_hit"])
     line = {
-        "metric": "MoE-FFN tokens/s (Mixtral-shape Q8_0 layer)",
+        "metric": "MoE-FFN tokens/s (" + args.config + ")",
         "value": h["tokens_per_s"],
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -208,13 +245,13 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q8_0 weights, f32 activations/accumulation",
-        "data": "synthetic (seeded N(0,0.02) experts quantized to Q8_0, F32 router N(0,1/sqrt(d)), x ~ N(0,1))",
-        "config": {"workload": f"config 2: Mixtral-8x7B-shaped MoE layer, d 4096, E 8, top-2, d_ff 14336, "
-                               f"Q8_0 experts, T={args.tokens}",
+        "dtype": f"{em.TYPE_NAMES[spec.wtype]} weights; decode: int16-quantized activations, int32/f32 accumulate; "
+                 f"prefill: fp16 MFMA operands, f32 accumulate; routing f32/f64 exact",
+        "data": "synthetic (seeded N(0,0.02) experts in the config's encoding, F32 router N(0,1/sqrt(d)), x ~ N(0,1))",
+        "config": {"workload": f"{desc}, T={args.tokens}",
                    "tokens": args.tokens, "d": spec.d, "d_ff": spec.d_ff, "E": spec.E, "k": spec.k,
                    "mode": "hipgraph" if h["graph_us"] is not None and h["graph_us"] <= h["eager_us"] else "eager"},
-        "roofline": {"kernel": "proj_kernel<Q8_0, gate/up + SwiGLU>", "bound": "hbm",
+        "roofline": {"kernel": f"gate/up + SwiGLU expert kernel ({em.TYPE_NAMES[spec.wtype]})", "bound": "hbm",
                      "achieved": h["gate_up_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": h["gate_up_gbs"] / HBM_PEAK_GBS, "traffic": None,
                      "bytes_per_launch": gu_bytes, "avg_launch_us": h["gate_up_us"]},
