@@ -51,7 +51,7 @@ int check_matrix(const void* p, int type, int K) {
   if (rb == -2) return EMBER_ERR_TYPE;
   if (rb < 0) return EMBER_ERR_SHAPE;
   // the decode kernel stages one activation row of K elements per token in 64 KiB of LDS
-  if ((type_quantizes_activations(type) ? (int64_t)K * 2 + K / 32 * 8 : (int64_t)K * 4) > 65536) return EMBER_ERR_SHAPE;
+  if ((type_quantizes_activations(type) ? (int64_t)K * 2 + K / 32 * 8 : ((int64_t)K + 63) / 64 * 256) > 65536) return EMBER_ERR_SHAPE;
   if (reinterpret_cast<uintptr_t>(p) % 16) return EMBER_ERR_ALIGN;
   return EMBER_OK;
 }
@@ -96,7 +96,7 @@ struct RouteLayout {
 };
 RouteLayout route_layout(int T, int E, int k, size_t base) {
   RouteLayout l;
-  const size_t slots = (size_t)T * k, nchunks = (slots + 63) / 64;
+  const size_t slots = (size_t)T * k, nchunks = (slots + 1023) / 1024;  // dispatch chunks of 1024 slots
   size_t o = base;
   l.rank = o; o = align_up(o + slots * 4);
   l.chunk_cnt = o; o = align_up(o + nchunks * E * 4);

@@ -28,6 +28,21 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef u32x4 u32x4_a4 __attribute__((aligned(4)));
 typedef short short2_t __attribute__((ext_vector_type(2)));
 
+// Staged activation rows are split into per-lane chunks of 2^NGL 16-byte granules (NGL = 3: 128 B,
+// NGL = 4: 256 B). Lane c reads granule i of chunk c while its neighbours read granule i of theirs,
+// which at a 128/256-byte stride would fall into the same LDS banks; each chunk's granules are
+// therefore stored rotated by a per-chunk amount so that 16 consecutive chunks' granule i occupy all
+// 16 bank slots of a 256-byte window.
+template <int NGL>
+__device__ inline int swz_granule(int c, int i) {
+  constexpr int NG = 1 << NGL;
+  const int rot = (c >> (4 - NGL)) & (NG - 1);
+  return (c << NGL) + ((i + rot) & (NG - 1));
+}
+template <int NGL>
+__device__ inline const uint8_t* lds_granule(const uint8_t* row, int c, int i) {
+  return row + 16 * swz_granule<NGL>(c, i);
+}
 __device__ inline int sdot2(uint32_t a, uint32_t b, int c) {
   return __builtin_amdgcn_sdot2(__builtin_bit_cast(short2_t, a), __builtin_bit_cast(short2_t, b), c, false);
 }
@@ -48,11 +63,6 @@ __device__ inline void load16(const uint8_t* p, uint32_t* raw) {
 struct XF {                 // float activations (F32 / F16 / BF16 weights)
   float v[64];
 };
-struct XQ {                 // int16 activations (Q8_0 / Q4_K weights): 64 values in 32 pairs
-  uint32_t w[32];
-  float s[2];               // per 32-block scale
-  int sum[2];               // per 32-block sum of the int16 values
-};
 
 template <int FMT>
 struct Fmt;
@@ -60,7 +70,7 @@ struct Fmt;
 // F32: chunk = 32 floats = 128 B.
 template <>
 struct Fmt<EMBER_TYPE_F32> {
-  static constexpr int CE = 32, NW = 32;
+  static constexpr int CE = 32, NW = 32, NGL = 3;  // activation chunk: 32 floats = 8 granules
   static constexpr bool QX = false;
   __host__ __device__ static int64_t row_bytes(int K) { return 4 * (int64_t)K; }
   __device__ static void load(const uint8_t* row, int c, int K, uint32_t* raw) {
@@ -91,7 +101,7 @@ struct Fmt<EMBER_TYPE_F32> {
 // BF16 / F16: chunk = 64 halves = 128 B.
 template <int FMT>
 struct FmtHalf {
-  static constexpr int CE = 64, NW = 32;
+  static constexpr int CE = 64, NW = 32, NGL = 4;  // activation chunk: 64 floats = 16 granules
   static constexpr bool QX = false;
   __host__ __device__ static int64_t row_bytes(int K) { return 2 * (int64_t)K; }
   __device__ static void load(const uint8_t* row, int c, int K, uint32_t* raw) {
@@ -135,7 +145,7 @@ struct Fmt<EMBER_TYPE_F16> : FmtHalf<EMBER_TYPE_F16> {};
 // Dword 0 = {d_A, q0, q1}; 1..7 = q2..q29; 8 = {q30, q31, d_B}; 9..16 = block B's q0..q31.
 template <>
 struct Fmt<EMBER_TYPE_Q8_0> {
-  static constexpr int CE = 64, NW = 17;
+  static constexpr int CE = 64, NW = 17, NGL = 3;  // activation chunk: 64 int16 = 8 granules
   static constexpr bool QX = true;
   __host__ __device__ static int64_t row_bytes(int K) { return (int64_t)K / 32 * 34; }
   __device__ static void load(const uint8_t* row, int c, int, uint32_t* raw) {
@@ -171,9 +181,9 @@ struct Fmt<EMBER_TYPE_Q8_0> {
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
         if (m < nvalid) {
-          const uint8_t* xr = lds + m * row_lds + (size_t)c * 128;
-          const u32x4 xa = *reinterpret_cast<const u32x4*>(xr + 4 * j4);
-          const u32x4 xb = *reinterpret_cast<const u32x4*>(xr + 64 + 4 * j4);
+          const uint8_t* xr = lds + m * row_lds;
+          const u32x4 xa = *reinterpret_cast<const u32x4*>(lds_granule<3>(xr, c, j4 >> 2));
+          const u32x4 xb = *reinterpret_cast<const u32x4*>(lds_granule<3>(xr, c, 4 + (j4 >> 2)));
           ia[m] = sdot2(ua[0], xa.x, ia[m]);
           ia[m] = sdot2(ua[1], xa.y, ia[m]);
           ia[m] = sdot2(ua[2], xa.z, ia[m]);
@@ -201,7 +211,7 @@ struct Fmt<EMBER_TYPE_Q8_0> {
 // {d, dmin, scales[12]} plus the quarter's 32 bytes of nibbles (low: group 2q, high: group 2q+1).
 template <>
 struct Fmt<EMBER_TYPE_Q4_K> {
-  static constexpr int CE = 64, NW = 12;
+  static constexpr int CE = 64, NW = 12, NGL = 3;
   static constexpr bool QX = true;
   __host__ __device__ static int64_t row_bytes(int K) { return (int64_t)K / 256 * 144; }
   __device__ static void load(const uint8_t* row, int c, int, uint32_t* raw) {
@@ -247,9 +257,9 @@ struct Fmt<EMBER_TYPE_Q4_K> {
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
         if (m < nvalid) {
-          const uint8_t* xr = lds + m * row_lds + (size_t)c * 128;
-          const u32x4 xa = *reinterpret_cast<const u32x4*>(xr + 8 * k2);
-          const u32x4 xb = *reinterpret_cast<const u32x4*>(xr + 64 + 8 * k2);
+          const uint8_t* xr = lds + m * row_lds;
+          const u32x4 xa = *reinterpret_cast<const u32x4*>(lds_granule<3>(xr, c, k2 >> 1));
+          const u32x4 xb = *reinterpret_cast<const u32x4*>(lds_granule<3>(xr, c, 4 + (k2 >> 1)));
           ia[m] = sdot2(ua[0], xa.x, ia[m]);
           ia[m] = sdot2(ua[1], xa.y, ia[m]);
           ia[m] = sdot2(ua[2], xa.z, ia[m]);
@@ -274,29 +284,54 @@ struct Fmt<EMBER_TYPE_Q4_K> {
   }
 };
 
-// Bytes of one token's activation row as staged in LDS: f32 values, or int16 values followed by the
-// per-32-block scales and sums.
-__host__ __device__ inline int act_lds_bytes(bool qx, int K) { return qx ? K * 2 + (K / 32) * 8 : K * 4; }
+// Bytes of one token's activation row as staged in LDS: f32 values (padded to whole 64-element
+// chunks, so that a partial last chunk's rotated granules stay inside the row), or int16 values
+// followed by the per-32-block scales and sums.
+__host__ __device__ inline int act_lds_bytes(bool qx, int K) { return qx ? K * 2 + (K / 32) * 8 : (K + 63) / 64 * 256; }
 
-// Block-cooperative copy of activation row `row` into LDS slot `dst` (16-byte granules).
-__device__ inline void stage_row(bool qx, const ProjArgs& a, int row, uint8_t* dst) {
+// Block-cooperative copy of the activation rows rows[0..nrows) into consecutive LDS slots of
+// row_lds bytes (16-byte granules; values rotated per chunk, then the per-block scales and sums).
+// All rows' loads are issued in one batch per thread before any store, so staging costs about one
+// memory latency instead of one per row and section.
+template <int NGL>
+__device__ inline void stage_rows(bool qx, const ProjArgs& a, const int* rows, int nrows, uint8_t* lds, int row_lds) {
+  typedef uint32_t v4 __attribute__((ext_vector_type(4)));
   const int K = a.K;
-  if (qx) {
-    copy16_to_lds(dst, a.act.q + (size_t)row * K, K / 8);
-    float* sc = reinterpret_cast<float*>(dst + K * 2);
-    int* sm = reinterpret_cast<int*>(sc + K / 32);
-    const int nb = K / 32;
-    if (nb % 4 == 0) {  // rows of scales / sums start on 16-byte boundaries
-      copy16_to_lds(sc, a.act.scale + (size_t)row * nb, nb / 4);
-      copy16_to_lds(sm, a.act.sum + (size_t)row * nb, nb / 4);
-    } else {
-      for (int i = threadIdx.x; i < nb; i += blockDim.x) {
-        sc[i] = a.act.scale[(size_t)row * nb + i];
-        sm[i] = a.act.sum[(size_t)row * nb + i];
-      }
+  const int nq = qx ? K / 8 : K / 4;  // granules of values per row
+  const int nb = K / 32;
+  const bool sg = qx && nb % 4 == 0;  // scales and sums start on 16-byte boundaries
+  const int per = nq + (sg ? nb / 2 : 0);
+  const int n = nrows * per;
+  const int stride = blockDim.x;
+  for (int base = threadIdx.x; base < n; base += 8 * stride) {
+    v4 t[8];
+    int dst[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {  // branch-free address math: every load is issued before any store
+      const int gi = min(base + u * stride, n - 1);
+      const int m = gi / per, r = gi - m * per;
+      const size_t row = (size_t)rows[m];
+      const bool val = r < nq, isc = !val && r < nq + nb / 4;
+      const int rs = val ? r : isc ? r - nq : r - nq - nb / 4;
+      const uint8_t* base_p = val ? (qx ? reinterpret_cast<const uint8_t*>(a.act.q + row * K)
+                                        : reinterpret_cast<const uint8_t*>(a.in + row * K))
+                                  : isc ? reinterpret_cast<const uint8_t*>(a.act.scale + row * nb)
+                                        : reinterpret_cast<const uint8_t*>(a.act.sum + row * nb);
+      t[u] = *reinterpret_cast<const v4*>(base_p + 16 * rs);
+      dst[u] = m * row_lds + (val ? 16 * swz_granule<NGL>(r >> NGL, r & ((1 << NGL) - 1))
+                                  : K * 2 + (isc ? 0 : nb * 4) + 16 * rs);
     }
-  } else {
-    copy16_to_lds(dst, a.in + (size_t)row * K, K / 4);
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (base + u * stride < n) *reinterpret_cast<v4*>(lds + dst[u]) = t[u];
+  }
+  if (qx && !sg) {
+    for (int i = threadIdx.x; i < nrows * nb; i += stride) {
+      const int m = i / nb, b = i - m * nb;
+      const size_t row = (size_t)rows[m];
+      reinterpret_cast<float*>(lds + m * row_lds + K * 2)[b] = a.act.scale[row * nb + b];
+      reinterpret_cast<int*>(lds + m * row_lds + K * 2 + nb * 4)[b] = a.act.sum[row * nb + b];
+    }
   }
 }
 
@@ -304,35 +339,18 @@ __device__ inline void stage_row(bool qx, const ProjArgs& a, int row, uint8_t* d
 template <int FMT>
 __device__ inline void lds_xf(const uint8_t* row, int c, int K, XF& x) {
   constexpr int CE = Fmt<FMT>::CE;
-  const float* p = reinterpret_cast<const float*>(row) + (size_t)c * CE;
+  constexpr int NGL = Fmt<FMT>::NGL;
   const int n = K - c * CE;
 #pragma unroll
   for (int v = 0; v < CE / 4; ++v) {
-    const float4 q = (4 * v < n) ? *reinterpret_cast<const float4*>(p + 4 * v) : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4 q = (4 * v < n) ? *reinterpret_cast<const float4*>(lds_granule<NGL>(row, c, v))
+                                 : make_float4(0.f, 0.f, 0.f, 0.f);
     x.v[4 * v] = q.x;
     x.v[4 * v + 1] = q.y;
     x.v[4 * v + 2] = q.z;
     x.v[4 * v + 3] = q.w;
   }
 }
-__device__ inline void lds_xq(const uint8_t* row, int c, int K, XQ& x) {
-  const uint8_t* p = row + (size_t)c * 128;
-#pragma unroll
-  for (int v = 0; v < 8; ++v) {
-    const u32x4 q = *reinterpret_cast<const u32x4*>(p + 16 * v);
-    x.w[4 * v] = q.x;
-    x.w[4 * v + 1] = q.y;
-    x.w[4 * v + 2] = q.z;
-    x.w[4 * v + 3] = q.w;
-  }
-  const float* sc = reinterpret_cast<const float*>(row + K * 2);
-  const int* sm = reinterpret_cast<const int*>(sc + K / 32);
-  x.s[0] = sc[2 * c];
-  x.s[1] = sc[2 * c + 1];
-  x.sum[0] = sm[2 * c];
-  x.sum[1] = sm[2 * c + 1];
-}
-
 // dot_tokens for the float formats: decode the chunk once per token from the staged f32 rows.
 template <int FMT, int MT>
 __device__ inline void dot_tokens_f(const uint32_t* raw, const uint8_t* lds, int row_lds, int c, int K, int nvalid,
@@ -395,15 +413,15 @@ __global__ void __launch_bounds__(256) proj_kernel(ProjArgs a, int L_log2) {
 
   extern __shared__ __align__(16) uint8_t act_lds[];
   const int row_lds = act_lds_bytes(F::QX, K);
+  __shared__ int rows[MT];
   for (int m0 = 0; m0 < M; m0 += MT) {
     __syncthreads();  // the previous token group's rows are no longer read
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      if (m0 + m < M) {
-        const int p = p0 + m0 + m;
-        stage_row(F::QX, a, a.in_by_perm ? a.perm[p] / a.k : p, act_lds + m * row_lds);
-      }
+    if (threadIdx.x < MT && m0 + (int)threadIdx.x < M) {
+      const int p = p0 + m0 + threadIdx.x;
+      rows[threadIdx.x] = a.in_by_perm ? a.perm[p] / a.k : p;
     }
+    __syncthreads();
+    stage_rows<F::NGL>(F::QX, a, rows, min(MT, M - m0), act_lds, row_lds);
     __syncthreads();
     float acc[G][RR][MT];
 #pragma unroll
@@ -413,22 +431,28 @@ __global__ void __launch_bounds__(256) proj_kernel(ProjArgs a, int L_log2) {
 #pragma unroll
         for (int m = 0; m < MT; ++m) acc[g][i][m] = 0.0f;
     const int nvalid = min(MT, M - m0);
-    for (int st = 0; st < nsteps; ++st) {
+    // weights of step st -> buf (zeros outside the row range / past the last chunk)
+    auto load_step = [&](int st, uint32_t (&buf)[G][RR][F::NW]) {
       const int grp = slot + (st / NC) * nslots;
       const int c = rl + (st % NC) * L;
-      uint32_t raw[G][RR][F::NW];
 #pragma unroll
       for (int g = 0; g < G; ++g)
 #pragma unroll
         for (int i = 0; i < RR; ++i) {
           const int r = grp * RR + i;
           if (c < C && r < a.rows) {
-            F::load((g ? W1 : W0) + (int64_t)r * rb, c, K, raw[g][i]);
+            F::load((g ? W1 : W0) + (int64_t)r * rb, c, K, buf[g][i]);
           } else {
 #pragma unroll
-            for (int w = 0; w < F::NW; ++w) raw[g][i][w] = 0u;
+            for (int w = 0; w < F::NW; ++w) buf[g][i][w] = 0u;
           }
         }
+    };
+    for (int st = 0; st < nsteps; ++st) {
+      const int grp = slot + (st / NC) * nslots;
+      const int c = rl + (st % NC) * L;
+      uint32_t raw[G][RR][F::NW];
+      load_step(st, raw);
       if (c < C) {
 #pragma unroll
         for (int g = 0; g < G; ++g)
@@ -482,7 +506,8 @@ int launch_proj_fmt(const ProjArgs& a, int MT, hipStream_t st) {
   const int ngroups = (a.rows + RR - 1) / RR;
   // enough blocks to fill the chip (~8 per CU over all segments), each slot walking a few groups
   const int segs = std::max(a.max_segments, 1);
-  int blocks = (2048 + segs - 1) / segs;
+  static const int kTarget = [] { const char* v = std::getenv("EMBER_PROJ_BLOCKS"); return v ? atoi(v) : 2048; }();
+  int blocks = (kTarget + segs - 1) / segs;
   blocks = std::min(blocks, (ngroups + slots_per_block - 1) / slots_per_block);
   blocks = std::max(blocks, 1);
   dim3 grid(blocks, a.max_segments);
@@ -586,9 +611,50 @@ __global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ 
   out[(size_t)t * d + o] = acc;
 }
 
+// The same with four consecutive outputs per thread (d % 4 == 0): 16-byte loads of y rows.
+__global__ void __launch_bounds__(256) combine4_kernel(const float* __restrict__ y, const float* __restrict__ gates,
+                                                       const int32_t* __restrict__ pos,
+                                                       const float* __restrict__ y_shared, float scale, int k, int d,
+                                                       float* __restrict__ out) {
+  const int t = blockIdx.y;
+  const int o = 4 * (blockIdx.x * blockDim.x + threadIdx.x);
+  if (o >= d) return;
+  float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+  for (int j = 0; j < k; ++j) {
+    const int p = pos[(size_t)t * k + j];
+    const float g = gates[(size_t)t * k + j];
+    if (p >= 0) {
+      const float4 v = *reinterpret_cast<const float4*>(y + (size_t)p * d + o);
+      a0 = a0 + g * v.x;
+      a1 = a1 + g * v.y;
+      a2 = a2 + g * v.z;
+      a3 = a3 + g * v.w;
+    }
+  }
+  if (scale != 1.0f) {
+    a0 = a0 * scale + 0.0f;
+    a1 = a1 * scale + 0.0f;
+    a2 = a2 * scale + 0.0f;
+    a3 = a3 * scale + 0.0f;
+  }
+  if (y_shared) {
+    const float4 v = *reinterpret_cast<const float4*>(y_shared + (size_t)t * d + o);
+    a0 = a0 + v.x;
+    a1 = a1 + v.y;
+    a2 = a2 + v.z;
+    a3 = a3 + v.w;
+  }
+  *reinterpret_cast<float4*>(out + (size_t)t * d + o) = make_float4(a0, a1, a2, a3);
+}
+
 int launch_combine(const float* y, const float* gates, const int32_t* pos, const float* y_shared, float scale, int T,
                    int k, int d, float* out, hipStream_t st) {
   if (T <= 0) return EMBER_OK;
+  if (d % 4 == 0) {
+    dim3 grid((d / 4 + 255) / 256, T);
+    combine4_kernel<<<grid, 256, 0, st>>>(y, gates, pos, y_shared, scale, k, d, out);
+    return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
+  }
   dim3 grid((d + 255) / 256, T);
   combine_kernel<<<grid, 256, 0, st>>>(y, gates, pos, y_shared, scale, k, d, out);
   return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;

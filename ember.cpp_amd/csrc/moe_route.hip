@@ -14,7 +14,7 @@
 namespace ember_moe {
 using namespace ember_math;
 
-constexpr int kRouterLdsFloats = 16384;  // 64 KiB of LDS for the small-T router
+constexpr int kRouterLdsFloats = 36864;  // 144 KiB of LDS for the row-staged router
 
 // ---------------------------------------------------------------------------------------------
 // Router logits, small T: one thread per (token, expert, chain); the 8 chains of a pair are 8
@@ -52,9 +52,8 @@ __global__ void __launch_bounds__(256) router_logits_direct(const float* __restr
 __host__ __device__ inline int router_lds_rows(int d) { return max(1, min(32, kRouterLdsFloats / (d + 8) - 1)); }
 
 __global__ void __launch_bounds__(256) router_logits_lds(const float* __restrict__ x, const float* __restrict__ R,
-                                                         float* __restrict__ logits, int T, int d, int E) {
+                                                         float* __restrict__ logits, int T, int d, int E, int EG) {
   extern __shared__ __align__(16) float rl_lds[];
-  const int EG = router_lds_rows(d);
   const int t = blockIdx.y, e0 = blockIdx.x * EG;
   const int ne = min(EG, E - e0);
   const int ld = d + 8;
@@ -95,17 +94,17 @@ __global__ void __launch_bounds__(256) router_logits_lds(const float* __restrict
 // pair) walks K in tiles of 512 staged in LDS; each thread keeps the pair's eight FP64 chains as
 // independent accumulators (8-way ILP), element 8q + c going to chain c in increasing q, exactly the
 // reference's order.
-constexpr int RP_KT = 256;
-template <int TT, int TE>
+template <int TT, int TE, int PT, int PE, int RP_KT>
 __global__ void __launch_bounds__(256) router_logits_pt(const float* __restrict__ x, const float* __restrict__ R,
                                                         float* __restrict__ logits, int T, int d, int E) {
+  static_assert((TT / PT) * (TE / PE) == 256, "one thread per PT x PE block of pairs");
   extern __shared__ __align__(16) float rp_lds[];
   constexpr int LD = RP_KT + 4;
   constexpr int ROWS = TT + TE;
   constexpr int Q4 = RP_KT / 4;                    // float4 granules per row of a full tile
   constexpr int PER = (ROWS * Q4 + 255) / 256;     // granules per thread per tile
   const int t0 = blockIdx.x * TT, e0 = blockIdx.y * TE;
-  const int tl = threadIdx.x / TE, el = threadIdx.x % TE;
+  const int tq = threadIdx.x / (TE / PE), eq = threadIdx.x % (TE / PE);
   const int n8 = d - d % 8;
   const int ntiles = (n8 + RP_KT - 1) / RP_KT;
   float4 pre[PER];
@@ -127,7 +126,13 @@ __global__ void __launch_bounds__(256) router_logits_pt(const float* __restrict_
       }
     }
   };
-  double a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  double a[PT][PE][8];
+#pragma unroll
+  for (int i = 0; i < PT; ++i)
+#pragma unroll
+    for (int j = 0; j < PE; ++j)
+#pragma unroll
+      for (int c = 0; c < 8; ++c) a[i][j][c] = 0.0;
   if (ntiles > 0) fetch(0);
   for (int kt = 0; kt < ntiles; ++kt) {
     const int kn = min(RP_KT, n8 - kt * RP_KT);
@@ -137,31 +142,44 @@ __global__ void __launch_bounds__(256) router_logits_pt(const float* __restrict_
       const int i = threadIdx.x + u * 256;
       if (i < ROWS * Q4) *reinterpret_cast<float4*>(buf + (i / Q4) * LD + 4 * (i % Q4)) = pre[u];
     }
-    __syncthreads();
+    __syncthreads();  // two buffers alternate, so one barrier per tile suffices
     if (kt + 1 < ntiles) fetch(kt + 1);
-    const float* xr = buf + tl * LD;
-    const float* rr = buf + (TT + el) * LD;
-    for (int i = 0; i < kn; i += 8) {
-      const float4 x0 = *reinterpret_cast<const float4*>(xr + i), x1 = *reinterpret_cast<const float4*>(xr + i + 4);
-      const float4 r0 = *reinterpret_cast<const float4*>(rr + i), r1 = *reinterpret_cast<const float4*>(rr + i + 4);
-      a[0] = a[0] + (double)r0.x * (double)x0.x;
-      a[1] = a[1] + (double)r0.y * (double)x0.y;
-      a[2] = a[2] + (double)r0.z * (double)x0.z;
-      a[3] = a[3] + (double)r0.w * (double)x0.w;
-      a[4] = a[4] + (double)r1.x * (double)x1.x;
-      a[5] = a[5] + (double)r1.y * (double)x1.y;
-      a[6] = a[6] + (double)r1.z * (double)x1.z;
-      a[7] = a[7] + (double)r1.w * (double)x1.w;
+    for (int k8 = 0; k8 < kn; k8 += 8) {
+      float xv[PT][8], rv[PE][8];
+#pragma unroll
+      for (int i = 0; i < PT; ++i) {
+        const float* xr = buf + (tq * PT + i) * LD + k8;
+        const float4 u0 = *reinterpret_cast<const float4*>(xr), u1 = *reinterpret_cast<const float4*>(xr + 4);
+        xv[i][0] = u0.x; xv[i][1] = u0.y; xv[i][2] = u0.z; xv[i][3] = u0.w;
+        xv[i][4] = u1.x; xv[i][5] = u1.y; xv[i][6] = u1.z; xv[i][7] = u1.w;
+      }
+#pragma unroll
+      for (int j = 0; j < PE; ++j) {
+        const float* rr = buf + (TT + eq * PE + j) * LD + k8;
+        const float4 u0 = *reinterpret_cast<const float4*>(rr), u1 = *reinterpret_cast<const float4*>(rr + 4);
+        rv[j][0] = u0.x; rv[j][1] = u0.y; rv[j][2] = u0.z; rv[j][3] = u0.w;
+        rv[j][4] = u1.x; rv[j][5] = u1.y; rv[j][6] = u1.z; rv[j][7] = u1.w;
+      }
+#pragma unroll
+      for (int i = 0; i < PT; ++i)
+#pragma unroll
+        for (int j = 0; j < PE; ++j)
+#pragma unroll
+          for (int c = 0; c < 8; ++c) a[i][j][c] = a[i][j][c] + (double)rv[j][c] * (double)xv[i][c];
     }
-    // two LDS buffers alternate, so one barrier per tile keeps a buffer from being overwritten
-    // while another wave still reads it
   }
-  const int t = t0 + tl, e = e0 + el;
-  if (t >= T || e >= E) return;
-  double tail = 0.0;
-  for (int i = n8; i < d; ++i) tail = tail + (double)R[(size_t)e * d + i] * (double)x[(size_t)t * d + i];
-  const double v = (((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]))) + tail;
-  logits[(size_t)t * E + e] = (float)v;
+#pragma unroll
+  for (int i = 0; i < PT; ++i)
+#pragma unroll
+    for (int j = 0; j < PE; ++j) {
+      const int t = t0 + tq * PT + i, e = e0 + eq * PE + j;
+      if (t >= T || e >= E) continue;
+      double tail = 0.0;
+      for (int q = n8; q < d; ++q) tail = tail + (double)R[(size_t)e * d + q] * (double)x[(size_t)t * d + q];
+      const double* c8 = a[i][j];
+      const double v = (((c8[0] + c8[1]) + (c8[2] + c8[3])) + ((c8[4] + c8[5]) + (c8[6] + c8[7]))) + tail;
+      logits[(size_t)t * E + e] = (float)v;
+    }
 }
 
 // Router logits, large T: a 32-token x 16-expert tile per 256-thread block. Thread (chain c, group g)
@@ -349,10 +367,125 @@ __host__ __device__ inline size_t route_wave_lds(int E) {
   return (bytes + 15) & ~(size_t)15;
 }
 
-// Routes one token on one wave (all 64 lanes call it). Softmax scoring without bias / groups
-// (moe_ffn_f32_cpu) runs a parallel argmax whose result equals the serial strict-> scan for NaN-free
-// rows; rows with a NaN, and the DeepSeek-style router, run the reference's serial algorithm on
-// lane 0. wl: route_wave_lds(E) bytes of LDS owned by this wave.
+// k passes of a wave-wide argmax over val[e] (LDS, NaN-free), each pass taking the largest untaken
+// value with ties to the lower index — the result of the reference's serial strict-> scans. Experts
+// with cand[e] == 0 are skipped (cand may be null); a pass that finds nothing ends the search. Lane 0
+// writes the picks in pick order; returns their number (uniform across the wave).
+__device__ int wave_topk(const float* val, const char* cand, int E, int k, int* picks) {
+  const int lane = threadIdx.x & 63;
+  uint32_t mine_taken = 0;  // bit q: expert lane + 64q taken (E <= 2048)
+  int n = 0;
+  for (int j = 0; j < k; ++j) {
+    float bv = 0.0f;
+    int bi = -1;
+    for (int e = lane, q = 0; e < E; e += 64, ++q)
+      if (!((mine_taken >> q) & 1u) && (!cand || cand[e]) && better(val[e], e, bv, bi)) {
+        bv = val[e];
+        bi = e;
+      }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const float ov = __shfl_xor(bv, off, 64);
+      const int oi = __shfl_xor(bi, off, 64);
+      if (better(ov, oi, bv, bi)) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    if (bi < 0) break;
+    if ((bi & 63) == lane) mine_taken |= 1u << (bi >> 6);
+    if (lane == 0) picks[n] = bi;
+    ++n;
+  }
+  wave_sync_lds();
+  if (lane == 0)
+    for (int a = 1; a < n; ++a)
+      for (int b = a; b > 0 && picks[b - 1] > picks[b]; --b) {
+        const int tmp = picks[b];
+        picks[b] = picks[b - 1];
+        picks[b - 1] = tmp;
+      }
+  wave_sync_lds();
+  return n;
+}
+
+// moe_ffn_routed_f32_cpu's router (utils.cpp:766-820) across the wave for NaN-free scores: every
+// per-expert float operation is the reference's; the float sums that fix rounding (the softmax
+// normaliser, the renorm denominator) stay serial in ascending expert order on lane 0; the maximum,
+// the group top-2 and the argmax passes are order-independent for NaN-free values. Returns false
+// (nothing written) when a NaN appears in the scores, so the caller falls back to the serial scan.
+__device__ bool route_routed_wave(const float* row, int E, int k, int renorm, int sigmoid, const float* bias,
+                                  int groups_n, int groups_top, float* s, float* c, char* cand, int* picks,
+                                  int32_t* idx_t, float* gate_t) {
+  const int lane = threadIdx.x & 63;
+  if (sigmoid) {
+    for (int e = lane; e < E; e += 64) s[e] = 1.0f / (1.0f + expf_glibc(-row[e]));
+  } else {
+    float mx = -__builtin_inff();
+    for (int e = lane; e < E; e += 64) mx = smax(mx, row[e]);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) mx = smax(mx, __shfl_xor(mx, off, 64));
+    for (int e = lane; e < E; e += 64) s[e] = expf_glibc(row[e] - mx);
+    wave_sync_lds();
+    float z = 0.0f;
+    if (lane == 0)
+      for (int e = 0; e < E; ++e) z = z + s[e];
+    z = __shfl(z, 0, 64);
+    for (int e = lane; e < E; e += 64) s[e] = s[e] / z;
+  }
+  bool bad = false;
+  for (int e = lane; e < E; e += 64) {
+    const float v = bias ? s[e] + bias[e] : s[e];
+    c[e] = v;
+    bad |= (v != v) || (s[e] != s[e]);
+  }
+  if (__any(bad)) return false;
+  wave_sync_lds();
+  const char* cmask = nullptr;
+  if (groups_n > 1) {
+    const int per = E / groups_n;
+    float* gsc = c + E;
+    for (int g = lane; g < groups_n; g += 64) {
+      float top1 = -__builtin_inff(), top2 = -__builtin_inff();
+      for (int e = g * per; e < (g + 1) * per; ++e) {
+        if (c[e] > top1) {
+          top2 = top1;
+          top1 = c[e];
+        } else if (c[e] > top2) {
+          top2 = c[e];
+        }
+      }
+      gsc[g] = per == 1 ? top1 : top1 + top2;
+    }
+    wave_sync_lds();
+    const int ng = wave_topk(gsc, nullptr, groups_n, groups_top, picks);
+    for (int e = lane; e < E; e += 64) cand[e] = 0;
+    wave_sync_lds();
+    for (int j = 0; j < ng; ++j)
+      for (int e = picks[j] * per + lane; e < (picks[j] + 1) * per; e += 64) cand[e] = 1;
+    wave_sync_lds();
+    cmask = cand;
+  }
+  const int n = wave_topk(c, cmask, E, k, picks);
+  float z = 0.0f;
+  for (int j = 0; j < n; ++j) z = z + s[picks[j]];
+  if (lane < k) {
+    if (lane < n) {
+      const int e = picks[lane];
+      idx_t[lane] = e;
+      gate_t[lane] = renorm ? s[e] / z : s[e];
+    } else {
+      idx_t[lane] = -1;
+      gate_t[lane] = 0.0f;
+    }
+  }
+  return true;
+}
+
+// Routes one token on one wave (all 64 lanes call it). NaN-free rows run wave-parallel scans whose
+// results equal the reference's serial scans; rows with a NaN (in the logits or in the DeepSeek-style
+// scores) run the reference's serial algorithm on lane 0. wl: route_wave_lds(E) bytes of LDS owned by
+// this wave.
 __device__ void route_token(const float* __restrict__ r, int E, int k, int renorm, int routed, int sigmoid,
                             const float* __restrict__ bias, int groups_n, int groups_top, unsigned char* wl,
                             int32_t* __restrict__ idx_t, float* __restrict__ gate_t) {
@@ -372,7 +505,11 @@ __device__ void route_token(const float* __restrict__ r, int E, int k, int renor
   }
   has_nan = __any(has_nan);
   wave_sync_lds();
+  if (routed && !has_nan && groups_n <= 64 &&
+      route_routed_wave(row, E, k, renorm, sigmoid, bias, groups_n, groups_top, s, cbuf, cand, picks, idx_t, gate_t))
+    return;
   if (routed || has_nan) {
+    wave_sync_lds();
     if (lane == 0) {
       if (routed)
         route_routed_serial(row, E, k, renorm, sigmoid, bias, groups_n, groups_top, s, cbuf, cand, taken, picks, idx_t,
@@ -382,38 +519,7 @@ __device__ void route_token(const float* __restrict__ r, int E, int k, int renor
     }
     return;
   }
-  // Parallel top-k: lane-local best over its experts e = lane + 64q, then a butterfly over the wave.
-  uint32_t mine_taken = 0;  // bit q: expert lane + 64q taken (E <= 2048)
-  const int kk = min(k, E);
-  for (int j = 0; j < kk; ++j) {
-    float bv = 0.0f;
-    int bi = -1;
-    for (int e = lane, q = 0; e < E; e += 64, ++q)
-      if (!((mine_taken >> q) & 1u) && better(row[e], e, bv, bi)) {
-        bv = row[e];
-        bi = e;
-      }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-      const float ov = __shfl_xor(bv, off, 64);
-      const int oi = __shfl_xor(bi, off, 64);
-      if (better(ov, oi, bv, bi)) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-    if ((bi & 63) == lane) mine_taken |= 1u << (bi >> 6);
-    if (lane == 0) picks[j] = bi;
-  }
-  wave_sync_lds();
-  if (lane == 0)
-    for (int a = 1; a < kk; ++a)
-      for (int b = a; b > 0 && picks[b - 1] > picks[b]; --b) {
-        const int tmp = picks[b];
-        picks[b] = picks[b - 1];
-        picks[b - 1] = tmp;
-      }
-  wave_sync_lds();
+  const int kk = wave_topk(row, nullptr, E, min(k, E), picks);
   float mx = -__builtin_inff();
   double z = 0.0;
   if (renorm) {
@@ -427,7 +533,9 @@ __device__ void route_token(const float* __restrict__ r, int E, int k, int renor
     for (int off = 32; off >= 1; off >>= 1) mx = smax(mx, __shfl_xor(mx, off, 64));
     for (int e = lane; e < E; e += 64) ex[e] = exp_glibc((double)(row[e] - mx));
     wave_sync_lds();
-    for (int e = 0; e < E; ++e) z = z + ex[e];  // ascending, as the reference sums
+    if (lane == 0)
+      for (int e = 0; e < E; ++e) z = z + ex[e];  // ascending, as the reference sums
+    z = __shfl(z, 0, 64);
   }
   if (lane < k) {
     if (lane < kk) {
@@ -454,22 +562,49 @@ __global__ void __launch_bounds__(256) route_kernel(const float* __restrict__ lo
 }
 
 // ---------------------------------------------------------------------------------------------
-// Dispatch: stable counting sort of the T*k slots by expert. Slots are cut into 64-slot chunks,
-// one wave each. (1) rank of each slot among equal experts earlier in its chunk, and per-chunk
-// per-expert counts; (2) one block scans the counts into per-expert offsets and per-chunk bases;
-// (3) each slot lands at base[chunk][e] + rank.
+// Dispatch: stable counting sort of the T*k slots by expert. Slots are cut into 1024-slot chunks, one
+// block each. (1) each slot's rank among equal experts earlier in its chunk (within a wave by
+// shuffles, across the chunk's waves by a per-expert prefix in LDS) and per-chunk per-expert counts;
+// (2) one block scans the counts into per-expert offsets, the list of experts with tokens, and each
+// chunk's base position per expert; (3) each slot lands at base[chunk][e] + rank.
+constexpr int kChunk = 1024;
 
-__global__ void __launch_bounds__(256) dispatch_count(const int32_t* __restrict__ idx, int nslots, int E,
-                                                      int32_t* __restrict__ rank, int32_t* __restrict__ chunk_cnt) {
+// Exclusive prefix sum over the threads of a block (one value per thread, blockDim.x <= 1024);
+// tmp: 16 ints of LDS. Every thread of the block must call it.
+__device__ int block_exclusive_scan(int v, int* tmp, int* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
+  int x = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(x, off, 64);
+    if (lane >= off) x += y;
+  }
+  if (lane == 63) tmp[wave] = x;
+  __syncthreads();
+  if (wave == 0) {
+    int t = lane < nw ? tmp[lane] : 0;
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) {
+      const int y = __shfl_up(t, off, 64);
+      if (lane >= off) t += y;
+    }
+    if (lane < nw) tmp[lane] = t;
+  }
+  __syncthreads();
+  const int base = wave ? tmp[wave - 1] : 0;
+  *total = tmp[nw - 1];
+  __syncthreads();
+  return base + x - v;
+}
+
+__global__ void __launch_bounds__(kChunk) dispatch_count(const int32_t* __restrict__ idx, int nslots, int E,
+                                                         int32_t* __restrict__ rank, int32_t* __restrict__ chunk_cnt) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int chunk = blockIdx.x * 4 + wave;
-  const int nchunks = (nslots + 63) / 64;
-  if (chunk >= nchunks) return;
-  int* cnt = reinterpret_cast<int*>(lds_raw) + (size_t)wave * E;
-  for (int e = lane; e < E; e += 64) cnt[e] = 0;
-  wave_sync_lds();
-  const int s = chunk * 64 + lane;
+  int* wcnt = reinterpret_cast<int*>(lds_raw);  // [16][E]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = blockIdx.x;
+  const int s = c * kChunk + threadIdx.x;
+  for (int i = threadIdx.x; i < 16 * E; i += kChunk) wcnt[i] = 0;
   const int e = s < nslots ? idx[s] : -1;
   int rk = 0, later = 0;
   for (int j = 0; j < 64; ++j) {
@@ -479,45 +614,48 @@ __global__ void __launch_bounds__(256) dispatch_count(const int32_t* __restrict_
       if (j > lane) ++later;
     }
   }
-  if (s < nslots) rank[s] = rk;
-  if (e >= 0 && later == 0) cnt[e] = rk + 1;
-  wave_sync_lds();
-  for (int ee = lane; ee < E; ee += 64) chunk_cnt[(size_t)chunk * E + ee] = cnt[ee];
+  __syncthreads();
+  if (e >= 0 && later == 0) wcnt[wave * E + e] = rk + 1;
+  __syncthreads();
+  for (int q = threadIdx.x; q < E; q += kChunk) {
+    int run = 0;
+    for (int w = 0; w < 16; ++w) {
+      const int t = wcnt[w * E + q];
+      wcnt[w * E + q] = run;
+      run += t;
+    }
+    chunk_cnt[(size_t)c * E + q] = run;
+  }
+  __syncthreads();
+  if (s < nslots) rank[s] = e >= 0 ? wcnt[wave * E + e] + rk : 0;
 }
 
-// One block: offsets[E+1], the ascending list of experts with tokens (used[], n_used), and
-// chunk_cnt overwritten with each chunk's base position per expert.
+// One block of 1024 threads (E <= 1024): offsets[E+1], used[] / n_used, and chunk_cnt overwritten with
+// each chunk's base position per expert.
 __global__ void __launch_bounds__(1024) dispatch_scan(int32_t* __restrict__ chunk_cnt, int nchunks, int E,
                                                       int32_t* __restrict__ offsets, int32_t* __restrict__ used,
                                                       int32_t* __restrict__ n_used) {
-  extern __shared__ __align__(16) unsigned char lds_raw[];
-  int* tot = reinterpret_cast<int*>(lds_raw);
-  for (int e = threadIdx.x; e < E; e += blockDim.x) {
-    int acc = 0;
-    for (int c = 0; c < nchunks; ++c) acc += chunk_cnt[(size_t)c * E + e];
-    tot[e] = acc;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int run = 0, nu = 0;
-    for (int e = 0; e < E; ++e) {
-      const int n = tot[e];
-      offsets[e] = run;
-      tot[e] = run;
-      run += n;
-      if (n > 0) used[nu++] = e;
-    }
-    offsets[E] = run;
-    *n_used = nu;
-  }
-  __syncthreads();
-  for (int e = threadIdx.x; e < E; e += blockDim.x) {
-    int run = tot[e];
+  __shared__ int tmp[16];
+  const int e = threadIdx.x;
+  int tot = 0;
+  if (e < E)
+    for (int c = 0; c < nchunks; ++c) tot += chunk_cnt[(size_t)c * E + e];
+  int all = 0, nu = 0;
+  const int off = block_exclusive_scan(e < E ? tot : 0, tmp, &all);
+  const int upos = block_exclusive_scan(e < E && tot > 0 ? 1 : 0, tmp, &nu);
+  if (e < E) {
+    offsets[e] = off;
+    if (tot > 0) used[upos] = e;
+    int run = off;
     for (int c = 0; c < nchunks; ++c) {
       const int n = chunk_cnt[(size_t)c * E + e];
       chunk_cnt[(size_t)c * E + e] = run;
       run += n;
     }
+  }
+  if (e == 0) {
+    offsets[E] = all;
+    *n_used = nu;
   }
 }
 
@@ -532,7 +670,7 @@ __global__ void __launch_bounds__(256) dispatch_scatter(const int32_t* __restric
     pos[s] = -1;
     return;
   }
-  const int p = chunk_base[(size_t)(s / 64) * E + e] + rank[s];
+  const int p = chunk_base[(size_t)(s / kChunk) * E + e] + rank[s];
   perm[p] = s;
   pos[s] = p;
 }
@@ -566,17 +704,23 @@ __global__ void __launch_bounds__(512) route_dispatch_small(const float* __restr
     if (e >= 0) atomicAdd(&cnt[e], 1);
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    int run = 0, nu = 0;
-    for (int q = 0; q < E; ++q) {
-      const int c = cnt[q];
-      ds.offsets[q] = run;
-      cnt[q] = run;
-      run += c;
-      if (c > 0) ds.used[nu++] = q;
+  {
+    // E <= 512 = blockDim: one expert per thread
+    const int q = threadIdx.x;
+    const int c = q < E ? cnt[q] : 0;
+    int all = 0, nu = 0;
+    const int off = block_exclusive_scan(c, cnt + E, &all);
+    const int upos = block_exclusive_scan(c > 0 ? 1 : 0, cnt + E, &nu);
+    if (q < E) {
+      ds.offsets[q] = off;
+      if (c > 0) ds.used[upos] = q;
     }
-    ds.offsets[E] = run;
-    *ds.n_used = nu;
+    __syncthreads();
+    if (q < E) cnt[q] = off;
+    if (q == 0) {
+      ds.offsets[E] = all;
+      *ds.n_used = nu;
+    }
   }
   __syncthreads();
   if (sl < n) {
@@ -597,24 +741,32 @@ __global__ void __launch_bounds__(512) route_dispatch_small(const float* __restr
 
 int launch_router_logits(const float* x, int T, int d, int E, const float* R, float* logits, hipStream_t st) {
   if (T <= 0) return EMBER_OK;
-  if (T < 32 && 2 * (d + 8) <= kRouterLdsFloats) {
-    const int EG = router_lds_rows(d);
-    dim3 grid((E + EG - 1) / EG, T);
-    router_logits_lds<<<grid, 256, (size_t)(EG + 1) * (d + 8) * sizeof(float), st>>>(x, R, logits, T, d, E);
-  } else if (d % 4 == 0) {
+  // rows per block: as many as fit, but no more than keeps >= 256 blocks in flight
+  const int EG = max(1, min(router_lds_rows(d), (int)(((int64_t)T * E + 255) / 256)));
+  const int64_t lds_blocks = (int64_t)T * ((E + EG - 1) / EG);
+  if (2 * (d + 8) <= kRouterLdsFloats && (lds_blocks <= 1024 || d % 4)) {
+    // few blocks: each stages whole rows once and runs its chains from LDS (one memory latency)
     static const bool lds_ok =
-        hipFuncSetAttribute(reinterpret_cast<const void*>(&router_logits_pt<32, 8>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, 2 * 40 * (RP_KT + 4) * (int)sizeof(float)) ==
-        hipSuccess;
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&router_logits_lds), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            kRouterLdsFloats * (int)sizeof(float)) == hipSuccess;
+    if (!lds_ok) return EMBER_ERR_LAUNCH;
+    dim3 grid((E + EG - 1) / EG, T);
+    router_logits_lds<<<grid, 256, (size_t)(EG + 1) * (d + 8) * sizeof(float), st>>>(x, R, logits, T, d, E, EG);
+  } else if (d % 4 == 0) {
+    const size_t lds_small = (size_t)2 * (32 + 8) * (256 + 4) * sizeof(float);
+    const size_t lds_big = (size_t)2 * (32 + 32) * (128 + 4) * sizeof(float);
+    static const bool lds_ok =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&router_logits_pt<32, 8, 1, 1, 256>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_small) == hipSuccess &&
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&router_logits_pt<32, 32, 2, 2, 128>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_big) == hipSuccess;
     if (!lds_ok) return EMBER_ERR_LAUNCH;
     if (E <= 8) {
       dim3 grid((T + 31) / 32, (E + 7) / 8);
-      router_logits_pt<32, 8><<<grid, 256, (size_t)2 * (32 + 8) * (RP_KT + 4) * sizeof(float), st>>>(x, R, logits, T,
-                                                                                                   d, E);
+      router_logits_pt<32, 8, 1, 1, 256><<<grid, 256, lds_small, st>>>(x, R, logits, T, d, E);
     } else {
-      dim3 grid((T + 15) / 16, (E + 15) / 16);
-      router_logits_pt<16, 16><<<grid, 256, (size_t)2 * (16 + 16) * (RP_KT + 4) * sizeof(float), st>>>(x, R, logits,
-                                                                                                     T, d, E);
+      dim3 grid((T + 31) / 32, (E + 31) / 32);
+      router_logits_pt<32, 32, 2, 2, 128><<<grid, 256, lds_big, st>>>(x, R, logits, T, d, E);
     }
   } else if (T >= 32 && E >= 8) {
     dim3 grid((T + RL_TT - 1) / RL_TT, (E + RL_TE - 1) / RL_TE);
@@ -645,7 +797,7 @@ int launch_route_dispatch(const float* logits, int T, int E, int k, int renorm, 
     int s = launch_route(logits, T, E, k, renorm, routed, sigmoid, bias, groups_n, groups_top, idx, gates, st);
     return s ? s : launch_dispatch(idx, T, k, E, ds, st);
   }
-  const size_t lds = kSmallT * route_wave_lds(E) + (size_t)(kSmallSlots + E) * sizeof(int);
+  const size_t lds = kSmallT * route_wave_lds(E) + (size_t)(kSmallSlots + E + 16) * sizeof(int);
   route_dispatch_small<<<1, 512, lds, st>>>(logits, T, E, k, renorm, routed, sigmoid, bias, groups_n, groups_top, idx,
                                             gates, ds);
   return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
@@ -653,10 +805,10 @@ int launch_route_dispatch(const float* logits, int T, int E, int k, int renorm, 
 
 int launch_dispatch(const int32_t* idx, int T, int k, int E, const DispatchScratch& ds, hipStream_t st) {
   const int nslots = T * k;
-  const int nchunks = (nslots + 63) / 64;
+  const int nchunks = (nslots + kChunk - 1) / kChunk;
   if (nslots <= 0) return EMBER_OK;
-  dispatch_count<<<(nchunks + 3) / 4, 256, 4 * (size_t)E * sizeof(int), st>>>(idx, nslots, E, ds.rank, ds.chunk_cnt);
-  dispatch_scan<<<1, 1024, (size_t)E * sizeof(int), st>>>(ds.chunk_cnt, nchunks, E, ds.offsets, ds.used, ds.n_used);
+  dispatch_count<<<nchunks, kChunk, 16 * (size_t)E * sizeof(int), st>>>(idx, nslots, E, ds.rank, ds.chunk_cnt);
+  dispatch_scan<<<1, 1024, 0, st>>>(ds.chunk_cnt, nchunks, E, ds.offsets, ds.used, ds.n_used);
   dispatch_scatter<<<(nslots + 255) / 256, 256, 0, st>>>(idx, nslots, E, ds.rank, ds.chunk_cnt, ds.perm, ds.pos);
   return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
 }
