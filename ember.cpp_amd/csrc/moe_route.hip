@@ -9,7 +9,7 @@
 //    (moe_math.hpp); the DeepSeek-style router runs the reference's float algorithm serially.
 // The dispatch permutation has no reference counterpart: slots s = t*k + j are stably sorted by
 // expert id (offsets[E+1], perm[p] = s, pos[s] = p), built without atomics on global memory.
-#include "moe_internal.hpp"
+#include "moe_route_dev.hpp"
 
 namespace ember_moe {
 using namespace ember_math;
@@ -243,312 +243,6 @@ __global__ void __launch_bounds__(256) router_logits_tiled(const float* __restri
   }
 }
 
-// ---------------------------------------------------------------------------------------------
-// Routing: one wave per token.
-
-__device__ inline float smax(float a, float b) { return (a < b) ? b : a; }  // std::max(a, b)
-
-// a is a strictly better argmax candidate than b: larger value, ties to the lower index; -1 = none.
-__device__ inline bool better(float va, int ia, float vb, int ib) {
-  if (ia < 0) return false;
-  if (ib < 0) return true;
-  return va > vb || (va == vb && ia < ib);
-}
-
-__device__ inline void wave_sync_lds() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-// moe_ffn_f32_cpu's routing (utils.cpp:706-733), serial, for rows holding a NaN.
-__device__ void route_softmax_serial(const float* r, int E, int k, int renorm, char* taken, int* picks,
-                                     int32_t* idx, float* gates) {
-  for (int e = 0; e < E; ++e) taken[e] = 0;
-  const int kk = min(k, E);
-  for (int j = 0; j < kk; ++j) {
-    int best = -1;
-    for (int e = 0; e < E; ++e)
-      if (!taken[e] && (best < 0 || r[e] > r[best])) best = e;
-    taken[best] = 1;
-    picks[j] = best;
-  }
-  for (int a = 1; a < kk; ++a)
-    for (int b = a; b > 0 && picks[b - 1] > picks[b]; --b) {
-      const int tmp = picks[b];
-      picks[b] = picks[b - 1];
-      picks[b - 1] = tmp;
-    }
-  float mx = -__builtin_inff();
-  double z = 0.0;
-  if (renorm) {
-    for (int j = 0; j < kk; ++j) mx = smax(mx, r[picks[j]]);
-    for (int j = 0; j < kk; ++j) z = z + exp_glibc((double)(r[picks[j]] - mx));
-  } else {
-    for (int e = 0; e < E; ++e) mx = smax(mx, r[e]);
-    for (int e = 0; e < E; ++e) z = z + exp_glibc((double)(r[e] - mx));
-  }
-  for (int j = 0; j < k; ++j) {
-    idx[j] = j < kk ? picks[j] : -1;
-    gates[j] = j < kk ? (float)(exp_glibc((double)(r[picks[j]] - mx)) / z) : 0.0f;
-  }
-}
-
-// moe_ffn_routed_f32_cpu's router (utils.cpp:766-820), serial: float scores, selection bias, groups.
-__device__ void route_routed_serial(const float* r, int E, int k, int renorm, int sigmoid, const float* bias,
-                                    int groups_n, int groups_top, float* s, float* c, char* cand, char* taken,
-                                    int* picks, int32_t* idx, float* gates) {
-  if (sigmoid) {
-    for (int e = 0; e < E; ++e) s[e] = 1.0f / (1.0f + expf_glibc(-r[e]));
-  } else {
-    float mx = -__builtin_inff();
-    for (int e = 0; e < E; ++e) mx = smax(mx, r[e]);
-    float z = 0.0f;
-    for (int e = 0; e < E; ++e) {
-      s[e] = expf_glibc(r[e] - mx);
-      z = z + s[e];
-    }
-    for (int e = 0; e < E; ++e) s[e] = s[e] / z;
-  }
-  for (int e = 0; e < E; ++e) c[e] = bias ? s[e] + bias[e] : s[e];
-  for (int e = 0; e < E; ++e) cand[e] = 1;
-  if (groups_n > 1) {
-    const int per = E / groups_n;
-    float* gscore = c + E;  // the caller reserves 2E floats at c; groups_n <= E
-    for (int g = 0; g < groups_n; ++g) {
-      float top1 = -__builtin_inff(), top2 = -__builtin_inff();
-      for (int e = g * per; e < (g + 1) * per; ++e) {
-        if (c[e] > top1) {
-          top2 = top1;
-          top1 = c[e];
-        } else if (c[e] > top2) {
-          top2 = c[e];
-        }
-      }
-      gscore[g] = per == 1 ? top1 : top1 + top2;
-    }
-    for (int g = 0; g < groups_n; ++g) taken[g] = 0;
-    for (int j = 0; j < groups_top && j < groups_n; ++j) {
-      int best = -1;
-      for (int g = 0; g < groups_n; ++g)
-        if (!taken[g] && (best < 0 || gscore[g] > gscore[best])) best = g;
-      taken[best] = 1;
-    }
-    for (int e = 0; e < E; ++e) cand[e] = taken[e / per];
-  }
-  for (int e = 0; e < E; ++e) taken[e] = 0;
-  int n = 0;
-  for (int j = 0; j < k; ++j) {
-    int best = -1;
-    for (int e = 0; e < E; ++e)
-      if (cand[e] && !taken[e] && (best < 0 || c[e] > c[best])) best = e;
-    if (best < 0) break;
-    taken[best] = 1;
-    picks[n++] = best;
-  }
-  for (int a = 1; a < n; ++a)
-    for (int b = a; b > 0 && picks[b - 1] > picks[b]; --b) {
-      const int tmp = picks[b];
-      picks[b] = picks[b - 1];
-      picks[b - 1] = tmp;
-    }
-  float z = 0.0f;
-  for (int j = 0; j < n; ++j) z = z + s[picks[j]];
-  for (int j = 0; j < k; ++j) {
-    idx[j] = j < n ? picks[j] : -1;
-    gates[j] = j < n ? (renorm ? s[picks[j]] / z : s[picks[j]]) : 0.0f;
-  }
-}
-
-// Per-wave LDS footprint of route_kernel for E experts.
-__host__ __device__ inline size_t route_wave_lds(int E) {
-  const size_t bytes = (size_t)E * 8 /*ex*/ + (size_t)E * 4 /*s*/ + (size_t)2 * E * 4 /*c + group scores*/ +
-                       (size_t)64 * 4 /*picks*/ + (size_t)((2 * E + 3) & ~3) /*cand, taken*/ + (size_t)E * 4 /*row*/;
-  return (bytes + 15) & ~(size_t)15;
-}
-
-// k passes of a wave-wide argmax over val[e] (LDS, NaN-free), each pass taking the largest untaken
-// value with ties to the lower index — the result of the reference's serial strict-> scans. Experts
-// with cand[e] == 0 are skipped (cand may be null); a pass that finds nothing ends the search. Lane 0
-// writes the picks in pick order; returns their number (uniform across the wave).
-__device__ int wave_topk(const float* val, const char* cand, int E, int k, int* picks) {
-  const int lane = threadIdx.x & 63;
-  uint32_t mine_taken = 0;  // bit q: expert lane + 64q taken (E <= 2048)
-  int n = 0;
-  for (int j = 0; j < k; ++j) {
-    float bv = 0.0f;
-    int bi = -1;
-    for (int e = lane, q = 0; e < E; e += 64, ++q)
-      if (!((mine_taken >> q) & 1u) && (!cand || cand[e]) && better(val[e], e, bv, bi)) {
-        bv = val[e];
-        bi = e;
-      }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-      const float ov = __shfl_xor(bv, off, 64);
-      const int oi = __shfl_xor(bi, off, 64);
-      if (better(ov, oi, bv, bi)) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-    if (bi < 0) break;
-    if ((bi & 63) == lane) mine_taken |= 1u << (bi >> 6);
-    if (lane == 0) picks[n] = bi;
-    ++n;
-  }
-  wave_sync_lds();
-  if (lane == 0)
-    for (int a = 1; a < n; ++a)
-      for (int b = a; b > 0 && picks[b - 1] > picks[b]; --b) {
-        const int tmp = picks[b];
-        picks[b] = picks[b - 1];
-        picks[b - 1] = tmp;
-      }
-  wave_sync_lds();
-  return n;
-}
-
-// moe_ffn_routed_f32_cpu's router (utils.cpp:766-820) across the wave for NaN-free scores: every
-// per-expert float operation is the reference's; the float sums that fix rounding (the softmax
-// normaliser, the renorm denominator) stay serial in ascending expert order on lane 0; the maximum,
-// the group top-2 and the argmax passes are order-independent for NaN-free values. Returns false
-// (nothing written) when a NaN appears in the scores, so the caller falls back to the serial scan.
-__device__ bool route_routed_wave(const float* row, int E, int k, int renorm, int sigmoid, const float* bias,
-                                  int groups_n, int groups_top, float* s, float* c, char* cand, int* picks,
-                                  int32_t* idx_t, float* gate_t) {
-  const int lane = threadIdx.x & 63;
-  if (sigmoid) {
-    for (int e = lane; e < E; e += 64) s[e] = 1.0f / (1.0f + expf_glibc(-row[e]));
-  } else {
-    float mx = -__builtin_inff();
-    for (int e = lane; e < E; e += 64) mx = smax(mx, row[e]);
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) mx = smax(mx, __shfl_xor(mx, off, 64));
-    for (int e = lane; e < E; e += 64) s[e] = expf_glibc(row[e] - mx);
-    wave_sync_lds();
-    float z = 0.0f;
-    if (lane == 0)
-      for (int e = 0; e < E; ++e) z = z + s[e];
-    z = __shfl(z, 0, 64);
-    for (int e = lane; e < E; e += 64) s[e] = s[e] / z;
-  }
-  bool bad = false;
-  for (int e = lane; e < E; e += 64) {
-    const float v = bias ? s[e] + bias[e] : s[e];
-    c[e] = v;
-    bad |= (v != v) || (s[e] != s[e]);
-  }
-  if (__any(bad)) return false;
-  wave_sync_lds();
-  const char* cmask = nullptr;
-  if (groups_n > 1) {
-    const int per = E / groups_n;
-    float* gsc = c + E;
-    for (int g = lane; g < groups_n; g += 64) {
-      float top1 = -__builtin_inff(), top2 = -__builtin_inff();
-      for (int e = g * per; e < (g + 1) * per; ++e) {
-        if (c[e] > top1) {
-          top2 = top1;
-          top1 = c[e];
-        } else if (c[e] > top2) {
-          top2 = c[e];
-        }
-      }
-      gsc[g] = per == 1 ? top1 : top1 + top2;
-    }
-    wave_sync_lds();
-    const int ng = wave_topk(gsc, nullptr, groups_n, groups_top, picks);
-    for (int e = lane; e < E; e += 64) cand[e] = 0;
-    wave_sync_lds();
-    for (int j = 0; j < ng; ++j)
-      for (int e = picks[j] * per + lane; e < (picks[j] + 1) * per; e += 64) cand[e] = 1;
-    wave_sync_lds();
-    cmask = cand;
-  }
-  const int n = wave_topk(c, cmask, E, k, picks);
-  float z = 0.0f;
-  for (int j = 0; j < n; ++j) z = z + s[picks[j]];
-  if (lane < k) {
-    if (lane < n) {
-      const int e = picks[lane];
-      idx_t[lane] = e;
-      gate_t[lane] = renorm ? s[e] / z : s[e];
-    } else {
-      idx_t[lane] = -1;
-      gate_t[lane] = 0.0f;
-    }
-  }
-  return true;
-}
-
-// Routes one token on one wave (all 64 lanes call it). NaN-free rows run wave-parallel scans whose
-// results equal the reference's serial scans; rows with a NaN (in the logits or in the DeepSeek-style
-// scores) run the reference's serial algorithm on lane 0. wl: route_wave_lds(E) bytes of LDS owned by
-// this wave.
-__device__ void route_token(const float* __restrict__ r, int E, int k, int renorm, int routed, int sigmoid,
-                            const float* __restrict__ bias, int groups_n, int groups_top, unsigned char* wl,
-                            int32_t* __restrict__ idx_t, float* __restrict__ gate_t) {
-  const int lane = threadIdx.x & 63;
-  double* ex = reinterpret_cast<double*>(wl);
-  float* s = reinterpret_cast<float*>(wl + (size_t)E * 8);
-  float* cbuf = s + E;
-  int* picks = reinterpret_cast<int*>(cbuf + 2 * E);
-  char* cand = reinterpret_cast<char*>(picks + 64);
-  char* taken = cand + E;
-  float* row = reinterpret_cast<float*>(wl + route_wave_lds(E) - (size_t)E * 4);
-  bool has_nan = false;
-  for (int e = lane; e < E; e += 64) {
-    const float v = r[e];
-    row[e] = v;
-    has_nan |= (v != v);
-  }
-  has_nan = __any(has_nan);
-  wave_sync_lds();
-  if (routed && !has_nan && groups_n <= 64 &&
-      route_routed_wave(row, E, k, renorm, sigmoid, bias, groups_n, groups_top, s, cbuf, cand, picks, idx_t, gate_t))
-    return;
-  if (routed || has_nan) {
-    wave_sync_lds();
-    if (lane == 0) {
-      if (routed)
-        route_routed_serial(row, E, k, renorm, sigmoid, bias, groups_n, groups_top, s, cbuf, cand, taken, picks, idx_t,
-                            gate_t);
-      else
-        route_softmax_serial(row, E, k, renorm, taken, picks, idx_t, gate_t);
-    }
-    return;
-  }
-  const int kk = wave_topk(row, nullptr, E, min(k, E), picks);
-  float mx = -__builtin_inff();
-  double z = 0.0;
-  if (renorm) {
-    for (int j = 0; j < kk; ++j) mx = smax(mx, row[picks[j]]);
-    for (int j = 0; j < kk; ++j) z = z + exp_glibc((double)(row[picks[j]] - mx));
-  } else {
-    // The maximum of a NaN-free row does not depend on the scan order (only the sign of a zero
-    // maximum can, and r - (+0) and r - (-0) round to equal exp arguments for every r).
-    for (int e = lane; e < E; e += 64) mx = smax(mx, row[e]);
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) mx = smax(mx, __shfl_xor(mx, off, 64));
-    for (int e = lane; e < E; e += 64) ex[e] = exp_glibc((double)(row[e] - mx));
-    wave_sync_lds();
-    if (lane == 0)
-      for (int e = 0; e < E; ++e) z = z + ex[e];  // ascending, as the reference sums
-    z = __shfl(z, 0, 64);
-  }
-  if (lane < k) {
-    if (lane < kk) {
-      const int e = picks[lane];
-      idx_t[lane] = e;
-      gate_t[lane] = (float)(exp_glibc((double)(row[e] - mx)) / z);
-    } else {
-      idx_t[lane] = -1;
-      gate_t[lane] = 0.0f;
-    }
-  }
-}
-
 __global__ void __launch_bounds__(256) route_kernel(const float* __restrict__ logits, int T, int E, int k, int renorm,
                                                     int routed, int sigmoid, const float* __restrict__ bias,
                                                     int groups_n, int groups_top, int32_t* __restrict__ idx,
@@ -568,34 +262,6 @@ __global__ void __launch_bounds__(256) route_kernel(const float* __restrict__ lo
 // (2) one block scans the counts into per-expert offsets, the list of experts with tokens, and each
 // chunk's base position per expert; (3) each slot lands at base[chunk][e] + rank.
 constexpr int kChunk = 1024;
-
-// Exclusive prefix sum over the threads of a block (one value per thread, blockDim.x <= 1024);
-// tmp: 16 ints of LDS. Every thread of the block must call it.
-__device__ int block_exclusive_scan(int v, int* tmp, int* total) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
-  int x = v;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int y = __shfl_up(x, off, 64);
-    if (lane >= off) x += y;
-  }
-  if (lane == 63) tmp[wave] = x;
-  __syncthreads();
-  if (wave == 0) {
-    int t = lane < nw ? tmp[lane] : 0;
-#pragma unroll
-    for (int off = 1; off < 16; off <<= 1) {
-      const int y = __shfl_up(t, off, 64);
-      if (lane >= off) t += y;
-    }
-    if (lane < nw) tmp[lane] = t;
-  }
-  __syncthreads();
-  const int base = wave ? tmp[wave - 1] : 0;
-  *total = tmp[nw - 1];
-  __syncthreads();
-  return base + x - v;
-}
 
 __global__ void __launch_bounds__(kChunk) dispatch_count(const int32_t* __restrict__ idx, int nslots, int E,
                                                          int32_t* __restrict__ rank, int32_t* __restrict__ chunk_cnt) {
