@@ -190,6 +190,9 @@ def main():
     ap.add_argument("--tokens", type=int, default=None, help="headline token count (default: the config's first)")
     ap.add_argument("--sweep", type=str, default=None, help="comma-separated token counts (default: the config's)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run 5 plain device-to-device copies of MIB MiB (the reference kernel that scales "
+                         "rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes), then exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for {args.gpus}); the multi-GPU layout is a design "
@@ -197,6 +200,16 @@ def main():
         sys.exit(2)
 
     import torch
+
+    if args.calibrate_copy:
+        n = args.calibrate_copy * (1 << 20) // 4
+        src = torch.randn(n, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] copied {args.calibrate_copy} MiB x 5")
+        return
 
     import ember_moe as em
 

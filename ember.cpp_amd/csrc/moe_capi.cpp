@@ -50,8 +50,10 @@ int check_matrix(const void* p, int type, int K) {
   const int64_t rb = row_bytes(type, K);
   if (rb == -2) return EMBER_ERR_TYPE;
   if (rb < 0) return EMBER_ERR_SHAPE;
-  // the decode kernel stages one activation row of K elements per token in 64 KiB of LDS
-  if ((type_quantizes_activations(type) ? (int64_t)K * 2 + K / 32 * 8 : ((int64_t)K + 63) / 64 * 256) > 65536) return EMBER_ERR_SHAPE;
+  // the decode kernel stages one activation row of K elements per token in LDS
+  if ((type_quantizes_activations(type) ? (int64_t)K * 2 + K / 32 * 8 : ((int64_t)K + 63) / 64 * 256) >
+      proj_max_row_bytes())
+    return EMBER_ERR_SHAPE;
   if (reinterpret_cast<uintptr_t>(p) % 16) return EMBER_ERR_ALIGN;
   return EMBER_OK;
 }
@@ -107,24 +109,13 @@ RouteLayout route_layout(int T, int E, int k, size_t base) {
   return l;
 }
 
-struct ActLayout {
-  size_t q, scale, sum;
-};
 struct Layout {
   size_t logits, idx, gates, offsets, perm, h, y, hs, ys;
   size_t x16, h16, hs16, tiles, n_tiles;  // MFMA paths
   int mode, mode_shared;                  // PathMode of the routed experts and of the shared expert
-  ActLayout xq, hq, hsq;  // int16 activations of x, h and the shared expert's h (quantized formats)
   RouteLayout r;
   size_t end;
 };
-size_t act_layout(size_t o, size_t rows, int K, bool on, ActLayout* a) {
-  const size_t n = on ? rows * (size_t)K : 0;
-  a->q = o; o = align_up(o + n * 2);
-  a->scale = o; o = align_up(o + n / 32 * 4);
-  a->sum = o; o = align_up(o + n / 32 * 4);
-  return o;
-}
 Layout layout(const ember_moe_layer* w, int T) {
   Layout l;
   const size_t slots = (size_t)T * w->k;
@@ -139,11 +130,6 @@ Layout layout(const ember_moe_layer* w, int T) {
   l.y = o; o = align_up(o + slots * w->d * 4);
   l.hs = o; o = align_up(o + (size_t)T * w->d_ff_shared * 4);
   l.ys = o; o = align_up(o + (w->d_ff_shared > 0 ? (size_t)T * w->d * 4 : 0));
-  const bool qx = type_quantizes_activations(w->gate_type) ||
-                  (w->d_ff_shared > 0 && type_quantizes_activations(w->gate_shared_type));
-  o = act_layout(o, T, w->d, qx, &l.xq);
-  o = act_layout(o, slots, w->d_ff, type_quantizes_activations(w->down_type), &l.hq);
-  o = act_layout(o, T, w->d_ff_shared, w->d_ff_shared > 0 && type_quantizes_activations(w->down_shared_type), &l.hsq);
   l.mode = path_mode(w->gate_type, w->d, w->down_type, w->d_ff, (double)T * w->k / w->E);
   l.mode_shared = w->d_ff_shared > 0
                       ? path_mode(w->gate_shared_type, w->d, w->down_shared_type, w->d_ff_shared, (double)T)
@@ -164,10 +150,6 @@ Layout layout(const ember_moe_layer* w, int T) {
 template <class P>
 P* at(void* base, size_t off) {
   return reinterpret_cast<P*>(static_cast<char*>(base) + off);
-}
-
-ActQ act_at(void* scratch, const ActLayout& l, int K) {
-  return ActQ{at<int16_t>(scratch, l.q), at<float>(scratch, l.scale), at<int>(scratch, l.sum), K};
 }
 
 DispatchScratch dispatch_scratch(void* scratch, const RouteLayout& r, int32_t* offsets, int32_t* perm) {
@@ -235,26 +217,28 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
   float* h = at<float>(scratch, l.h);
   float* y = at<float>(scratch, l.y);
 
+  const int groups_n = std::max(w->groups_n, 1), groups_top = std::max(w->groups_top, 1);
+  const int renorm = w->renorm ? 1 : 0, routed = is_routed(w) ? 1 : 0;
+  const int sigmoid = w->scoring == EMBER_SCORE_SIGMOID ? 1 : 0;
   mark(ev, 0, st);
   if ((s = launch_router_logits(x, T, d, E, w->router, logits, st))) return s;
   mark(ev, 1, st);
-  const int groups_n = std::max(w->groups_n, 1), groups_top = std::max(w->groups_top, 1);
-  if ((s = launch_route_dispatch(logits, T, E, k, w->renorm ? 1 : 0, is_routed(w) ? 1 : 0,
-                                 w->scoring == EMBER_SCORE_SIGMOID ? 1 : 0, w->selection_bias, groups_n, groups_top,
+  if ((s = launch_route_dispatch(logits, T, E, k, renorm, routed, sigmoid, w->selection_bias, groups_n, groups_top,
                                  idx, gates, ds, st)))
     return s;
   mark(ev, 2, st);
   mark(ev, 3, st);
 
-  const ActQ xq = act_at(scratch, l.xq, d);
-  const bool shared_mfma = w->d_ff_shared > 0 && l.mode_shared != kGemv;
-  const bool gemv_x = (l.mode == kGemv && type_quantizes_activations(w->gate_type)) ||
-                      (w->d_ff_shared > 0 && !shared_mfma && type_quantizes_activations(w->gate_shared_type));
-  if (gemv_x)
-    if ((s = launch_quantize_act(x, T, d, xq, st))) return s;
+  const bool shared = w->d_ff_shared > 0;
+  const bool shared_mfma = shared && l.mode_shared != kGemv;
+  // the shared expert joins the routed decode launches when its type matches (one more segment)
+  const bool shared_fused = shared && !shared_mfma && l.mode == kGemv && w->gate_shared_type == w->gate_type &&
+                            w->down_shared_type == w->down_type;
   _Float16* x16 = at<_Float16>(scratch, l.x16);
   if (l.mode != kGemv || shared_mfma)
     if ((s = launch_to_f16(x, (int64_t)T * d, x16, st))) return s;
+  float* ys = shared ? at<float>(scratch, l.ys) : nullptr;
+  float* hs = at<float>(scratch, l.hs);
 
   if (l.mode != kGemv) {
     const bool skinny = l.mode == kSkinny;
@@ -298,51 +282,57 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     if ((s = gemm(g, false, mt))) return s;
     mark(ev, 5, st);
   } else {
-
-  ProjArgs a{};
-  a.offsets = offsets;
-  a.used = ds.used;
-  a.n_used = ds.n_used;
-  a.perm = perm;
-  a.k = k;
-  a.T = T;
-  a.max_segments = std::min(E, T * k);
-  // gate/up + SwiGLU: x rows gathered through perm, h in sorted order.
-  a.w0 = w->gate;
-  a.w1 = w->up;
-  a.type = w->gate_type;
-  a.rows = d_ff;
-  a.K = d;
-  a.expert_stride = row_bytes(w->gate_type, d) * d_ff;
-  a.in = x;
-  a.act = xq;
-  a.out = h;
-  a.gated = true;
-  a.in_by_perm = true;
-  if ((s = launch_projection(a, st))) return s;
-  mark(ev, 4, st);
-  const ActQ hq = act_at(scratch, l.hq, d_ff);
-  if (type_quantizes_activations(w->down_type))
-    if ((s = launch_quantize_act(h, T * k, d_ff, hq, st))) return s;
-  // down: h -> y, both in sorted order.
-  a.w0 = w->down;
-  a.w1 = nullptr;
-  a.type = w->down_type;
-  a.rows = d;
-  a.K = d_ff;
-  a.expert_stride = row_bytes(w->down_type, d_ff) * d;
-  a.in = h;
-  a.act = hq;
-  a.out = y;
-  a.gated = false;
-  a.in_by_perm = false;
-  if ((s = launch_projection(a, st))) return s;
-  mark(ev, 5, st);
-
+    // gate/up + SwiGLU (x rows gathered through perm, h in dispatch order), then down (h -> y)
+    ProjArgs a{};
+    a.type = w->gate_type;
+    a.gated = true;
+    a.w0 = w->gate;
+    a.w1 = w->up;
+    a.rows = d_ff;
+    a.K = d;
+    a.expert_stride = row_bytes(w->gate_type, d) * d_ff;
+    a.in = x;
+    a.out = h;
+    a.offsets = offsets;
+    a.used = ds.used;
+    a.n_used = ds.n_used;
+    a.perm = perm;
+    a.k = k;
+    a.in_by_perm = true;
+    a.max_segments = std::min(E, T * k);
+    a.T = T;
+    if (shared_fused) {
+      a.s_w0 = w->gate_shared;
+      a.s_w1 = w->up_shared;
+      a.s_rows = w->d_ff_shared;
+      a.s_K = d;
+      a.s_in = x;
+      a.s_out = hs;
+    }
+    if ((s = launch_projection(a, st))) return s;
+    mark(ev, 4, st);
+    a.type = w->down_type;
+    a.gated = false;
+    a.w0 = w->down;
+    a.w1 = nullptr;
+    a.rows = d;
+    a.K = d_ff;
+    a.expert_stride = row_bytes(w->down_type, d_ff) * d;
+    a.in = h;
+    a.out = y;
+    a.in_by_perm = false;
+    if (shared_fused) {
+      a.s_w0 = w->down_shared;
+      a.s_w1 = nullptr;
+      a.s_rows = d;
+      a.s_K = w->d_ff_shared;
+      a.s_in = hs;
+      a.s_out = ys;
+    }
+    if ((s = launch_projection(a, st))) return s;
+    mark(ev, 5, st);
   }
-  float* ys = nullptr;
   if (shared_mfma) {
-    ys = at<float>(scratch, l.ys);
     _Float16* hs16 = at<_Float16>(scratch, l.hs16);
     GemmArgs g{};
     g.A = x16;
@@ -367,34 +357,26 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     g.out_h = nullptr;
     g.out_y = ys;
     if ((s = skinny ? launch_gemm_skinny(g, false, mt, st) : launch_gemm(g, false, mt, st))) return s;
-  } else if (w->d_ff_shared > 0) {
-    float* hs = at<float>(scratch, l.hs);
-    ys = at<float>(scratch, l.ys);
+  } else if (shared && !shared_fused) {
     ProjArgs b{};
-    b.T = T;
-    b.max_segments = 1;
-    b.w0 = w->gate_shared;
-    b.w1 = w->up_shared;
-    b.type = w->gate_shared_type;
-    b.rows = w->d_ff_shared;
-    b.K = d;
-    b.in = x;
-    b.act = xq;
-    b.out = hs;
     b.gated = true;
+    b.type = w->gate_shared_type;
+    b.T = T;
+    b.s_w0 = w->gate_shared;
+    b.s_w1 = w->up_shared;
+    b.s_rows = w->d_ff_shared;
+    b.s_K = d;
+    b.s_in = x;
+    b.s_out = hs;
     if ((s = launch_projection(b, st))) return s;
-    const ActQ hsq = act_at(scratch, l.hsq, w->d_ff_shared);
-    if (type_quantizes_activations(w->down_shared_type))
-      if ((s = launch_quantize_act(hs, T, w->d_ff_shared, hsq, st))) return s;
-    b.w0 = w->down_shared;
-    b.w1 = nullptr;
-    b.type = w->down_shared_type;
-    b.rows = d;
-    b.K = w->d_ff_shared;
-    b.in = hs;
-    b.act = hsq;
-    b.out = ys;
     b.gated = false;
+    b.type = w->down_shared_type;
+    b.s_w0 = w->down_shared;
+    b.s_w1 = nullptr;
+    b.s_rows = d;
+    b.s_K = w->d_ff_shared;
+    b.s_in = hs;
+    b.s_out = ys;
     if ((s = launch_projection(b, st))) return s;
   }
   mark(ev, 6, st);

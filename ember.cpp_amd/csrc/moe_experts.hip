@@ -19,220 +19,275 @@
 // the whole segment (grid-stride), with the next step's weights loaded before the current step is
 // computed. grid.y enumerates expert segments (experts that received tokens, from the dispatch
 // step), so no host synchronisation is needed.
+#include <cstdlib>
+#include <type_traits>
+
 #include "moe_fmt.hpp"
 
 namespace ember_moe {
 using namespace ember_math;
 
 
-// One projection pass. Thread layout: lane group of L lanes per row slot; RR rows per step; MT tokens
-// per pass over the weights. Steps (row group, chunk round) are double-buffered.
-template <int FMT, int RR, int MT, bool GATED>
-__global__ void __launch_bounds__(256) proj_kernel(ProjArgs a, int L_log2) {
-  using F = Fmt<FMT>;
-  constexpr int G = GATED ? 2 : 1;
-  const int L = 1 << L_log2;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int sub = lane >> L_log2, rl = lane & (L - 1);
-  const int slots_per_block = 4 * (64 >> L_log2);
-  const int slot = blockIdx.x * slots_per_block + wave * (64 >> L_log2) + sub;
-  const int nslots = gridDim.x * slots_per_block;
-  int e = 0, p0 = 0, M = a.T;
-  if (a.used) {
-    if ((int)blockIdx.y >= *a.n_used) return;
-    e = a.used[blockIdx.y];
-    p0 = a.offsets[e];
-    M = a.offsets[e + 1] - p0;
-  }
-  const int K = a.K;
-  const int64_t rb = F::row_bytes(K);
-  const int C = (K + F::CE - 1) / F::CE;
-  const int NC = (C + L - 1) / L;  // chunk rounds per row (uniform across the lane group)
-  const uint8_t* W0 = static_cast<const uint8_t*>(a.w0) + (int64_t)e * a.expert_stride;
-  const uint8_t* W1 = GATED ? static_cast<const uint8_t*>(a.w1) + (int64_t)e * a.expert_stride : W0;
-  const int ngroups = (a.rows + RR - 1) / RR;
-  // number of steps this slot walks: row groups slot, slot + nslots, ... times NC chunk rounds
-  const int my_groups = slot < ngroups ? (ngroups - 1 - slot) / nslots + 1 : 0;
-  const int nsteps = my_groups * NC;
+constexpr int kProjThreads = 512;            // 8 waves per block
+constexpr int kProjLdsBytes = 80 * 1024;     // staged activation rows per block (two blocks per CU)
 
+// f(integral_constant<int, j>) for j = 0 .. N-1 (compile-time ring positions)
+template <int N, class Fn, int... J>
+__device__ inline void ring_for_impl(Fn&& f, std::integer_sequence<int, J...>) {
+  (f(std::integral_constant<int, J>{}), ...);
+}
+template <int N, class Fn>
+__device__ inline void ring_for(Fn&& f) {
+  ring_for_impl<N>(f, std::make_integer_sequence<int, N>{});
+}
+
+// Which segment block b of G serves, and its share of that segment's rows. Routed segments get blocks
+// in proportion to their rows (the shared segment, when present, gets the rest), at least one each.
+struct SegView {
+  const uint8_t* W0;
+  const uint8_t* W1;
+  int rows, K, p0, M;
+  const float* in;
+  float* out;
+  bool by_perm;
+  int jb, nb;  // block index within the segment, blocks of the segment
+};
+
+// The dispatch order a launch schedules from (global arrays, or LDS copies after in-block routing).
+struct Dispatch {
+  int n_used;
+  const int32_t* used;
+  const int32_t* offsets;
+  const int32_t* perm;
+};
+
+template <bool GATED>
+__device__ inline bool seg_view(const ProjArgs& a, const Dispatch& dp, int b, int G, SegView& v) {
+  const int nseg = a.used ? dp.n_used : 0;
+  const int64_t r_rows = (int64_t)nseg * a.rows;
+  const int64_t s_rows = a.s_w0 ? a.s_rows : 0;
+  if (r_rows + s_rows == 0) return false;
+  int Gr = 0;
+  if (nseg > 0) Gr = s_rows ? (int)max((int64_t)nseg, min((int64_t)G - 1, G * r_rows / (r_rows + s_rows))) : G;
+  if (b < Gr) {
+    const int s = (int)((((int64_t)b + 1) * nseg - 1) / Gr);
+    const int bs = (int)(((int64_t)s * Gr) / nseg), be = (int)(((int64_t)(s + 1) * Gr) / nseg);
+    v.jb = b - bs;
+    v.nb = be - bs;
+    const int e = dp.used[s];
+    v.p0 = dp.offsets[e];
+    v.M = dp.offsets[e + 1] - v.p0;
+    v.W0 = static_cast<const uint8_t*>(a.w0) + (int64_t)e * a.expert_stride;
+    v.W1 = GATED ? static_cast<const uint8_t*>(a.w1) + (int64_t)e * a.expert_stride : v.W0;
+    v.rows = a.rows;
+    v.K = a.K;
+    v.in = a.in;
+    v.out = a.out;
+    v.by_perm = a.in_by_perm;
+  } else {
+    if (!s_rows) return false;
+    v.jb = b - Gr;
+    v.nb = G - Gr;
+    v.p0 = 0;
+    v.M = a.T;
+    v.W0 = static_cast<const uint8_t*>(a.s_w0);
+    v.W1 = GATED ? static_cast<const uint8_t*>(a.s_w1) : v.W0;
+    v.rows = a.s_rows;
+    v.K = a.s_K;
+    v.in = a.s_in;
+    v.out = a.s_out;
+    v.by_perm = false;
+  }
+  return true;
+}
+
+// One projection. A block serves a contiguous row range of one segment; each of its waves a
+// contiguous sub-range. L lanes (a power of two <= 64) cover a row, one chunk per lane per step
+// (looping NC rounds when a row has more than L chunks), so a step covers 64 / L rows. The weights of
+// step s + 1 are in flight while step s is computed (two register buffers). MT tokens per pass over
+// the weights; their activation rows are staged in LDS (quantized on the way for Q8_0 / Q4_K).
+template <int FMT, int MT, bool GATED, int NB, int NT, int WPE>
+__global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) proj_kernel(ProjArgs a) {
+  using F = Fmt<FMT>;
+  constexpr int G2 = GATED ? 2 : 1;
   extern __shared__ __align__(16) uint8_t act_lds[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = NT / 64;
+  Dispatch dp{a.used ? *a.n_used : 0, a.used, a.offsets, a.perm};
+  SegView v;
+  if (!seg_view<GATED>(a, dp, blockIdx.x, gridDim.x, v)) return;
+  const int rb0 = (int)((int64_t)v.jb * v.rows / v.nb), rb1 = (int)((int64_t)(v.jb + 1) * v.rows / v.nb);
+  const int rw0 = rb0 + wave * (rb1 - rb0) / nwaves, rw1 = rb0 + (wave + 1) * (rb1 - rb0) / nwaves;
+  const int K = v.K;
+  const int C = (K + F::CE - 1) / F::CE;
+  int Lg = 0;
+  while ((1 << Lg) < C && Lg < 6) ++Lg;
+  const int L = 1 << Lg, RPS = 64 >> Lg;
+  const int sub = lane >> Lg, rl = lane & (L - 1);
+  const int NC = (C + L - 1) / L;
+  const int nsteps = ((rw1 - rw0 + RPS - 1) / RPS) * NC;
+  const int64_t rb = F::row_bytes(K);
   const int row_lds = act_lds_bytes(F::QX, K);
-  __shared__ int rows[MT];
-  for (int m0 = 0; m0 < M; m0 += MT) {
-    __syncthreads();  // the previous token group's rows are no longer read
-    if (threadIdx.x < MT && m0 + (int)threadIdx.x < M) {
-      const int p = p0 + m0 + threadIdx.x;
-      rows[threadIdx.x] = a.in_by_perm ? a.perm[p] / a.k : p;
-    }
-    __syncthreads();
-    stage_rows<F::NGL>(F::QX, StageSrc{a.in, a.act.q, a.act.scale, a.act.sum, a.K}, rows, min(MT, M - m0), act_lds, row_lds);
-    __syncthreads();
-    float acc[G][RR][MT];
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int i = 0; i < RR; ++i)
-#pragma unroll
-        for (int m = 0; m < MT; ++m) acc[g][i][m] = 0.0f;
-    const int nvalid = min(MT, M - m0);
-    // weights of step st -> buf (zeros outside the row range / past the last chunk)
-    auto load_step = [&](int st, uint32_t (&buf)[G][RR][F::NW]) {
-      const int grp = slot + (st / NC) * nslots;
-      const int c = rl + (st % NC) * L;
-#pragma unroll
-      for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int i = 0; i < RR; ++i) {
-          const int r = grp * RR + i;
-          if (c < C && r < a.rows) {
-            F::load((g ? W1 : W0) + (int64_t)r * rb, c, K, buf[g][i]);
-          } else {
-#pragma unroll
-            for (int w = 0; w < F::NW; ++w) buf[g][i][w] = 0u;
-          }
-        }
+
+  __shared__ int rows_idx[MT];
+
+  // weights of matrix g (0: gate or the only one, 1: up) for step st; out-of-range (row, chunk) pairs
+  // load a valid neighbour, which dot() then ignores
+  auto load_step = [&](int st, int g, uint32_t (&buf)[F::NW]) {
+    const int r = min(rw0 + (st / NC) * RPS + sub, rw1 - 1);
+    const int c = min(rl + (st % NC) * L, C - 1);
+    F::load((g ? v.W1 : v.W0) + (int64_t)r * rb, c, K, buf);
+  };
+
+  // Weight loads form one sequence q = 0, 1, ... (gated: gate and up of a step alternate) that runs
+  // through a ring of NB register buffers: NB - 1 loads are in flight while one buffer is consumed.
+  const int nloads = nsteps * G2;
+#pragma unroll 1
+  for (int m0 = 0; m0 < v.M; m0 += MT) {
+    const int nvalid = min(MT, v.M - m0);
+    uint32_t buf[NB][F::NW];
+    // the first weights travel while the activations are staged
+    auto pre = [&](auto J) {
+      constexpr int j = decltype(J)::value;
+      if (j < nloads) load_step(j / G2, j % G2, buf[j]);
     };
-    for (int st = 0; st < nsteps; ++st) {
-      const int grp = slot + (st / NC) * nslots;
-      const int c = rl + (st % NC) * L;
-      uint32_t raw[G][RR][F::NW];
-      load_step(st, raw);
-      if (c < C) {
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-#pragma unroll
-          for (int i = 0; i < RR; ++i) F::template dot_tokens<MT>(raw[g][i], act_lds, row_lds, c, K, nvalid, acc[g][i]);
-      }
-      if (st % NC == NC - 1) {  // row group complete: reduce over the lane group and write
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-#pragma unroll
-          for (int i = 0; i < RR; ++i)
-#pragma unroll
-            for (int m = 0; m < MT; ++m) {
-              float v = acc[g][i][m];
-              for (int off = L >> 1; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-              acc[g][i][m] = v;
-            }
-        if (rl == 0) {
-#pragma unroll
-          for (int i = 0; i < RR; ++i) {
-            const int r = grp * RR + i;
-            if (r >= a.rows) continue;
-#pragma unroll
-            for (int m = 0; m < MT; ++m) {
-              if (m >= nvalid) continue;
-              const size_t o = (size_t)(p0 + m0 + m) * a.rows + r;
-              a.out[o] = GATED ? swiglu(acc[0][i][m], acc[G - 1][i][m]) : acc[0][i][m];
-            }
-          }
-        }
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-#pragma unroll
-          for (int i = 0; i < RR; ++i)
-#pragma unroll
-            for (int m = 0; m < MT; ++m) acc[g][i][m] = 0.0f;
-      }
+    ring_for<NB - 1>(pre);
+    __syncthreads();  // the previous pass no longer reads the staged rows
+    if (threadIdx.x < nvalid) {
+      const int p = v.p0 + m0 + threadIdx.x;
+      rows_idx[threadIdx.x] = v.by_perm ? dp.perm[p] / a.k : p;
     }
+    __syncthreads();
+    if constexpr (F::QX)
+      stage_rows_quant(v.in, K, rows_idx, nvalid, act_lds, row_lds);
+    else
+      stage_rows_f32<F::NGL>(v.in, K, rows_idx, nvalid, act_lds, row_lds);
+    __syncthreads();
+
+    float acc[G2][MT];
+#pragma unroll
+    for (int g = 0; g < G2; ++g)
+#pragma unroll
+      for (int m = 0; m < MT; ++m) acc[g][m] = 0.0f;
+
+    auto dot = [&](int st, const uint32_t (&b)[F::NW], float (&ac)[MT]) {
+      const int r = rw0 + (st / NC) * RPS + sub;
+      const int c = rl + (st % NC) * L;
+      if (c < C && r < rw1) F::template dot_tokens<MT>(b, act_lds, row_lds, c, K, nvalid, ac);
+    };
+    auto finish = [&](int st) {
+      if (st % NC != NC - 1) return;  // the row is complete: reduce over the lane group and write
+      const int r = rw0 + (st / NC) * RPS + sub;
+#pragma unroll
+      for (int g = 0; g < G2; ++g)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+          float t = acc[g][m];
+          for (int off = L >> 1; off >= 1; off >>= 1) t += __shfl_xor(t, off, 64);
+          acc[g][m] = t;
+        }
+      if (rl == 0 && r < rw1) {
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+          if (m < nvalid)
+            v.out[(size_t)(v.p0 + m0 + m) * v.rows + r] = GATED ? swiglu(acc[0][m], acc[G2 - 1][m]) : acc[0][m];
+      }
+#pragma unroll
+      for (int g = 0; g < G2; ++g)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[g][m] = 0.0f;
+    };
+    // One ring position per call, with compile-time buffer indices so the ring stays in registers. The
+    // walk advances U = lcm(NB, G2) loads per iteration, so that both the buffer (q % NB) and the
+    // matrix (q % G2) of load q are compile-time constants.
+    constexpr int U = (NB % G2 == 0) ? NB : NB * G2;
+    auto slot = [&](int q0, auto J) {
+      constexpr int j = decltype(J)::value;
+      const int q = q0 + j;
+      if (q < nloads) {
+        if (q + NB - 1 < nloads) load_step((q + NB - 1) / G2, (j + NB - 1) % G2, buf[(j + NB - 1) % NB]);
+        dot(q / G2, buf[j % NB], acc[j % G2]);
+        if (j % G2 == G2 - 1) finish(q / G2);
+      }
+    };
+#pragma unroll 1
+    for (int q0 = 0; q0 < nloads; q0 += U) ring_for<U>([&](auto J) { slot(q0, J); });
   }
 }
 
-constexpr int kProjLdsBytes = 64 * 1024;  // activation rows staged per block
-
-template <int FMT, int RR, bool GATED>
-int launch_proj_fmt(const ProjArgs& a, int MT, hipStream_t st) {
-  using F = Fmt<FMT>;
-  const int C = (a.K + F::CE - 1) / F::CE;
-  int L_log2 = 0;
-  while ((1 << L_log2) < C && L_log2 < 6) ++L_log2;
-  const int slots_per_block = 4 * (64 >> L_log2);
-  const int ngroups = (a.rows + RR - 1) / RR;
-  // enough blocks to fill the chip (~8 per CU over all segments), each slot walking a few groups
-  const int segs = std::max(a.max_segments, 1);
-  static const int kTarget = [] { const char* v = std::getenv("EMBER_PROJ_BLOCKS"); return v ? atoi(v) : 2048; }();
-  int blocks = (kTarget + segs - 1) / segs;
-  blocks = std::min(blocks, (ngroups + slots_per_block - 1) / slots_per_block);
-  blocks = std::max(blocks, 1);
-  dim3 grid(blocks, a.max_segments);
-  if (grid.y == 0) return EMBER_OK;
-  const int row_lds = act_lds_bytes(F::QX, a.K);
-  while (MT > 1 && MT * row_lds > kProjLdsBytes) MT >>= 1;
-  if (row_lds > kProjLdsBytes) return EMBER_ERR_SHAPE;
-  const size_t lds = (size_t)MT * row_lds;
-  if (MT == 1)
-    proj_kernel<FMT, RR, 1, GATED><<<grid, 256, lds, st>>>(a, L_log2);
-  else if (MT == 2)
-    proj_kernel<FMT, RR, 2, GATED><<<grid, 256, lds, st>>>(a, L_log2);
-  else
-    proj_kernel<FMT, RR, 4, GATED><<<grid, 256, lds, st>>>(a, L_log2);
+template <int FMT, int MT, bool GATED, int NB, int NT, int WPE>
+int launch_proj_cfg(const ProjArgs& a_in, size_t act_lds, hipStream_t st) {
+  const void* fn = reinterpret_cast<const void*>(&proj_kernel<FMT, MT, GATED, NB, NT, WPE>);
+  static const bool attr_ok =
+      hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kProjLdsBytes) == hipSuccess;
+  if (!attr_ok) return EMBER_ERR_LAUNCH;
+  const ProjArgs& a = a_in;
+  const size_t lds = act_lds;
+  // blocks per CU at this LDS size (cached per size; the launch is sized to one resident wave of blocks)
+  static size_t cached_lds = (size_t)-1;
+  static int cached_bpc = 1;
+  if (cached_lds != lds) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, NT, lds) != hipSuccess) return EMBER_ERR_LAUNCH;
+    cached_bpc = std::max(n, 1);
+    cached_lds = lds;
+  }
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return EMBER_ERR_LAUNCH;
+  static const int bpc_override = [] { const char* e = std::getenv("EMBER_PROJ_BPC"); return e ? atoi(e) : 0; }();
+  const int bpc = bpc_override > 0 ? std::min(bpc_override, cached_bpc) : cached_bpc;
+  const int segs = (a.used ? std::max(a.max_segments, 1) : 0) + (a.s_w0 ? 1 : 0);
+  const int G = std::max(cus * bpc, segs);
+  proj_kernel<FMT, MT, GATED, NB, NT, WPE><<<G, NT, lds, st>>>(a);
   return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
 }
 
+template <int FMT, int MT, bool GATED>
+int launch_proj_mt(const ProjArgs& a, size_t lds, hipStream_t st) {
+  static const int variant = [] { const char* e = std::getenv("EMBER_PROJ_VARIANT"); return e ? atoi(e) : 0; }();
+  switch (variant) {  // tuning override: ring depth / block size / waves per SIMD
+    case 1: return launch_proj_cfg<FMT, MT, GATED, 3, 512, 4>(a, lds, st);
+    case 2: return launch_proj_cfg<FMT, MT, GATED, 3, 256, 3>(a, lds, st);
+    default: return launch_proj_cfg<FMT, MT, GATED, 2, 512, 4>(a, lds, st);
+  }
+}
+
+template <int FMT, bool GATED>
+int launch_proj_fmt(const ProjArgs& a, hipStream_t st) {
+  using F = Fmt<FMT>;
+  int row_lds = 0;
+  if (a.used) row_lds = act_lds_bytes(F::QX, a.K);
+  if (a.s_w0) row_lds = std::max(row_lds, act_lds_bytes(F::QX, a.s_K));
+  if (row_lds == 0) return EMBER_OK;
+  if (row_lds > kProjLdsBytes) return EMBER_ERR_SHAPE;
+  int MT = a.T <= 1 ? 1 : (a.T <= 2 ? 2 : 4);
+  while (MT > 1 && MT * row_lds > kProjLdsBytes) MT >>= 1;
+  const size_t lds = (size_t)MT * row_lds;
+  if (MT == 1) return launch_proj_mt<FMT, 1, GATED>(a, lds, st);
+  if (MT == 2) return launch_proj_mt<FMT, 2, GATED>(a, lds, st);
+  return launch_proj_mt<FMT, 4, GATED>(a, lds, st);
+}
+
 template <bool GATED>
-int launch_proj_gated(const ProjArgs& a, int MT, hipStream_t st) {
+int launch_proj_gated(const ProjArgs& a, hipStream_t st) {
   switch (a.type) {
-    case EMBER_TYPE_F32: return launch_proj_fmt<EMBER_TYPE_F32, 1, GATED>(a, MT, st);
-    case EMBER_TYPE_F16: return launch_proj_fmt<EMBER_TYPE_F16, 1, GATED>(a, MT, st);
-    case EMBER_TYPE_BF16: return launch_proj_fmt<EMBER_TYPE_BF16, 1, GATED>(a, MT, st);
-    case EMBER_TYPE_Q8_0: return launch_proj_fmt<EMBER_TYPE_Q8_0, GATED ? 1 : 2, GATED>(a, MT, st);
-    case EMBER_TYPE_Q4_K: return launch_proj_fmt<EMBER_TYPE_Q4_K, GATED ? 1 : 2, GATED>(a, MT, st);
+    case EMBER_TYPE_F32: return launch_proj_fmt<EMBER_TYPE_F32, GATED>(a, st);
+    case EMBER_TYPE_F16: return launch_proj_fmt<EMBER_TYPE_F16, GATED>(a, st);
+    case EMBER_TYPE_BF16: return launch_proj_fmt<EMBER_TYPE_BF16, GATED>(a, st);
+    case EMBER_TYPE_Q8_0: return launch_proj_fmt<EMBER_TYPE_Q8_0, GATED>(a, st);
+    case EMBER_TYPE_Q4_K: return launch_proj_fmt<EMBER_TYPE_Q4_K, GATED>(a, st);
     default: return EMBER_ERR_TYPE;
   }
 }
 
-bool type_quantizes_activations(int type) { return type == EMBER_TYPE_Q8_0 || type == EMBER_TYPE_Q4_K; }
-
 int launch_projection(const ProjArgs& a, hipStream_t st) {
-  const int MT = a.T <= 1 ? 1 : (a.T <= 2 ? 2 : 4);
-  return a.gated ? launch_proj_gated<true>(a, MT, st) : launch_proj_gated<false>(a, MT, st);
+  return a.gated ? launch_proj_gated<true>(a, st) : launch_proj_gated<false>(a, st);
 }
 
-// Per-32-block int16 quantization of activation rows: q = rint(x / s), s = amax / 32767 (s = 0 for
-// an all-zero block), plus the block's sum of q. One thread per block of 32.
-__global__ void __launch_bounds__(256) quantize_act_kernel(const float* __restrict__ in, int rows, int K,
-                                                           int16_t* __restrict__ q, float* __restrict__ scale,
-                                                           int* __restrict__ sum) {
-  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int nb = K / 32;
-  if (b >= (int64_t)rows * nb) return;
-  const float4* p = reinterpret_cast<const float4*>(in + b * 32);
-  float v[32];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float4 t = p[i];
-    v[4 * i] = t.x;
-    v[4 * i + 1] = t.y;
-    v[4 * i + 2] = t.z;
-    v[4 * i + 3] = t.w;
-  }
-  float amax = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
-  const float s = amax / 32767.0f;
-  const float inv = amax > 0.0f ? 32767.0f / amax : 0.0f;
-  int tot = 0;
-  uint32_t packed[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int a0 = (int)__builtin_rintf(v[2 * i] * inv), a1 = (int)__builtin_rintf(v[2 * i + 1] * inv);
-    const int c0 = max(-32767, min(32767, a0)), c1 = max(-32767, min(32767, a1));
-    tot += c0 + c1;
-    packed[i] = (uint32_t)(uint16_t)c0 | ((uint32_t)(uint16_t)c1 << 16);
-  }
-  u32x4* dst = reinterpret_cast<u32x4*>(q + b * 32);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) dst[i] = u32x4{packed[4 * i], packed[4 * i + 1], packed[4 * i + 2], packed[4 * i + 3]};
-  scale[b] = s;
-  sum[b] = tot;
-}
+int proj_max_row_bytes() { return kProjLdsBytes; }
 
-int launch_quantize_act(const float* in, int rows, int K, const ActQ& a, hipStream_t st) {
-  const int64_t n = (int64_t)rows * (K / 32);
-  if (n <= 0) return EMBER_OK;
-  quantize_act_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(in, rows, K, a.q, a.scale, a.sum);
-  return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
-}
+bool type_quantizes_activations(int type) { return type == EMBER_TYPE_Q8_0 || type == EMBER_TYPE_Q4_K; }
 
 // out[t][o] = sum over j ascending (= experts ascending) of gate[t][j] * y[pos[t*k+j]][o], starting
 // from 0 (utils.cpp:736, 744-747); then (x * scale) + 0 (the IR's affine, graph_ir.cpp:923, 2727)

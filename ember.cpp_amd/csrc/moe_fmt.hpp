@@ -45,27 +45,28 @@ __device__ inline void load16(const uint8_t* p, uint32_t* raw) {
 
 // Activation operands of one chunk for one token.
 struct XF {                 // float activations (F32 / F16 / BF16 weights)
-  float v[64];
+  float v[32];
 };
 
 template <int FMT>
 struct Fmt;
 
-// F32: chunk = 32 floats = 128 B.
+// F32: chunk = 16 floats = 64 B.
 template <>
 struct Fmt<EMBER_TYPE_F32> {
-  static constexpr int CE = 32, NW = 32, NGL = 3;  // activation chunk: 32 floats = 8 granules
+  static constexpr int CE = 16, NW = 16, NGL = 2;  // activation chunk: 16 floats = 4 granules
   static constexpr bool QX = false;
   __host__ __device__ static int64_t row_bytes(int K) { return 4 * (int64_t)K; }
   __device__ static void load(const uint8_t* row, int c, int K, uint32_t* raw) {
     const int n = K - c * CE;  // valid elements (multiple of 4)
 #pragma unroll
-    for (int v = 0; v < 8; ++v) {
-      if (4 * v < n) {
-        load16(row + (size_t)c * 128 + 16 * v, raw + 4 * v);
-      } else {
-        raw[4 * v] = raw[4 * v + 1] = raw[4 * v + 2] = raw[4 * v + 3] = 0u;
-      }
+    for (int v = 0; v < 4; ++v) {  // branch-free: a granule past the row's end reloads granule 0, then zeroes
+      const bool ok = 4 * v < n;
+      const u32x4 q = *reinterpret_cast<const u32x4*>(row + (size_t)c * 64 + 16 * (ok ? v : 0));
+      raw[4 * v] = ok ? q.x : 0u;
+      raw[4 * v + 1] = ok ? q.y : 0u;
+      raw[4 * v + 2] = ok ? q.z : 0u;
+      raw[4 * v + 3] = ok ? q.w : 0u;
     }
   }
   template <int MT>
@@ -74,7 +75,7 @@ struct Fmt<EMBER_TYPE_F32> {
   __device__ static float dot(const uint32_t* raw, const XF& x, int) {
     float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 32; i += 2) {
+    for (int i = 0; i < 16; i += 2) {
       a0 = __builtin_fmaf(as_f32(raw[i]), x.v[i], a0);
       a1 = __builtin_fmaf(as_f32(raw[i + 1]), x.v[i + 1], a1);
     }
@@ -82,21 +83,22 @@ struct Fmt<EMBER_TYPE_F32> {
   }
 };
 
-// BF16 / F16: chunk = 64 halves = 128 B.
+// BF16 / F16: chunk = 32 halves = 64 B.
 template <int FMT>
 struct FmtHalf {
-  static constexpr int CE = 64, NW = 32, NGL = 4;  // activation chunk: 64 floats = 16 granules
+  static constexpr int CE = 32, NW = 16, NGL = 3;  // activation chunk: 32 floats = 8 granules
   static constexpr bool QX = false;
   __host__ __device__ static int64_t row_bytes(int K) { return 2 * (int64_t)K; }
   __device__ static void load(const uint8_t* row, int c, int K, uint32_t* raw) {
     const int n = K - c * CE;  // multiple of 8
 #pragma unroll
-    for (int v = 0; v < 8; ++v) {
-      if (8 * v < n) {
-        load16(row + (size_t)c * 128 + 16 * v, raw + 4 * v);
-      } else {
-        raw[4 * v] = raw[4 * v + 1] = raw[4 * v + 2] = raw[4 * v + 3] = 0u;
-      }
+    for (int v = 0; v < 4; ++v) {  // branch-free: a granule past the row's end reloads granule 0, then zeroes
+      const bool ok = 8 * v < n;
+      const u32x4 q = *reinterpret_cast<const u32x4*>(row + (size_t)c * 64 + 16 * (ok ? v : 0));
+      raw[4 * v] = ok ? q.x : 0u;
+      raw[4 * v + 1] = ok ? q.y : 0u;
+      raw[4 * v + 2] = ok ? q.z : 0u;
+      raw[4 * v + 3] = ok ? q.w : 0u;
     }
   }
   __device__ static float lo(uint32_t w) {
@@ -113,7 +115,7 @@ struct FmtHalf {
   __device__ static float dot(const uint32_t* raw, const XF& x, int) {
     float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) {
+    for (int i = 0; i < 16; ++i) {
       a0 = __builtin_fmaf(lo(raw[i]), x.v[2 * i], a0);
       a1 = __builtin_fmaf(hi(raw[i]), x.v[2 * i + 1], a1);
     }
@@ -327,6 +329,82 @@ __device__ inline void stage_rows(bool qx, const StageSrc& a, const int* rows, i
   }
 }
 
+// Per-32-element-block int16 quantization of one block of activations, the values quantize_act_kernel
+// writes: s = amax / 32767, q = rint(x * (32767 / amax)) clamped to +-32767 (q = 0, s = 0 for an
+// all-zero block), plus the block's sum of q.
+__device__ inline void quant_block32(const float* src, uint32_t* packed, float* scale, int* sum) {
+  float v[32];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float4 t = reinterpret_cast<const float4*>(src)[i];
+    v[4 * i] = t.x;
+    v[4 * i + 1] = t.y;
+    v[4 * i + 2] = t.z;
+    v[4 * i + 3] = t.w;
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  const float inv = amax > 0.0f ? 32767.0f / amax : 0.0f;
+  int tot = 0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int a0 = (int)__builtin_rintf(v[2 * i] * inv), a1 = (int)__builtin_rintf(v[2 * i + 1] * inv);
+    const int c0 = max(-32767, min(32767, a0)), c1 = max(-32767, min(32767, a1));
+    tot += c0 + c1;
+    packed[i] = (uint32_t)(uint16_t)c0 | ((uint32_t)(uint16_t)c1 << 16);
+  }
+  *scale = amax / 32767.0f;
+  *sum = tot;
+}
+
+// Stages f32 activation rows rows[0..nrows) of [*][K] into LDS already quantized (act_lds_bytes
+// layout for the quantizing formats: int16 values in rotated 64-element chunks, then the per-block
+// scales, then the per-block sums). One thread per 32-element block.
+__device__ inline void stage_rows_quant(const float* in, int K, const int* rows, int nrows, uint8_t* lds, int row_lds) {
+  const int nb = K / 32;
+  const int n = nrows * nb;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    const int m = i / nb, b = i - m * nb;
+    uint32_t packed[16];
+    float sc;
+    int sm;
+    quant_block32(in + (size_t)rows[m] * K + (size_t)b * 32, packed, &sc, &sm);
+    uint8_t* row = lds + m * row_lds;
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      *reinterpret_cast<u32x4*>(row + 16 * swz_granule<3>(b >> 1, (b & 1) * 4 + g)) =
+          u32x4{packed[4 * g], packed[4 * g + 1], packed[4 * g + 2], packed[4 * g + 3]};
+    reinterpret_cast<float*>(row + K * 2)[b] = sc;
+    reinterpret_cast<int*>(row + K * 2 + nb * 4)[b] = sm;
+  }
+}
+
+// Stages f32 activation rows rows[0..nrows) of [*][K] into LDS in rotated chunks of 2^NGL granules
+// (float formats). Four granules per thread are loaded before any is stored.
+template <int NGL>
+__device__ inline void stage_rows_f32(const float* in, int K, const int* rows, int nrows, uint8_t* lds, int row_lds) {
+  const int nq = K / 4, n = nrows * nq;
+  const int stride = blockDim.x;
+  for (int base = threadIdx.x; base < n; base += 4 * stride) {
+    u32x4 t[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = min(base + u * stride, n - 1);
+      const int m = i / nq, r = i - m * nq;
+      t[u] = *reinterpret_cast<const u32x4*>(in + (size_t)rows[m] * K + 4 * r);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = base + u * stride;
+      if (i < n) {
+        const int m = i / nq, r = i - m * nq;
+        *reinterpret_cast<u32x4*>(lds + m * row_lds + 16 * swz_granule<NGL>(r >> NGL, r & ((1 << NGL) - 1))) = t[u];
+      }
+    }
+  }
+}
+
 // Activation operands of chunk c (element offset c*CE) from a staged row.
 template <int FMT>
 __device__ inline void lds_xf(const uint8_t* row, int c, int K, XF& x) {
@@ -335,12 +413,13 @@ __device__ inline void lds_xf(const uint8_t* row, int c, int K, XF& x) {
   const int n = K - c * CE;
 #pragma unroll
   for (int v = 0; v < CE / 4; ++v) {
-    const float4 q = (4 * v < n) ? *reinterpret_cast<const float4*>(lds_granule<NGL>(row, c, v))
-                                 : make_float4(0.f, 0.f, 0.f, 0.f);
-    x.v[4 * v] = q.x;
-    x.v[4 * v + 1] = q.y;
-    x.v[4 * v + 2] = q.z;
-    x.v[4 * v + 3] = q.w;
+    // rows are padded to whole 64-element chunks, so the read stays in the row; the tail reads zero
+    const bool ok = 4 * v < n;
+    const float4 q = *reinterpret_cast<const float4*>(lds_granule<NGL>(row, c, v));
+    x.v[4 * v] = ok ? q.x : 0.0f;
+    x.v[4 * v + 1] = ok ? q.y : 0.0f;
+    x.v[4 * v + 2] = ok ? q.z : 0.0f;
+    x.v[4 * v + 3] = ok ? q.w : 0.0f;
   }
 }
 // dot_tokens for the float formats: decode the chunk once per token from the staged f32 rows.
@@ -361,14 +440,40 @@ __device__ void FmtHalf<FMT>::dot_tokens(const uint32_t* raw, const uint8_t* lds
 template <int FMT, int MT>
 __device__ inline void dot_tokens_f(const uint32_t* raw, const uint8_t* lds, int row_lds, int c, int K, int nvalid,
                                     float* out) {
+  constexpr int CE = Fmt<FMT>::CE;
+  constexpr int NGL = Fmt<FMT>::NGL;
+  const int n = K - c * CE;
+  float a0[MT], a1[MT];
 #pragma unroll
-  for (int m = 0; m < MT; ++m) {
-    if (m < nvalid) {
-      XF xv;
-      lds_xf<FMT>(lds + m * row_lds, c, K, xv);
-      out[m] += Fmt<FMT>::dot(raw, xv, c);
+  for (int m = 0; m < MT; ++m) a0[m] = a1[m] = 0.0f;
+#pragma unroll
+  for (int v = 0; v < CE / 4; ++v) {
+    float w[4];
+    if constexpr (FMT == EMBER_TYPE_F32) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) w[i] = as_f32(raw[4 * v + i]);
+    } else {
+      w[0] = Fmt<FMT>::lo(raw[2 * v]);
+      w[1] = Fmt<FMT>::hi(raw[2 * v]);
+      w[2] = Fmt<FMT>::lo(raw[2 * v + 1]);
+      w[3] = Fmt<FMT>::hi(raw[2 * v + 1]);
+    }
+    // rows are padded to whole 64-element chunks, so the read stays in the row; the tail reads zero
+    const bool ok = 4 * v < n;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      if (m < nvalid) {
+        const float4 q = *reinterpret_cast<const float4*>(lds_granule<NGL>(lds + m * row_lds, c, v));
+        a0[m] = __builtin_fmaf(w[0], ok ? q.x : 0.0f, a0[m]);
+        a1[m] = __builtin_fmaf(w[1], ok ? q.y : 0.0f, a1[m]);
+        a0[m] = __builtin_fmaf(w[2], ok ? q.z : 0.0f, a0[m]);
+        a1[m] = __builtin_fmaf(w[3], ok ? q.w : 0.0f, a1[m]);
+      }
     }
   }
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+    if (m < nvalid) out[m] += a0[m] + a1[m];
 }
 
 __device__ inline float swiglu(float g, float u) { return g * (1.0f / (1.0f + expf_glibc(-g))) * u; }

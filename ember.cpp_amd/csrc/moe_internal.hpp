@@ -48,38 +48,38 @@ int launch_route_dispatch(const float* logits, int T, int E, int k, int renorm, 
                           const float* bias, int groups_n, int groups_top, int32_t* idx, float* gates,
                           const DispatchScratch& ds, hipStream_t st);
 
-// Activations quantized to int16 per 32-element block (for Q8_0 / Q4_K weights).
-struct ActQ {
-  int16_t* q;     // [rows][K]
-  float* scale;   // [rows][K/32]
-  int* sum;       // [rows][K/32]
-  int K;
-};
-
 bool type_quantizes_activations(int type);
-int launch_quantize_act(const float* in, int rows, int K, const ActQ& a, hipStream_t st);
+int proj_max_row_bytes();  // LDS bytes one staged activation row of the decode kernel may take
 
-// One projection over a set of token segments: out[p][row] for rows [0, rows) of a
-// [rows][K] matrix per expert (or the single shared matrix).
+// One projection launch over expert segments: out[p][row] for rows [0, rows) of a [rows][K] matrix
+// per segment. Routed segments are the experts used[0..*n_used) with the dispatch-order positions
+// offsets[e]..offsets[e+1); an optional shared-expert segment (s_w0 non-null, same weight type) covers
+// tokens 0..T-1 and is scheduled in the same launch. Activations are f32; the quantizing formats
+// quantize them to int16 per 32-element block while staging them into LDS.
 struct ProjArgs {
-  const void* w0;      // gate (or the only) stack base
-  const void* w1;      // up stack base (gated projections) or null
-  int type;            // ggml type of w0 / w1
-  int rows, K;         // matrix shape per expert
+  int type;               // ggml type of every matrix of the launch
+  bool gated;             // gate/up pair + SwiGLU vs a plain projection
+  // routed segments (used non-null)
+  const void* w0;         // gate (or the only) stack base
+  const void* w1;         // up stack base (gated) or null
+  int rows, K;            // matrix shape per expert
   int64_t expert_stride;  // bytes between consecutive experts' matrices
-  const float* in;     // activations: x [T][K] (gated) or h [npos][K] (down), f32
-  ActQ act;            // the same activations quantized (used when `type` quantizes activations)
-  float* out;          // h [npos][rows] (gated) or y [npos][rows] (down)
-  // Segments: routed (offsets/used/n_used/perm valid, k > 0) or shared (one segment of T tokens).
+  const float* in;        // x [T][K] (gathered through perm) or h [npos][K]
+  float* out;             // h [npos][rows] or y [npos][rows], dispatch order
   const int32_t* offsets;
   const int32_t* used;
   const int32_t* n_used;
   const int32_t* perm;
-  int k;               // slots per token; the input row of sorted position p is perm[p] / k (gated)
+  int k;                  // slots per token; the input row of position p is perm[p] / k when in_by_perm
+  bool in_by_perm;
+  int max_segments;       // upper bound on *n_used
+  // shared expert segment (s_w0 non-null): tokens 0..T-1, input rows t, output rows t
+  const void* s_w0;
+  const void* s_w1;
+  int s_rows, s_K;
+  const float* s_in;
+  float* s_out;
   int T;
-  int max_segments;    // grid.y upper bound on segments
-  bool gated;          // gate/up pair + SwiGLU (input rows gathered through perm) vs plain
-  bool in_by_perm;     // input row of position p is perm[p]/k (x for routed gated); else p
 };
 
 int launch_projection(const ProjArgs& a, hipStream_t st);
