@@ -101,11 +101,11 @@ __device__ inline bool seg_view(const ProjArgs& a, const Dispatch& dp, int b, in
   return true;
 }
 
-// One projection. A block serves a contiguous row range of one segment; each of its waves a
-// contiguous sub-range. L lanes (a power of two <= 64) cover a row, one chunk per lane per step
-// (looping NC rounds when a row has more than L chunks), so a step covers 64 / L rows. The weights of
-// step s + 1 are in flight while step s is computed (two register buffers). MT tokens per pass over
-// the weights; their activation rows are staged in LDS (quantized on the way for Q8_0 / Q4_K).
+// One projection. The blocks of a segment share its rows, interleaved over their waves (see below). L
+// lanes (a power of two <= 64) cover a row, one chunk per lane per step (looping NC rounds when a row
+// has more than L chunks), so a step covers 64 / L rows. Weight loads run through a ring of NB
+// register buffers ahead of the dots. MT tokens per pass over the weights; their activation rows are
+// staged in LDS (quantized on the way for Q8_0 / Q4_K).
 template <int FMT, int MT, bool GATED, int NB, int NT, int WPE>
 __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) proj_kernel(ProjArgs a) {
   using F = Fmt<FMT>;
@@ -115,8 +115,6 @@ __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) 
   Dispatch dp{a.used ? *a.n_used : 0, a.used, a.offsets, a.perm};
   SegView v;
   if (!seg_view<GATED>(a, dp, blockIdx.x, gridDim.x, v)) return;
-  const int rb0 = (int)((int64_t)v.jb * v.rows / v.nb), rb1 = (int)((int64_t)(v.jb + 1) * v.rows / v.nb);
-  const int rw0 = rb0 + wave * (rb1 - rb0) / nwaves, rw1 = rb0 + (wave + 1) * (rb1 - rb0) / nwaves;
   const int K = v.K;
   const int C = (K + F::CE - 1) / F::CE;
   int Lg = 0;
@@ -124,7 +122,14 @@ __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) 
   const int L = 1 << Lg, RPS = 64 >> Lg;
   const int sub = lane >> Lg, rl = lane & (L - 1);
   const int NC = (C + L - 1) / L;
-  const int nsteps = ((rw1 - rw0 + RPS - 1) / RPS) * NC;
+  // Rows are interleaved over the segment's waves: step st of wave w (w-th of the segment's W waves)
+  // covers row group (st / NC) * W + w, so that at any time the segment's waves read adjacent rows
+  // (DRAM pages stay open), rather than each wave streaming its own distant range.
+  const int wseg = v.jb * nwaves + wave, Wseg = v.nb * nwaves;
+  const int gt = (v.rows + RPS - 1) / RPS;
+  const int rbase = wseg * RPS, rstride = Wseg * RPS, rend = v.rows;
+  const int ngroups = wseg < gt ? (gt - wseg + Wseg - 1) / Wseg : 0;
+  const int nsteps = ngroups * NC;
   const int64_t rb = F::row_bytes(K);
   const int row_lds = act_lds_bytes(F::QX, K);
 
@@ -133,7 +138,7 @@ __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) 
   // weights of matrix g (0: gate or the only one, 1: up) for step st; out-of-range (row, chunk) pairs
   // load a valid neighbour, which dot() then ignores
   auto load_step = [&](int st, int g, uint32_t (&buf)[F::NW]) {
-    const int r = min(rw0 + (st / NC) * RPS + sub, rw1 - 1);
+    const int r = max(0, min(rbase + (st / NC) * rstride + sub, rend - 1));
     const int c = min(rl + (st % NC) * L, C - 1);
     F::load((g ? v.W1 : v.W0) + (int64_t)r * rb, c, K, buf);
   };
@@ -146,11 +151,13 @@ __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) 
     const int nvalid = min(MT, v.M - m0);
     uint32_t buf[NB][F::NW];
     // the first weights travel while the activations are staged
+    // loads past the end of the stream are clamped to valid addresses and their dots masked, so that
+    // the ring below is straight-line code (divergent guards make the compiler drain every load)
     auto pre = [&](auto J) {
       constexpr int j = decltype(J)::value;
-      if (j < nloads) load_step(j / G2, j % G2, buf[j]);
+      load_step(j / G2, j % G2, buf[j]);
     };
-    ring_for<NB - 1>(pre);
+    if (nloads > 0) ring_for<NB - 1>(pre);  // wave-uniform: a wave without rows loads nothing
     __syncthreads();  // the previous pass no longer reads the staged rows
     if (threadIdx.x < nvalid) {
       const int p = v.p0 + m0 + threadIdx.x;
@@ -169,23 +176,32 @@ __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) 
 #pragma unroll
       for (int m = 0; m < MT; ++m) acc[g][m] = 0.0f;
 
-    auto dot = [&](int st, const uint32_t (&b)[F::NW], float (&ac)[MT]) {
-      const int r = rw0 + (st / NC) * RPS + sub;
+    auto dot = [&](int q, const uint32_t (&b)[F::NW], float (&ac)[MT]) {
+      const int st = q / G2;
+      const int r = rbase + (st / NC) * rstride + sub;
       const int c = rl + (st % NC) * L;
-      if (c < C && r < rw1) F::template dot_tokens<MT>(b, act_lds, row_lds, c, K, nvalid, ac);
+      const bool ok = q < nloads && c < C && r < rend;
+      float t[MT];
+#pragma unroll
+      for (int m = 0; m < MT; ++m) t[m] = 0.0f;
+      F::template dot_tokens<MT>(b, act_lds, row_lds, min(c, C - 1), K, nvalid, t);
+#pragma unroll
+      for (int m = 0; m < MT; ++m) ac[m] += ok ? t[m] : 0.0f;
     };
     auto finish = [&](int st) {
-      if (st % NC != NC - 1) return;  // the row is complete: reduce over the lane group and write
-      const int r = rw0 + (st / NC) * RPS + sub;
+      if (st >= nsteps || st % NC != NC - 1) return;  // the row is complete: reduce over the lane group, write
+      const int r = rbase + (st / NC) * rstride + sub;
 #pragma unroll
       for (int g = 0; g < G2; ++g)
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
           float t = acc[g][m];
-          for (int off = L >> 1; off >= 1; off >>= 1) t += __shfl_xor(t, off, 64);
+#pragma unroll
+          for (int off = 32; off >= 1; off >>= 1)
+            if (off < L) t += __shfl_xor(t, off, 64);
           acc[g][m] = t;
         }
-      if (rl == 0 && r < rw1) {
+      if (rl == 0 && r < rend) {
 #pragma unroll
         for (int m = 0; m < MT; ++m)
           if (m < nvalid)
@@ -203,11 +219,9 @@ __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) 
     auto slot = [&](int q0, auto J) {
       constexpr int j = decltype(J)::value;
       const int q = q0 + j;
-      if (q < nloads) {
-        if (q + NB - 1 < nloads) load_step((q + NB - 1) / G2, (j + NB - 1) % G2, buf[(j + NB - 1) % NB]);
-        dot(q / G2, buf[j % NB], acc[j % G2]);
-        if (j % G2 == G2 - 1) finish(q / G2);
-      }
+      load_step((q + NB - 1) / G2, (j + NB - 1) % G2, buf[(j + NB - 1) % NB]);
+      dot(q, buf[j % NB], acc[j % G2]);
+      if (j % G2 == G2 - 1) finish(q / G2);
     };
 #pragma unroll 1
     for (int q0 = 0; q0 < nloads; q0 += U) ring_for<U>([&](auto J) { slot(q0, J); });
@@ -245,12 +259,9 @@ int launch_proj_cfg(const ProjArgs& a_in, size_t act_lds, hipStream_t st) {
 
 template <int FMT, int MT, bool GATED>
 int launch_proj_mt(const ProjArgs& a, size_t lds, hipStream_t st) {
-  static const int variant = [] { const char* e = std::getenv("EMBER_PROJ_VARIANT"); return e ? atoi(e) : 0; }();
-  switch (variant) {  // tuning override: ring depth / block size / waves per SIMD
-    case 1: return launch_proj_cfg<FMT, MT, GATED, 3, 512, 4>(a, lds, st);
-    case 2: return launch_proj_cfg<FMT, MT, GATED, 3, 256, 3>(a, lds, st);
-    default: return launch_proj_cfg<FMT, MT, GATED, 2, 512, 4>(a, lds, st);
-  }
+  // two register buffers, 512-thread blocks, four waves per SIMD (measured best of the ring depths
+  // 2-4 and block sizes 256 / 512 on MI355X for the Mixtral / Qwen / DeepSeek layer shapes)
+  return launch_proj_cfg<FMT, MT, GATED, 2, 512, 4>(a, lds, st);
 }
 
 template <int FMT, bool GATED>
