@@ -17,6 +17,9 @@
 // each wave 64x128. Tiles (expert, first token) come from a table the dispatch step writes, so
 // grid.x over-provisions m-tiles and extra blocks exit at once; grid.y covers N. Global loads of the
 // next K tile are issued before the MFMAs of the current one.
+#include <cstdlib>
+#include <type_traits>
+
 #include "moe_internal.hpp"
 
 namespace ember_moe {
@@ -357,6 +360,230 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs g, int NT) 
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Q8_0 grouped GEMM with direct global->LDS tile loads. Tiles of 256 tokens x 256 weight rows x 64 K
+// run through a ring of three LDS stages that global_load_lds fills without passing through
+// registers, so two tiles are in flight while one is multiplied. Waves 0-3 load the activation tile
+// (16-byte granules XOR-swizzled by row, for conflict-free fragment reads), waves 4-7 the weight tile
+// in its Q8_0 bytes: the 68 bytes of a row's K tile as five 16-byte granules, the fifth overlapping
+// (bytes 52..67), so a row occupies 80 bytes of LDS. 512 threads = 8 waves (two per SIMD: one wave's
+// fragment loads and decode overlap the other's MFMAs) in a 2 (M) x 4 (N) arrangement; a wave owns
+// 128 tokens x 64 weight rows (gated: 32 gate + 32 up columns, so SwiGLU pairs meet in one wave) and
+// decodes its own B fragments from the Q8_0 bytes straight into MFMA operands (fp16 d * q, one
+// rounding, as the decoders above).
+typedef __attribute__((address_space(3))) void lds_void_t;
+constexpr int kDmaThreads = 512, kDmaStages = 3;
+constexpr int kDmaRowB = 80;                     // LDS bytes of one weight row's K tile
+constexpr int kDmaA = GBM * GBK * 2;             // activation bytes per stage (32 KiB)
+constexpr int kDmaB = 256 * kDmaRowB;            // weight bytes per stage (20 KiB)
+constexpr int kDmaStage = kDmaA + kDmaB;
+constexpr size_t kDmaLds = (size_t)kDmaStages * kDmaStage;
+constexpr int kDmaInstA = kDmaA / 16 / 64 / 4;   // 16-byte DMA instructions per A-loading wave per tile (8)
+constexpr int kDmaInstB = kDmaB / 16 / 64 / 4;   // ... per B-loading wave (5)
+
+__device__ inline void lds_dma16(const void* g, uint8_t* lds) {
+  __builtin_amdgcn_global_load_lds(g, (lds_void_t*)lds, 16, 0, 0);
+}
+// s_waitcnt vmcnt(n) alone (expcnt and lgkmcnt left at their no-wait maxima)
+template <int N>
+__device__ inline void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <bool GATED>
+__global__ void __launch_bounds__(kDmaThreads) gemm_dma_q8_kernel(GemmArgs g, int NT) {
+  constexpr int BN = GATED ? 128 : 256;
+  extern __shared__ __align__(16) uint8_t dsm[];
+
+  const int xcd = blockIdx.x % 8, jb = blockIdx.x / 8;
+  const int mt = xcd + 8 * (jb / NT), nt = jb % NT;
+  int e = 0, p0 = 0, rows = 0;
+  if (g.tiles) {
+    if (mt >= *g.n_tiles) return;
+    e = g.tiles[2 * mt];
+    const int m0 = g.tiles[2 * mt + 1];
+    p0 = g.offsets[e] + m0;
+    rows = min(GBM, g.offsets[e + 1] - p0);
+  } else {
+    p0 = mt * GBM;
+    if (p0 >= g.T) return;
+    rows = min(GBM, g.T - p0);
+  }
+  const int n0 = nt * BN;
+  const int K = g.K, N = g.N;
+  const int nk = K / GBK;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave & 1, wn = wave >> 1;
+  const bool a_loader = wave < 4;  // wave-uniform
+
+  // DMA sources: instruction i of a loading wave fills 16-byte granules 64 (n_inst * w + i) + lane.
+  // A granule gi: row gi / 8, slot gi % 8 holding K granule slot ^ (row % 8); rows past the tile
+  // repeat its last row. B granule gb: row gb / 5, part gb % 5 = bytes 16 part (parts 0-3) or 52.
+  const uint8_t* src[kDmaInstA];
+  if (a_loader) {
+#pragma unroll
+    for (int i = 0; i < kDmaInstA; ++i) {
+      const int gi = 64 * (kDmaInstA * wave + i) + lane;
+      const int r = gi >> 3, kg = (gi & 7) ^ (r & 7);
+      const int p = p0 + min(r, rows - 1);
+      src[i] = reinterpret_cast<const uint8_t*>(g.A + (size_t)(g.perm ? g.perm[p] / g.k : p) * K + 8 * kg);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kDmaInstA; ++i) {
+      const int gb = 64 * (kDmaInstB * (wave - 4) + min(i, kDmaInstB - 1)) + lane;
+      const int r = gb / 5, part = gb - 5 * r;
+      const int q = GATED ? (r >> 7) : 0;
+      const int n = min(n0 + (GATED ? (r & 127) : r), N - 1);
+      src[i] = static_cast<const uint8_t*>(q ? g.W1 : g.W0) + (int64_t)e * g.expert_stride + (int64_t)n * g.row_bytes +
+               (part < 4 ? 16 * part : 52);
+    }
+  }
+  // DMA of tile kt (clamped: tiles past the end reload the last, never multiplied), instructions
+  // [i0, i1) of this wave's share, so that the issue can be spread over the MFMAs of a tile
+  auto issue = [&](int kt, int i0, int i1) {
+    const int kc = min(kt, nk - 1);
+    uint8_t* st = dsm + (kt % kDmaStages) * kDmaStage;
+    if (a_loader) {
+#pragma unroll
+      for (int i = 0; i < kDmaInstA; ++i)
+        if (i >= i0 && i < i1) lds_dma16(src[i] + (size_t)kc * GBK * 2, st + 1024 * (kDmaInstA * wave + i));
+    } else {
+#pragma unroll
+      for (int i = 0; i < kDmaInstB; ++i)
+        if (i >= 2 * i0 / 3 && i < (i1 == kDmaInstA ? kDmaInstB : 2 * i1 / 3))
+          lds_dma16(src[i] + (size_t)kc * 68, st + kDmaA + 1024 * (kDmaInstB * (wave - 4) + i));
+    }
+  };
+
+  floatx16 acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int jn = 0; jn < 2; ++jn)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][jn][r] = 0.0f;
+
+  // B tile row of this lane in subtile jn
+  auto brow_of = [&](int jn) {
+    if constexpr (GATED) return jn * 128 + wn * 32 + (lane & 31);
+    return wn * 64 + 32 * jn + (lane & 31);
+  };
+  const int h = lane >> 5;
+  const half2_t off = h2(0xe480e480u);  // -1152 = -(1024 + 128) in each half
+
+  // Fragments of K step ks (compile time) of the tile in stage `st`. Lane's 8 elements: K granule
+  // gk = 2 ks + h of the 64 = Q8_0 block b = ks / 2, bytes X + 8 h .. + 8 of the row's 68 with
+  // X = 34 b + 2 + 16 (ks % 2); for b = 1 those are dword aligned and, past byte 52, read from the
+  // overlapping fifth granule (LDS byte = global byte + 12); for b = 0 they sit two bytes past a
+  // dword and are funnel-shifted out of three dwords.
+  struct Frags {
+    half8 a[4], b[2];
+  };
+  auto load_frags = [&](const uint8_t* st, auto KS, Frags& f) {
+    constexpr int ks = decltype(KS)::value;
+    constexpr int b = ks >> 1;
+    constexpr int X = 34 * b + 2 + 16 * (ks & 1);
+    const int gk = 2 * ks + h;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = wm * 128 + 32 * i + (lane & 31);
+      f.a[i] = *reinterpret_cast<const half8*>(st + 16 * (8 * r + (gk ^ (r & 7))));
+    }
+    const uint8_t* Bs = st + kDmaA;
+#pragma unroll
+    for (int jn = 0; jn < 2; ++jn) {
+      const uint8_t* row = Bs + kDmaRowB * brow_of(jn);
+      const uint32_t dbits = b ? (*reinterpret_cast<const uint32_t*>(row + 32) >> 16)
+                               : (*reinterpret_cast<const uint32_t*>(row) & 0xffffu);
+      const half2_t d = h2(dbits * 0x10001u);
+      uint32_t w0, w1;
+      if constexpr (b == 0) {
+        const uint32_t* qw = reinterpret_cast<const uint32_t*>(row + (X & ~3) + 8 * h);
+        w0 = __builtin_amdgcn_alignbit(qw[1], qw[0], 16);
+        w1 = __builtin_amdgcn_alignbit(qw[2], qw[1], 16);
+      } else {
+        const int byte = X + 8 * h;
+        const uint32_t* qw = reinterpret_cast<const uint32_t*>(row + (byte + 8 > 64 ? byte + 12 : byte));
+        w0 = qw[0];
+        w1 = qw[1];
+      }
+      const uint32_t q0 = w0 ^ 0x80808080u, q1 = w1 ^ 0x80808080u;
+      const uint32_t o0 = u32((magic_pair(q0, 0) + off) * d), o1 = u32((magic_pair(q0, 1) + off) * d);
+      const uint32_t o2 = u32((magic_pair(q1, 0) + off) * d), o3 = u32((magic_pair(q1, 1) + off) * d);
+      f.b[jn] = __builtin_bit_cast(half8, u32x4{o0, o1, o2, o3});
+    }
+  };
+  auto mfmas = [&](const Frags& f) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int jn = 0; jn < 2; ++jn)
+        acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[i], f.b[jn], acc[i][jn], 0, 0, 0);
+  };
+  // the MFMAs of tile kt with the DMA of tile kt + 2 spread between its K steps (a VMEM instruction
+  // that stalls on a full memory queue then holds up this wave while the matrix core still has work)
+  auto compute = [&](int kt) {
+    const uint8_t* st = dsm + (kt % kDmaStages) * kDmaStage;
+    Frags f0, f1;
+    load_frags(st, std::integral_constant<int, 0>{}, f0);
+    issue(kt + 2, 0, 2);
+    load_frags(st, std::integral_constant<int, 1>{}, f1);
+    mfmas(f0);
+    issue(kt + 2, 2, 4);
+    load_frags(st, std::integral_constant<int, 2>{}, f0);
+    mfmas(f1);
+    issue(kt + 2, 4, 6);
+    load_frags(st, std::integral_constant<int, 3>{}, f1);
+    mfmas(f0);
+    issue(kt + 2, 6, kDmaInstA);
+    mfmas(f1);
+  };
+
+  static_assert(kDmaStages == 3, "the waits below assume one tile in flight beyond the current one");
+  issue(0, 0, kDmaInstA);
+  issue(1, 0, kDmaInstA);
+  for (int kt = 0; kt < nk; ++kt) {
+    // this wave's part of tile kt has landed (tile kt + 1 may still be in flight) ...
+    if (a_loader)
+      wait_vmcnt<kDmaInstA>();
+    else
+      wait_vmcnt<kDmaInstB>();
+    // ... and every wave's part; stage (kt + 2) % 3 is free again (its reads were consumed by the MFMAs
+    // of tile kt - 1 before each wave got here). A bare barrier: __syncthreads()'s release fence would
+    // wait for the DMA of tile kt + 1 as well. The empty asm statements keep the compiler from moving
+    // LDS accesses across it.
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    compute(kt);
+  }
+  wait_vmcnt<0>();  // no DMA may still target LDS when the block exits
+
+  // ---- epilogue: lane holds column (lane & 31) of each 32x32 subtile, rows 8*ii + 4*(lane>>5) + jj
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int jn = 0; jn < (GATED ? 1 : 2); ++jn) {
+      const int n = n0 + (GATED ? wn * 32 : wn * 64 + 32 * jn) + (lane & 31);
+      if (n >= N) continue;
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int m = wm * 128 + 32 * i + 8 * ii + 4 * (lane >> 5) + jj;
+          if (m >= rows) continue;
+          const size_t o = (size_t)(p0 + m) * N + n;
+          if constexpr (GATED) {
+            g.out_h[o] = (_Float16)swiglu_g(acc[i][0][4 * ii + jj], acc[i][1][4 * ii + jj]);
+          } else {
+            g.out_y[o] = acc[i][jn][4 * ii + jj];
+          }
+        }
+    }
+}
+
 // Skinny grouped GEMM for segments of a few dozen tokens (decode batches of 8+ tokens, short prefills):
 // 64-token tiles, 256 threads. Each wave owns 32 output columns (gate/up: 32 gate + 32 up rows; down:
 // 64 rows) and decodes its own weight rows straight into MFMA B operands: lane (n = lane % 32,
@@ -517,6 +744,15 @@ int launch_gemm_fmt(const GemmArgs& g, int max_mtiles, hipStream_t st) {
   const int mgroups = (max_mtiles + 7) / 8;
   const unsigned blocks = (unsigned)(8 * mgroups * NT);
   if (max_mtiles == 0 || NT == 0) return EMBER_OK;
+  static const bool dma_off = [] { const char* v = std::getenv("EMBER_GEMM_DMA"); return v && atoi(v) == 0; }();
+  if (FMT == EMBER_TYPE_Q8_0 && !dma_off) {
+    static const bool dma_ok =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma_q8_kernel<GATED>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDmaLds) == hipSuccess;
+    if (!dma_ok) return EMBER_ERR_LAUNCH;
+    gemm_dma_q8_kernel<GATED><<<blocks, kDmaThreads, kDmaLds, st>>>(g, NT);
+    return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
+  }
   gemm_kernel<FMT, GATED><<<blocks, kGemmThreads, kGemmLds, st>>>(g, NT);
   return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
 }
