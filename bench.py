@@ -7,7 +7,9 @@ One step = one ember_moe_ffn call over one batch of T tokens resident in HBM (th
 --tokens, default the config's first = decode). Prints ONE JSON line. Besides the contract fields it
 carries:
   roofline      the dominant kernel (gate/up + SwiGLU, HBM-bound): algorithmic bytes per launch over
-                its average duration from HIP events recorded around it on the launch stream
+                its average duration, timed with HIP events that the launch records in the kernel's
+                own dispatch packet on the launch stream; `traffic` is the kernel's HBM bytes per launch from the
+                committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary of the same workload (profiles/)
   cpu_baseline  the reference's CPU MoE path (oracle/_ref, compiled from the reference's own sources
                 when present; else the oracle's restatement) on the box's host cores, on a bounded
                 token sample of the same layer
@@ -139,12 +141,31 @@ def time_layer(em, dl, x, T, steps, warmup):
     except Exception as exc:  # the eager number stands alone
         log(f"[bench] graph capture skipped: {exc}")
 
+    # per-phase times; on the decode path the expert phases are the kernels' own durations (events in
+    # their dispatch packets), i.e. what rocprofv3 --kernel-trace reports for them
     phases = {p: 0.0 for p in em.PHASES}
     n = max(3, min(steps, 20))
     for _ in range(n):
         for p, v in em.moe_ffn_timed(dl.desc, x, T, out, scratch).items():
             phases[p] += v / n
     return eager_ms, graph_ms, phases, out
+
+
+def profiled_traffic(config, T):
+    """HBM bytes per launch of the gate/up kernel, from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    summary of this workload (profiles/*.md, line 'bench-traffic: <config> T=<T> gate_up <bytes>'), or
+    None when no summary covers it."""
+    d = os.path.join(ROOT, "profiles")
+    if not os.path.isdir(d):
+        return None
+    key = f"bench-traffic: {config} T={T} gate_up "
+    for name in sorted(os.listdir(d)):
+        if name.endswith(".md"):
+            with open(os.path.join(d, name)) as f:
+                for ln in f:
+                    if ln.startswith(key):
+                        return float(ln[len(key):].split()[0])
+    return None
 
 
 def cpu_baseline(hl, x_host, T_headline, max_seconds=20.0):
@@ -266,14 +287,14 @@ def main():
                    "mode": "hipgraph" if h["graph_us"] is not None and h["graph_us"] <= h["eager_us"] else "eager"},
         "roofline": {"kernel": f"gate/up + SwiGLU expert kernel ({em.TYPE_NAMES[spec.wtype]})", "bound": "hbm",
                      "achieved": h["gate_up_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": h["gate_up_gbs"] / HBM_PEAK_GBS, "traffic": None,
+                     "frac": h["gate_up_gbs"] / HBM_PEAK_GBS, "traffic": profiled_traffic(args.config, args.tokens),
                      "bytes_per_launch": gu_bytes, "avg_launch_us": h["gate_up_us"]},
         "layer_hbm_frac": h["layer_hbm_frac"],
         "sweep": [results[T] for T in sweep_T],
     }
     if not args.no_cpu:
         try:
-            line["cpu_baseline"] = cpu_baseline(hl, em.make_input(spec, 64), args.tokens)
+            line["cpu_baseline"] = cpu_baseline(hl, em.make_input(spec, 1024), args.tokens, max_seconds=12.0)
             line["cpu_baseline"]["host_cpu"] = _cpu_model()
         except Exception as exc:
             line["cpu_baseline"] = {"value": None, "error": str(exc)}

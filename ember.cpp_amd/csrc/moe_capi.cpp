@@ -196,7 +196,7 @@ inline void mark(hipEvent_t* ev, int i, hipStream_t st) {
 }
 
 int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* scratch, size_t scratch_bytes,
-            hipStream_t st, hipEvent_t* ev) {
+            hipStream_t st, hipEvent_t* ev, hipEvent_t* kev = nullptr, bool* kev_used = nullptr) {
   int s = validate(w);
   if (s) return s;
   if (T < 0) return EMBER_ERR_SHAPE;
@@ -309,6 +309,11 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
       a.s_in = x;
       a.s_out = hs;
     }
+    if (kev) {  // per-dispatch timing events of the two expert launches (ember_moe_ffn_timed)
+      a.ev_start = kev[0];
+      a.ev_stop = kev[1];
+      *kev_used = true;
+    }
     if ((s = launch_projection(a, st))) return s;
     mark(ev, 4, st);
     a.type = w->down_type;
@@ -328,6 +333,10 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
       a.s_K = w->d_ff_shared;
       a.s_in = hs;
       a.s_out = ys;
+    }
+    if (kev) {
+      a.ev_start = kev[2];
+      a.ev_stop = kev[3];
     }
     if ((s = launch_projection(a, st))) return s;
     mark(ev, 5, st);
@@ -394,16 +403,24 @@ int ember_moe_ffn(const ember_moe_layer* w, const float* x, int T, float* out, v
 int ember_moe_ffn_timed(const ember_moe_layer* w, const float* x, int T, float* out, void* scratch,
                         size_t scratch_bytes, hipStream_t st, float* phase_ms) {
   if (!phase_ms) return EMBER_ERR_NULL;
-  hipEvent_t ev[8];
-  for (int i = 0; i < 8; ++i)
+  hipEvent_t ev[12];  // 8 phase boundaries + start / stop of the gate/up and down dispatches
+  for (int i = 0; i < 12; ++i)
     if (hipEventCreate(&ev[i]) != hipSuccess) return EMBER_ERR_LAUNCH;
-  int s = run_ffn(w, x, T, out, scratch, scratch_bytes, st, ev);
+  // The dispatch events are recorded only by the decode path's expert launches; then they replace the
+  // event-to-event spans of those two phases (unrecorded events are never queried: a failed query
+  // would stay behind as HIP's last error).
+  bool kev_used = false;
+  int s = run_ffn(w, x, T, out, scratch, scratch_bytes, st, ev, ev + 8, &kev_used);
   if (s == EMBER_OK && T > 0) {
     if (hipEventSynchronize(ev[7]) != hipSuccess) s = EMBER_ERR_LAUNCH;
     for (int i = 0; i < EMBER_MOE_NPHASES && s == EMBER_OK; ++i)
       if (hipEventElapsedTime(&phase_ms[i], ev[i], ev[i + 1]) != hipSuccess) s = EMBER_ERR_LAUNCH;
+    if (s == EMBER_OK && kev_used &&
+        (hipEventElapsedTime(&phase_ms[3], ev[8], ev[9]) != hipSuccess ||
+         hipEventElapsedTime(&phase_ms[4], ev[10], ev[11]) != hipSuccess))
+      s = EMBER_ERR_LAUNCH;
   }
-  for (int i = 0; i < 8; ++i) hipEventDestroy(ev[i]);
+  for (int i = 0; i < 12; ++i) hipEventDestroy(ev[i]);
   return s;
 }
 

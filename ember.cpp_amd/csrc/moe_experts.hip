@@ -22,6 +22,8 @@
 #include <cstdlib>
 #include <type_traits>
 
+#include <hip/hip_ext.h>
+
 #include "moe_fmt.hpp"
 
 namespace ember_moe {
@@ -253,7 +255,12 @@ int launch_proj_cfg(const ProjArgs& a_in, size_t act_lds, hipStream_t st) {
   const int bpc = bpc_override > 0 ? std::min(bpc_override, cached_bpc) : cached_bpc;
   const int segs = (a.used ? std::max(a.max_segments, 1) : 0) + (a.s_w0 ? 1 : 0);
   const int G = std::max(cus * bpc, segs);
-  proj_kernel<FMT, MT, GATED, NB, NT, WPE><<<G, NT, lds, st>>>(a);
+  if (a.ev_start) {
+    hipExtLaunchKernelGGL(proj_kernel<FMT, MT, GATED, NB, NT, WPE>, dim3(G), dim3(NT), lds, st, a.ev_start, a.ev_stop,
+                          0, a);
+  } else {
+    proj_kernel<FMT, MT, GATED, NB, NT, WPE><<<G, NT, lds, st>>>(a);
+  }
   return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
 }
 

@@ -80,6 +80,8 @@ struct ProjArgs {
   const float* s_in;
   float* s_out;
   int T;
+  // host side only: when set, the launch records these events in its dispatch packet (kernel timing)
+  hipEvent_t ev_start, ev_stop;
 };
 
 int launch_projection(const ProjArgs& a, hipStream_t st);

@@ -68,7 +68,8 @@ int ember_moe_ffn(const ember_moe_layer* w, const float* x, int T, float* out, v
  * brackets each op with CUDA events). Records HIP events between the launches on `stream`, waits for
  * the last one (this call synchronises the host; it is a profiling entry, not for graph capture) and
  * writes the elapsed milliseconds of the EMBER_MOE_NPHASES phases: router logits, routing, dispatch,
- * gate/up + SwiGLU, down, shared expert, combine. */
+ * gate/up + SwiGLU, down, shared expert, combine. The gate/up and down phases of the decode path are
+ * the kernels' own durations (events attached to their dispatch packets), not event-to-event spans. */
 #define EMBER_MOE_NPHASES 7
 int ember_moe_ffn_timed(const ember_moe_layer* w, const float* x, int T, float* out, void* scratch,
                         size_t scratch_bytes, hipStream_t stream, float* phase_ms);
