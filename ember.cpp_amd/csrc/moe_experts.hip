@@ -43,8 +43,22 @@ __device__ inline void ring_for(Fn&& f) {
   ring_for_impl<N>(f, std::make_integer_sequence<int, N>{});
 }
 
-// Which segment block b of G serves, and its share of that segment's rows. Routed segments get blocks
-// in proportion to their rows (the shared segment, when present, gets the rest), at least one each.
+// Which segment block b of G serves, and its share of that segment's rows. Blocks go to segments in
+// proportion to their work, rows x (passes over the weights + kTokW / kPassW per extra token of a pass):
+// a segment's weight bytes set its streaming time and its tokens its dot-product time (on the
+// decode path a segment with four tokens costs well over one with a single token). Every segment gets
+// at least one block. Each wave computes the split itself (a prefix sum over the segments with
+// shuffles), so blocks need no coordination.
+constexpr int kPassW = 2, kTokW = 1;
+
+// The dispatch order a launch schedules from.
+struct Dispatch {
+  int n_used;
+  const int32_t* used;
+  const int32_t* offsets;
+  const int32_t* perm;
+};
+
 struct SegView {
   const uint8_t* W0;
   const uint8_t* W1;
@@ -55,30 +69,76 @@ struct SegView {
   int jb, nb;  // block index within the segment, blocks of the segment
 };
 
-// The dispatch order a launch schedules from (global arrays, or LDS copies after in-block routing).
-struct Dispatch {
-  int n_used;
-  const int32_t* used;
-  const int32_t* offsets;
-  const int32_t* perm;
-};
+__device__ inline float seg_work(int rows, int M, int MT) {
+  const int passes = (M + MT - 1) / MT;
+  return (float)rows * (float)(kPassW * passes + kTokW * (M - passes));
+}
 
-template <bool GATED>
+// inclusive prefix sum over the wave's lanes (every wave computes it identically)
+__device__ inline float wave_incl_scan(float v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const float y = __shfl_up(v, off, 64);
+    if (lane >= off) v += y;
+  }
+  return v;
+}
+__device__ inline int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+template <bool GATED, int MT>
 __device__ inline bool seg_view(const ProjArgs& a, const Dispatch& dp, int b, int G, SegView& v) {
   const int nseg = a.used ? dp.n_used : 0;
-  const int64_t r_rows = (int64_t)nseg * a.rows;
-  const int64_t s_rows = a.s_w0 ? a.s_rows : 0;
-  if (r_rows + s_rows == 0) return false;
+  const int lane = threadIdx.x & 63;
+  // routed work: total, then this block's segment from the prefix sums
+  float w_routed = 0.0f;
+  for (int s0 = 0; s0 < nseg; s0 += 64) {
+    const int s = s0 + lane;
+    float w = 0.0f;
+    if (s < nseg) {
+      const int e = dp.used[s];
+      w = seg_work(a.rows, dp.offsets[e + 1] - dp.offsets[e], MT);
+    }
+    w_routed += __shfl(wave_incl_scan(w), 63, 64);
+  }
+  const float w_shared = a.s_w0 ? seg_work(a.s_rows, a.T, MT) : 0.0f;
+  if (w_routed + w_shared == 0.0f) return false;
   int Gr = 0;
-  if (nseg > 0) Gr = s_rows ? (int)max((int64_t)nseg, min((int64_t)G - 1, G * r_rows / (r_rows + s_rows))) : G;
+  if (nseg > 0) Gr = w_shared ? uniform(max(nseg, min(G - 1, (int)(G * (w_routed / (w_routed + w_shared)))))) : G;
   if (b < Gr) {
-    const int s = (int)((((int64_t)b + 1) * nseg - 1) / Gr);
-    const int bs = (int)(((int64_t)s * Gr) / nseg), be = (int)(((int64_t)(s + 1) * Gr) / nseg);
+    // block start of segment s: s + floor((Gr - nseg) * W(<s) / W); the block's segment is the one
+    // whose [start, next start) holds b
+    const float spare = (float)(Gr - nseg);
+    int seg = 0, bs = 0, be = Gr;
+    float carry = 0.0f;
+    for (int s0 = 0; s0 < nseg; s0 += 64) {
+      const int s = s0 + lane;
+      float w = 0.0f;
+      if (s < nseg) {
+        const int e = dp.used[s];
+        w = seg_work(a.rows, dp.offsets[e + 1] - dp.offsets[e], MT);
+      }
+      const float incl = carry + wave_incl_scan(w);
+      const float excl = incl - w;
+      const int start = s + min(Gr - nseg, (int)(spare * (excl / w_routed)));
+      const int next = s + 1 + min(Gr - nseg, (int)(spare * (incl / w_routed)));
+      const uint64_t m = __ballot(s < nseg && start <= b && b < next);
+      if (m) {
+        const int src = __builtin_ctzll(m);
+        seg = __shfl(s, src, 64);
+        bs = __shfl(start, src, 64);
+        be = __shfl(next, src, 64);
+      }
+      carry = __shfl(incl, 63, 64);
+    }
+    seg = uniform(seg);
+    bs = uniform(bs);
+    be = uniform(be);
     v.jb = b - bs;
     v.nb = be - bs;
-    const int e = dp.used[s];
-    v.p0 = dp.offsets[e];
-    v.M = dp.offsets[e + 1] - v.p0;
+    const int e = uniform(dp.used[seg]);
+    v.p0 = uniform(dp.offsets[e]);
+    v.M = uniform(dp.offsets[e + 1]) - v.p0;
     v.W0 = static_cast<const uint8_t*>(a.w0) + (int64_t)e * a.expert_stride;
     v.W1 = GATED ? static_cast<const uint8_t*>(a.w1) + (int64_t)e * a.expert_stride : v.W0;
     v.rows = a.rows;
@@ -87,7 +147,7 @@ __device__ inline bool seg_view(const ProjArgs& a, const Dispatch& dp, int b, in
     v.out = a.out;
     v.by_perm = a.in_by_perm;
   } else {
-    if (!s_rows) return false;
+    if (w_shared == 0.0f) return false;
     v.jb = b - Gr;
     v.nb = G - Gr;
     v.p0 = 0;
@@ -116,7 +176,7 @@ __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = NT / 64;
   Dispatch dp{a.used ? *a.n_used : 0, a.used, a.offsets, a.perm};
   SegView v;
-  if (!seg_view<GATED>(a, dp, blockIdx.x, gridDim.x, v)) return;
+  if (!seg_view<GATED, MT>(a, dp, blockIdx.x, gridDim.x, v)) return;
   const int K = v.K;
   const int C = (K + F::CE - 1) / F::CE;
   int Lg = 0;
@@ -279,7 +339,8 @@ int launch_proj_fmt(const ProjArgs& a, hipStream_t st) {
   if (a.s_w0) row_lds = std::max(row_lds, act_lds_bytes(F::QX, a.s_K));
   if (row_lds == 0) return EMBER_OK;
   if (row_lds > kProjLdsBytes) return EMBER_ERR_SHAPE;
-  int MT = a.T <= 1 ? 1 : (a.T <= 2 ? 2 : 4);
+  // tokens per pass: up to 2 for gate/up (its 4-token variant runs out of registers), up to 4 for down
+  int MT = a.T <= 1 ? 1 : (a.T <= 2 || GATED ? 2 : 4);
   while (MT > 1 && MT * row_lds > kProjLdsBytes) MT >>= 1;
   const size_t lds = (size_t)MT * row_lds;
   if (MT == 1) return launch_proj_mt<FMT, 1, GATED>(a, lds, st);
