@@ -127,7 +127,8 @@ Layout layout(const ember_moe_layer* w, int T) {
   l.perm = o; o = align_up(o + slots * 4);
   l.r = route_layout(T, w->E, w->k, o); o = l.r.end;
   l.h = o; o = align_up(o + slots * w->d_ff * 4);
-  l.y = o; o = align_up(o + slots * w->d * 4);
+  // y holds kMaxKSplit partial sums per row when the skinny path splits the down projection's K
+  l.y = o; o = align_up(o + slots * w->d * 4 * kMaxKSplit);
   l.hs = o; o = align_up(o + (size_t)T * w->d_ff_shared * 4);
   l.ys = o; o = align_up(o + (w->d_ff_shared > 0 ? (size_t)T * w->d * 4 : 0));
   l.mode = path_mode(w->gate_type, w->d, w->down_type, w->d_ff, (double)T * w->k / w->E);
@@ -216,6 +217,7 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
   const DispatchScratch ds = dispatch_scratch(scratch, l.r, offsets, perm);
   float* h = at<float>(scratch, l.h);
   float* y = at<float>(scratch, l.y);
+  int ksplit = 1;  // partial sums per y row (K split of the down projection)
 
   const int groups_n = std::max(w->groups_n, 1), groups_top = std::max(w->groups_top, 1);
   const int renorm = w->renorm ? 1 : 0, routed = is_routed(w) ? 1 : 0;
@@ -279,6 +281,10 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     g.K = d_ff;
     g.out_h = nullptr;
     g.out_y = y;
+    if (skinny) {
+      g.ksplit = ksplit = gemm_skinny_ksplit(g.type, mt, d, d_ff);
+      g.part_stride = (int64_t)T * k * d;
+    }
     if ((s = gemm(g, false, mt))) return s;
     mark(ev, 5, st);
   } else {
@@ -389,7 +395,8 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     if ((s = launch_projection(b, st))) return s;
   }
   mark(ev, 6, st);
-  s = launch_combine(y, gates, ds.pos, ys, w->out_scale == 0.0f ? 1.0f : w->out_scale, T, k, d, out, st);
+  s = launch_combine(y, ksplit, (int64_t)T * k * d, gates, ds.pos, ys, w->out_scale == 0.0f ? 1.0f : w->out_scale, T,
+                     k, d, out, st);
   mark(ev, 7, st);
   return s;
 }

@@ -370,9 +370,15 @@ bool type_quantizes_activations(int type) { return type == EMBER_TYPE_Q8_0 || ty
 
 // out[t][o] = sum over j ascending (= experts ascending) of gate[t][j] * y[pos[t*k+j]][o], starting
 // from 0 (utils.cpp:736, 744-747); then (x * scale) + 0 (the IR's affine, graph_ir.cpp:923, 2727)
-// and + the shared expert's row (graph_ir.cpp:926-928). One thread per output element.
-__global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ y, const float* __restrict__ gates,
-                                                      const int32_t* __restrict__ pos,
+// and + the shared expert's row (graph_ir.cpp:926-928). A y row given as nparts K-split partial sums
+// is their sum in ascending part order. One thread per output element.
+__device__ inline float y_at(const float* __restrict__ y, int nparts, int64_t part_stride, size_t i) {
+  float v = y[i];
+  for (int s = 1; s < nparts; ++s) v = v + y[s * part_stride + i];
+  return v;
+}
+__global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ y, int nparts, int64_t part_stride,
+                                                      const float* __restrict__ gates, const int32_t* __restrict__ pos,
                                                       const float* __restrict__ y_shared, float scale, int k, int d,
                                                       float* __restrict__ out) {
   const int t = blockIdx.y;
@@ -382,7 +388,7 @@ __global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ 
   for (int j = 0; j < k; ++j) {
     const int p = pos[(size_t)t * k + j];
     const float g = gates[(size_t)t * k + j];
-    if (p >= 0) acc = acc + g * y[(size_t)p * d + o];
+    if (p >= 0) acc = acc + g * y_at(y, nparts, part_stride, (size_t)p * d + o);
   }
   if (scale != 1.0f) acc = acc * scale + 0.0f;
   if (y_shared) acc = acc + y_shared[(size_t)t * d + o];
@@ -390,8 +396,8 @@ __global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ 
 }
 
 // The same with four consecutive outputs per thread (d % 4 == 0): 16-byte loads of y rows.
-__global__ void __launch_bounds__(256) combine4_kernel(const float* __restrict__ y, const float* __restrict__ gates,
-                                                       const int32_t* __restrict__ pos,
+__global__ void __launch_bounds__(256) combine4_kernel(const float* __restrict__ y, int nparts, int64_t part_stride,
+                                                       const float* __restrict__ gates, const int32_t* __restrict__ pos,
                                                        const float* __restrict__ y_shared, float scale, int k, int d,
                                                        float* __restrict__ out) {
   const int t = blockIdx.y;
@@ -402,7 +408,14 @@ __global__ void __launch_bounds__(256) combine4_kernel(const float* __restrict__
     const int p = pos[(size_t)t * k + j];
     const float g = gates[(size_t)t * k + j];
     if (p >= 0) {
-      const float4 v = *reinterpret_cast<const float4*>(y + (size_t)p * d + o);
+      float4 v = *reinterpret_cast<const float4*>(y + (size_t)p * d + o);
+      for (int s = 1; s < nparts; ++s) {
+        const float4 w = *reinterpret_cast<const float4*>(y + s * part_stride + (size_t)p * d + o);
+        v.x = v.x + w.x;
+        v.y = v.y + w.y;
+        v.z = v.z + w.z;
+        v.w = v.w + w.w;
+      }
       a0 = a0 + g * v.x;
       a1 = a1 + g * v.y;
       a2 = a2 + g * v.z;
@@ -425,16 +438,16 @@ __global__ void __launch_bounds__(256) combine4_kernel(const float* __restrict__
   *reinterpret_cast<float4*>(out + (size_t)t * d + o) = make_float4(a0, a1, a2, a3);
 }
 
-int launch_combine(const float* y, const float* gates, const int32_t* pos, const float* y_shared, float scale, int T,
-                   int k, int d, float* out, hipStream_t st) {
+int launch_combine(const float* y, int nparts, int64_t part_stride, const float* gates, const int32_t* pos,
+                   const float* y_shared, float scale, int T, int k, int d, float* out, hipStream_t st) {
   if (T <= 0) return EMBER_OK;
   if (d % 4 == 0) {
     dim3 grid((d / 4 + 255) / 256, T);
-    combine4_kernel<<<grid, 256, 0, st>>>(y, gates, pos, y_shared, scale, k, d, out);
+    combine4_kernel<<<grid, 256, 0, st>>>(y, nparts, part_stride, gates, pos, y_shared, scale, k, d, out);
     return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
   }
   dim3 grid((d + 255) / 256, T);
-  combine_kernel<<<grid, 256, 0, st>>>(y, gates, pos, y_shared, scale, k, d, out);
+  combine_kernel<<<grid, 256, 0, st>>>(y, nparts, part_stride, gates, pos, y_shared, scale, k, d, out);
   return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
 }
 

@@ -584,6 +584,188 @@ __global__ void __launch_bounds__(kDmaThreads) gemm_dma_q8_kernel(GemmArgs g, in
     }
 }
 
+// The same with 64-token tiles, for segments of a few to a few dozen tokens (decode batches, short
+// prefills), where the layer is bound by streaming the weights: 256 threads = 4 waves side by side
+// in N (each 64 tokens x 64 weight rows, gated: 32 gate + 32 up columns), a five-stage LDS ring (four
+// tiles in flight), every wave loading 2 activation and 5 weight granules per tile.
+constexpr int kD64Threads = 256, kD64Stages = 5, kD64BM = 64;
+constexpr int kD64A = kD64BM * GBK * 2;            // 8 KiB
+constexpr int kD64Stage = kD64A + kDmaB;          // + 20 KiB of Q8_0 rows
+constexpr size_t kD64Lds = (size_t)kD64Stages * kD64Stage;
+constexpr int kD64InstA = kD64A / 16 / 64 / 4;     // 2 per wave
+constexpr int kD64InstB = kDmaB / 16 / 64 / 4;     // 5 per wave
+
+template <bool GATED>
+__global__ void __launch_bounds__(kD64Threads) gemm_dma64_q8_kernel(GemmArgs g, int NT) {
+  constexpr int BN = GATED ? 128 : 256;
+  extern __shared__ __align__(16) uint8_t dsm[];
+
+  // block -> (m-tile, n-tile, K split part); part ks covers K tiles [kt0, kt0 + nk)
+  const int mt = blockIdx.x % g.max_mt, rest = blockIdx.x / g.max_mt;
+  const int nt = rest % NT, ks = rest / NT;
+  int e = 0, p0 = 0, rows = 0;
+  if (g.tiles) {
+    if (mt >= *g.n_tiles) return;
+    e = g.tiles[2 * mt];
+    const int m0 = g.tiles[2 * mt + 1];
+    p0 = g.offsets[e] + m0;
+    rows = min(kD64BM, g.offsets[e + 1] - p0);
+  } else {
+    p0 = mt * kD64BM;
+    if (p0 >= g.T) return;
+    rows = min(kD64BM, g.T - p0);
+  }
+  const int n0 = nt * BN;
+  const int K = g.K, N = g.N;
+  const int nk_all = K / GBK;
+  const int kt0 = ks * nk_all / g.ksplit, nk = (ks + 1) * nk_all / g.ksplit - kt0;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wn = wave;
+
+  const uint8_t* srcA[kD64InstA];
+  const uint8_t* srcB[kD64InstB];
+#pragma unroll
+  for (int i = 0; i < kD64InstA; ++i) {
+    const int gi = 64 * (kD64InstA * wave + i) + lane;
+    const int r = gi >> 3, kg = (gi & 7) ^ (r & 7);
+    const int p = p0 + min(r, rows - 1);
+    srcA[i] = reinterpret_cast<const uint8_t*>(g.A + (size_t)(g.perm ? g.perm[p] / g.k : p) * K + 8 * kg);
+  }
+#pragma unroll
+  for (int i = 0; i < kD64InstB; ++i) {
+    const int gb = 64 * (kD64InstB * wave + i) + lane;
+    const int r = gb / 5, part = gb - 5 * r;
+    const int q = GATED ? (r >> 7) : 0;
+    const int n = min(n0 + (GATED ? (r & 127) : r), N - 1);
+    srcB[i] = static_cast<const uint8_t*>(q ? g.W1 : g.W0) + (int64_t)e * g.expert_stride + (int64_t)n * g.row_bytes +
+              (part < 4 ? 16 * part : 52);
+  }
+  // DMA of tile kt (clamped past the end), part j of 4: A granule j / 2 on even parts, weight
+  // granules spread over the four parts
+  auto issue = [&](int kt, int j) {  // kt: tile index within this block's K range
+    const int kc = kt0 + min(kt, nk - 1);
+    uint8_t* st = dsm + (kt % kD64Stages) * kD64Stage;
+    if ((j & 1) == 0) {
+      const int i = j >> 1;
+      lds_dma16(srcA[i] + (size_t)kc * GBK * 2, st + 1024 * (kD64InstA * wave + i));
+    }
+#pragma unroll
+    for (int i = 0; i < kD64InstB; ++i)
+      if ((i * 4) / kD64InstB == j) lds_dma16(srcB[i] + (size_t)kc * 68, st + kD64A + 1024 * (kD64InstB * wave + i));
+  };
+
+  floatx16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int jn = 0; jn < 2; ++jn)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][jn][r] = 0.0f;
+
+  auto brow_of = [&](int jn) {
+    if constexpr (GATED) return jn * 128 + wn * 32 + (lane & 31);
+    return wn * 64 + 32 * jn + (lane & 31);
+  };
+  const int h = lane >> 5;
+  const half2_t off = h2(0xe480e480u);
+  struct Frags {
+    half8 a[2], b[2];
+  };
+  auto load_frags = [&](const uint8_t* st, auto KS, Frags& f) {
+    constexpr int ks = decltype(KS)::value;
+    constexpr int b = ks >> 1;
+    constexpr int X = 34 * b + 2 + 16 * (ks & 1);
+    const int gk = 2 * ks + h;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int r = 32 * i + (lane & 31);
+      f.a[i] = *reinterpret_cast<const half8*>(st + 16 * (8 * r + (gk ^ (r & 7))));
+    }
+    const uint8_t* Bs = st + kD64A;
+#pragma unroll
+    for (int jn = 0; jn < 2; ++jn) {
+      const uint8_t* row = Bs + kDmaRowB * brow_of(jn);
+      const uint32_t dbits = b ? (*reinterpret_cast<const uint32_t*>(row + 32) >> 16)
+                               : (*reinterpret_cast<const uint32_t*>(row) & 0xffffu);
+      const half2_t d = h2(dbits * 0x10001u);
+      uint32_t w0, w1;
+      if constexpr (b == 0) {
+        const uint32_t* qw = reinterpret_cast<const uint32_t*>(row + (X & ~3) + 8 * h);
+        w0 = __builtin_amdgcn_alignbit(qw[1], qw[0], 16);
+        w1 = __builtin_amdgcn_alignbit(qw[2], qw[1], 16);
+      } else {
+        const int byte = X + 8 * h;
+        const uint32_t* qw = reinterpret_cast<const uint32_t*>(row + (byte + 8 > 64 ? byte + 12 : byte));
+        w0 = qw[0];
+        w1 = qw[1];
+      }
+      const uint32_t q0 = w0 ^ 0x80808080u, q1 = w1 ^ 0x80808080u;
+      const uint32_t o0 = u32((magic_pair(q0, 0) + off) * d), o1 = u32((magic_pair(q0, 1) + off) * d);
+      const uint32_t o2 = u32((magic_pair(q1, 0) + off) * d), o3 = u32((magic_pair(q1, 1) + off) * d);
+      f.b[jn] = __builtin_bit_cast(half8, u32x4{o0, o1, o2, o3});
+    }
+  };
+  auto mfmas = [&](const Frags& f) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int jn = 0; jn < 2; ++jn)
+        acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[i], f.b[jn], acc[i][jn], 0, 0, 0);
+  };
+  auto compute = [&](int kt) {
+    const uint8_t* st = dsm + (kt % kD64Stages) * kD64Stage;
+    Frags f0, f1;
+    load_frags(st, std::integral_constant<int, 0>{}, f0);
+    issue(kt + kD64Stages - 1, 0);
+    load_frags(st, std::integral_constant<int, 1>{}, f1);
+    mfmas(f0);
+    issue(kt + kD64Stages - 1, 1);
+    load_frags(st, std::integral_constant<int, 2>{}, f0);
+    mfmas(f1);
+    issue(kt + kD64Stages - 1, 2);
+    load_frags(st, std::integral_constant<int, 3>{}, f1);
+    mfmas(f0);
+    issue(kt + kD64Stages - 1, 3);
+    mfmas(f1);
+  };
+
+  constexpr int kPerTile = kD64InstA + kD64InstB;
+  static_assert(kD64Stages == 5, "the wait below keeps three tiles in flight beyond the current one");
+#pragma unroll
+  for (int t = 0; t < kD64Stages - 1; ++t)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) issue(t, j);
+  for (int kt = 0; kt < nk; ++kt) {
+    wait_vmcnt<3 * kPerTile>();  // this wave's part of tile kt has landed
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();  // ... every wave's; stage (kt + 4) % 5 is free again
+    asm volatile("" ::: "memory");
+    compute(kt);
+  }
+  wait_vmcnt<0>();
+
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int jn = 0; jn < (GATED ? 1 : 2); ++jn) {
+      const int n = n0 + (GATED ? wn * 32 : wn * 64 + 32 * jn) + (lane & 31);
+      if (n >= N) continue;
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int m = 32 * i + 8 * ii + 4 * (lane >> 5) + jj;
+          if (m >= rows) continue;
+          const size_t o = (size_t)(p0 + m) * N + n;
+          if constexpr (GATED) {
+            g.out_h[o] = (_Float16)swiglu_g(acc[i][0][4 * ii + jj], acc[i][1][4 * ii + jj]);
+          } else {
+            g.out_y[ks * g.part_stride + o] = acc[i][jn][4 * ii + jj];
+          }
+        }
+    }
+}
+
 // Skinny grouped GEMM for segments of a few dozen tokens (decode batches of 8+ tokens, short prefills):
 // 64-token tiles, 256 threads. Each wave owns 32 output columns (gate/up: 32 gate + 32 up rows; down:
 // 64 rows) and decodes its own weight rows straight into MFMA B operands: lane (n = lane % 32,
@@ -778,6 +960,15 @@ int launch_skinny_fmt(GemmArgs g, int max_mtiles, hipStream_t st) {
   const int NT = (g.N + BN - 1) / BN;
   if (max_mtiles == 0 || NT == 0) return EMBER_OK;
   g.max_mt = max_mtiles;
+  static const bool dma_off = [] { const char* v = std::getenv("EMBER_GEMM_DMA"); return v && atoi(v) == 0; }();
+  if (FMT == EMBER_TYPE_Q8_0 && !dma_off) {
+    static const bool ok = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma64_q8_kernel<GATED>),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)kD64Lds) == hipSuccess;
+    if (!ok) return EMBER_ERR_LAUNCH;
+    if (GATED || g.ksplit < 1) g.ksplit = 1;
+    gemm_dma64_q8_kernel<GATED><<<(unsigned)(max_mtiles * NT * g.ksplit), kD64Threads, kD64Lds, st>>>(g, NT);
+    return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
+  }
   gemm_skinny_kernel<FMT, GATED><<<(unsigned)(max_mtiles * NT), 256, 0, st>>>(g, NT);
   return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
 }
@@ -798,6 +989,14 @@ int launch_gemm_skinny(const GemmArgs& g, bool gated, int max_mtiles, hipStream_
 }
 
 int gemm_skinny_max_tiles(int T, int k, int E) { return (T * k + SBM - 1) / SBM + std::min(E, T * k); }
+
+int gemm_skinny_ksplit(int type, int max_mtiles, int N, int K) {
+  if (type != EMBER_TYPE_Q8_0) return 1;  // the split lives in the Q8_0 DMA kernel
+  const int blocks = max_mtiles * ((N + 255) / 256);
+  int ks = 1;
+  while (ks < kMaxKSplit && blocks * ks < 512 && K / GBK >= 16 * ks * 2) ks *= 2;
+  return ks;
+}
 
 // x (f32) -> fp16, RNE, elementwise.
 __global__ void __launch_bounds__(256) to_f16_kernel(const float* __restrict__ x, int64_t n, _Float16* __restrict__ y) {

@@ -104,6 +104,8 @@ struct GemmArgs {
   _Float16* out_h;         // gated: silu(gate) * up as fp16 [pos][N]
   float* out_y;            // plain: f32 [pos][N]
   int max_mt;              // m-tile slots of the launch (set by the launcher)
+  int ksplit;              // plain projections: K split over this many blocks, partial sums to
+  int64_t part_stride;     // out_y + s * part_stride (floats), summed in order by the combine
 };
 bool gemm_supported(int type, int K);
 int gemm_max_tiles(int T, int k, int E);
@@ -113,8 +115,13 @@ int launch_build_tiles(const int32_t* offsets, int E, bool skinny, int32_t* tile
 // Skinny variant for segments of a few dozen tokens (64-token tiles).
 int launch_gemm_skinny(const GemmArgs& g, bool gated, int max_mtiles, hipStream_t st);
 int gemm_skinny_max_tiles(int T, int k, int E);
+// K split of the skinny path's plain (down) projection: 1..kMaxKSplit, so that the launch has enough
+// blocks for the chip when the output is narrow
+constexpr int kMaxKSplit = 4;
+int gemm_skinny_ksplit(int type, int max_mtiles, int N, int K);
 
-int launch_combine(const float* y, const float* gates, const int32_t* pos, const float* y_shared, float scale, int T,
+int launch_combine(const float* y, int nparts, int64_t part_stride, const float* gates, const int32_t* pos,
+                   const float* y_shared, float scale, int T,
                    int k, int d, float* out, hipStream_t st);
 
 }  // namespace ember_moe
