@@ -168,15 +168,13 @@ __device__ inline bool seg_view(const ProjArgs& a, const Dispatch& dp, int b, in
 // has more than L chunks), so a step covers 64 / L rows. Weight loads run through a ring of NB
 // register buffers ahead of the dots. MT tokens per pass over the weights; their activation rows are
 // staged in LDS (quantized on the way for Q8_0 / Q4_K).
-template <int FMT, int MT, bool GATED, int NB, int NT, int WPE>
-__global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) proj_kernel(ProjArgs a) {
+// The body of proj_kernel for one segment view.
+template <int FMT, int MT, bool GATED, int NB, int NT>
+__device__ inline void proj_body(const ProjArgs& a, const Dispatch& dp, const SegView& v) {
   using F = Fmt<FMT>;
   constexpr int G2 = GATED ? 2 : 1;
   extern __shared__ __align__(16) uint8_t act_lds[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = NT / 64;
-  Dispatch dp{a.used ? *a.n_used : 0, a.used, a.offsets, a.perm};
-  SegView v;
-  if (!seg_view<GATED, MT>(a, dp, blockIdx.x, gridDim.x, v)) return;
   const int K = v.K;
   const int C = (K + F::CE - 1) / F::CE;
   int Lg = 0;
@@ -288,6 +286,14 @@ __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) 
 #pragma unroll 1
     for (int q0 = 0; q0 < nloads; q0 += U) ring_for<U>([&](auto J) { slot(q0, J); });
   }
+}
+
+template <int FMT, int MT, bool GATED, int NB, int NT, int WPE>
+__global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) proj_kernel(ProjArgs a) {
+  Dispatch dp{a.used ? *a.n_used : 0, a.used, a.offsets, a.perm};
+  SegView v;
+  const bool active = seg_view<GATED, MT>(a, dp, blockIdx.x, gridDim.x, v);
+  if (active) proj_body<FMT, MT, GATED, NB, NT>(a, dp, v);
 }
 
 template <int FMT, int MT, bool GATED, int NB, int NT, int WPE>

@@ -355,18 +355,20 @@ __global__ void __launch_bounds__(512) route_dispatch_small(const float* __restr
   const int wave = threadIdx.x >> 6;
   const size_t wl = route_wave_lds(E);
   int* sidx = reinterpret_cast<int*>(lds_raw + kSmallT * wl);
-  int* cnt = sidx + kSmallSlots;
-  if (wave < T)
+  float* sgate = reinterpret_cast<float*>(sidx + kSmallSlots);
+  int* cnt = reinterpret_cast<int*>(sgate + kSmallSlots);
+  if (wave < T)  // picks and gates stay in LDS; the block copies them out below
     route_token(logits + (size_t)wave * E, E, k, renorm, routed, sigmoid, bias, groups_n, groups_top,
-                lds_raw + wave * wl, idx + (size_t)wave * k, gates + (size_t)wave * k);
+                lds_raw + wave * wl, sidx + (size_t)wave * k, sgate + (size_t)wave * k);
   for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[e] = 0;
-  __syncthreads();  // idx (global, written by this block) is visible block-wide
+  __syncthreads();
   const int n = T * k;
   const int sl = threadIdx.x;
   int e = -1;
   if (sl < n) {
-    e = idx[sl];
-    sidx[sl] = e;
+    e = sidx[sl];
+    idx[sl] = e;
+    gates[sl] = sgate[sl];
     if (e >= 0) atomicAdd(&cnt[e], 1);
   }
   __syncthreads();
@@ -463,7 +465,7 @@ int launch_route_dispatch(const float* logits, int T, int E, int k, int renorm, 
     int s = launch_route(logits, T, E, k, renorm, routed, sigmoid, bias, groups_n, groups_top, idx, gates, st);
     return s ? s : launch_dispatch(idx, T, k, E, ds, st);
   }
-  const size_t lds = kSmallT * route_wave_lds(E) + (size_t)(kSmallSlots + E + 16) * sizeof(int);
+  const size_t lds = kSmallT * route_wave_lds(E) + (size_t)(2 * kSmallSlots + E + 16) * sizeof(int);
   route_dispatch_small<<<1, 512, lds, st>>>(logits, T, E, k, renorm, routed, sigmoid, bias, groups_n, groups_top, idx,
                                             gates, ds);
   return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;

@@ -286,7 +286,14 @@ __device__ inline void route_token(const float* __restrict__ r, int E, int k, in
   double z = 0.0;
   if (renorm) {
     for (int j = 0; j < kk; ++j) mx = smax(mx, row[picks[j]]);
-    for (int j = 0; j < kk; ++j) z = z + exp_glibc((double)(row[picks[j]] - mx));
+    // lane j evaluates the j-th exponential (all at once); every lane adds them in pick order
+    const double exj = lane < kk ? exp_glibc((double)(row[picks[lane]] - mx)) : 0.0;
+    for (int j = 0; j < kk; ++j) z = z + __shfl(exj, j, 64);
+    if (lane < k) {
+      idx_t[lane] = lane < kk ? picks[lane] : -1;
+      gate_t[lane] = lane < kk ? (float)(exj / z) : 0.0f;
+    }
+    return;
   } else {
     // The maximum of a NaN-free row does not depend on the scan order (only the sign of a zero
     // maximum can, and r - (+0) and r - (-0) round to equal exp arguments for every r).
@@ -303,7 +310,7 @@ __device__ inline void route_token(const float* __restrict__ r, int E, int k, in
     if (lane < kk) {
       const int e = picks[lane];
       idx_t[lane] = e;
-      gate_t[lane] = (float)(exp_glibc((double)(row[e] - mx)) / z);
+      gate_t[lane] = (float)(ex[e] / z);  // the exponential the sum used
     } else {
       idx_t[lane] = -1;
       gate_t[lane] = 0.0f;
