@@ -133,7 +133,38 @@ __host__ __device__ inline size_t route_wave_lds(int E) {
 // value with ties to the lower index — the result of the reference's serial strict-> scans. Experts
 // with cand[e] == 0 are skipped (cand may be null); a pass that finds nothing ends the search. Lane 0
 // writes the picks in pick order; returns their number (uniform across the wave).
+__device__ inline int wave_topk_passes(const float* val, const char* cand, int E, int k, int* picks);
+
+// The same selection by ranks, for larger k: expert e is picked iff it is a candidate and fewer than k
+// candidates are strictly better (larger value, ties to the lower index) — exactly the experts the k
+// argmax passes pick, and already in ascending index order, the order the picks are returned in.
+// O(E^2 / 64) compares per lane against k dependent wave reductions.
+__device__ inline int wave_topk_rank(const float* val, const char* cand, int E, int k, int* picks) {
+  const int lane = threadIdx.x & 63;
+  int n = 0;  // picks so far (uniform)
+  for (int e0 = 0; e0 < E; e0 += 64) {
+    const int e = e0 + lane;
+    bool sel = false;
+    if (e < E && (!cand || cand[e])) {
+      const float v = val[e];
+      int rank = 0;
+      for (int o = 0; o < E; ++o)
+        if ((!cand || cand[o]) && better(val[o], o, v, e)) ++rank;
+      sel = rank < k;
+    }
+    const uint64_t m = __ballot(sel);
+    if (sel) picks[n + __builtin_popcountll(m & ((1ull << lane) - 1))] = e;
+    n += __builtin_popcountll(m);
+  }
+  wave_sync_lds();
+  return n;
+}
+
 __device__ inline int wave_topk(const float* val, const char* cand, int E, int k, int* picks) {
+  return k >= 4 ? wave_topk_rank(val, cand, E, k, picks) : wave_topk_passes(val, cand, E, k, picks);
+}
+
+__device__ inline int wave_topk_passes(const float* val, const char* cand, int E, int k, int* picks) {
   const int lane = threadIdx.x & 63;
   uint32_t mine_taken = 0;  // bit q: expert lane + 64q taken (E <= 2048)
   int n = 0;
