@@ -127,7 +127,7 @@ Layout layout(const ember_moe_layer* w, int T) {
   l.perm = o; o = align_up(o + slots * 4);
   l.r = route_layout(T, w->E, w->k, o); o = l.r.end;
   l.h = o; o = align_up(o + slots * w->d_ff * 4);
-  // y holds kMaxKSplit partial sums per row when the skinny path splits the down projection's K
+  // y holds kMaxKSplit partial sums per row when an MFMA path splits the down projection's K
   l.y = o; o = align_up(o + slots * w->d * 4 * kMaxKSplit);
   l.hs = o; o = align_up(o + (size_t)T * w->d_ff_shared * 4);
   l.ys = o; o = align_up(o + (w->d_ff_shared > 0 ? (size_t)T * w->d * 4 : 0));
@@ -281,10 +281,8 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     g.K = d_ff;
     g.out_h = nullptr;
     g.out_y = y;
-    if (skinny) {
-      g.ksplit = ksplit = gemm_skinny_ksplit(g.type, mt, d, d_ff);
-      g.part_stride = (int64_t)T * k * d;
-    }
+    g.ksplit = ksplit = skinny ? gemm_skinny_ksplit(g.type, mt, d, d_ff) : gemm_ksplit(g.type, T, k, E, d, d_ff);
+    g.part_stride = (int64_t)T * k * d;
     if ((s = gemm(g, false, mt))) return s;
     mark(ev, 5, st);
   } else {

@@ -363,14 +363,14 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs g, int NT) 
 // ---------------------------------------------------------------------------------------------
 // Q8_0 grouped GEMM with direct global->LDS tile loads. Tiles of 256 tokens x 256 weight rows x 64 K
 // run through a ring of three LDS stages that global_load_lds fills without passing through
-// registers, so two tiles are in flight while one is multiplied. Waves 0-3 load the activation tile
-// (16-byte granules XOR-swizzled by row, for conflict-free fragment reads), waves 4-7 the weight tile
-// in its Q8_0 bytes: the 68 bytes of a row's K tile as five 16-byte granules, the fifth overlapping
-// (bytes 52..67), so a row occupies 80 bytes of LDS. 512 threads = 8 waves (two per SIMD: one wave's
-// fragment loads and decode overlap the other's MFMAs) in a 2 (M) x 4 (N) arrangement; a wave owns
-// 128 tokens x 64 weight rows (gated: 32 gate + 32 up columns, so SwiGLU pairs meet in one wave) and
-// decodes its own B fragments from the Q8_0 bytes straight into MFMA operands (fp16 d * q, one
-// rounding, as the decoders above).
+// registers, so two tiles are in flight while one is multiplied. Every wave loads a share of both
+// operands: the activation tile as 16-byte granules XOR-swizzled by row pair (the 16 rows that one
+// 16-lane pass of ds_read_b128 reads fall on distinct bank groups of the 64-bank LDS), the weight
+// tile in its Q8_0 bytes: the 68 bytes of a row's K tile as five 16-byte granules, the fifth
+// overlapping (bytes 52..67), so a row occupies 80 bytes of LDS. 512 threads = 8 waves (two per
+// SIMD) in a 2 (M) x 4 (N) arrangement; a wave owns 128 tokens x 64 weight rows (gated: 32 gate +
+// 32 up columns, so SwiGLU pairs meet in one wave) and decodes its own B fragments from the Q8_0
+// bytes straight into MFMA operands (fp16 d * q, one rounding, as the decoders above).
 typedef __attribute__((address_space(3))) void lds_void_t;
 constexpr int kDmaThreads = 512, kDmaStages = 3;
 constexpr int kDmaRowB = 80;                     // LDS bytes of one weight row's K tile
@@ -378,8 +378,9 @@ constexpr int kDmaA = GBM * GBK * 2;             // activation bytes per stage (
 constexpr int kDmaB = 256 * kDmaRowB;            // weight bytes per stage (20 KiB)
 constexpr int kDmaStage = kDmaA + kDmaB;
 constexpr size_t kDmaLds = (size_t)kDmaStages * kDmaStage;
-constexpr int kDmaInstA = kDmaA / 16 / 64 / 4;   // 16-byte DMA instructions per A-loading wave per tile (8)
-constexpr int kDmaInstB = kDmaB / 16 / 64 / 4;   // ... per B-loading wave (5)
+constexpr int kDmaInstA = kDmaA / 1024 / 8;      // 16-byte DMA instructions per wave per tile: activations (4)
+constexpr int kDmaInstB = (kDmaB / 1024 + 7) / 8; // ... weights (3, the last shared)
+constexpr int kDmaInst = kDmaInstA + kDmaInstB;
 
 __device__ inline void lds_dma16(const void* g, uint8_t* lds) {
   __builtin_amdgcn_global_load_lds(g, (lds_void_t*)lds, 16, 0, 0);
@@ -396,8 +397,12 @@ __global__ void __launch_bounds__(kDmaThreads) gemm_dma_q8_kernel(GemmArgs g, in
   constexpr int BN = GATED ? 128 : 256;
   extern __shared__ __align__(16) uint8_t dsm[];
 
+  // block -> (m-tile, n-tile, K split part): XCD b % 8 runs m-tile (b % 8) + 8 ((b / 8) / (NT KS)), so
+  // the blocks an XCD holds at once share their activation tile in its L2
+  const int KS = GATED ? 1 : g.ksplit;
   const int xcd = blockIdx.x % 8, jb = blockIdx.x / 8;
-  const int mt = xcd + 8 * (jb / NT), nt = jb % NT;
+  const int mt = xcd + 8 * (jb / (NT * KS)), rem = jb % (NT * KS);
+  const int nt = rem / KS, ks = rem % KS;
   int e = 0, p0 = 0, rows = 0;
   if (g.tiles) {
     if (mt >= *g.n_tiles) return;
@@ -412,49 +417,53 @@ __global__ void __launch_bounds__(kDmaThreads) gemm_dma_q8_kernel(GemmArgs g, in
   }
   const int n0 = nt * BN;
   const int K = g.K, N = g.N;
-  const int nk = K / GBK;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave & 1, wn = wave >> 1;
-  const bool a_loader = wave < 4;  // wave-uniform
+  // this part's K tiles [kt0, kt0 + nk)
+  const int nk_all = K / GBK;
+  const int kt0 = ks * nk_all / KS, nk = (ks + 1) * nk_all / KS - kt0;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // wave w runs on SIMD w % 4, so each SIMD holds one wave of each M half: a tile whose rows end
+  // inside the first half leaves no SIMD with double work
+  const int wm = wave >> 2, wn = wave & 3;
+  // 32-row subtiles of this wave's M half that hold tokens (0..4); the others are skipped
+  const int msub = min(4, max(0, (rows - 128 * wm + 31) >> 5));
 
-  // DMA sources: instruction i of a loading wave fills 16-byte granules 64 (n_inst * w + i) + lane.
-  // A granule gi: row gi / 8, slot gi % 8 holding K granule slot ^ (row % 8); rows past the tile
-  // repeat its last row. B granule gb: row gb / 5, part gb % 5 = bytes 16 part (parts 0-3) or 52.
-  const uint8_t* src[kDmaInstA];
-  if (a_loader) {
+  // DMA sources, the same code in every wave (no branches in the K loop): DMA instruction j of a
+  // tile fills 16-byte granules 64 j + lane. Activations: instructions 4 w + i (i < 4); granule gi is
+  // row gi / 8, slot gi % 8 holding K granule slot ^ ((row / 2) % 8); rows past the tile repeat its last
+  // row.
+  // Weights: instructions min(3 w + i, 19) (i < 3; waves 6 and 7 repeat instruction 19, which rewrites
+  // identical bytes); granule gb is row gb / 5, part gb % 5 = bytes 16 part (parts 0-3) or 52.
+  const uint8_t* srcA[kDmaInstA];
+  const uint8_t* srcB[kDmaInstB];
 #pragma unroll
-    for (int i = 0; i < kDmaInstA; ++i) {
-      const int gi = 64 * (kDmaInstA * wave + i) + lane;
-      const int r = gi >> 3, kg = (gi & 7) ^ (r & 7);
-      const int p = p0 + min(r, rows - 1);
-      src[i] = reinterpret_cast<const uint8_t*>(g.A + (size_t)(g.perm ? g.perm[p] / g.k : p) * K + 8 * kg);
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < kDmaInstA; ++i) {
-      const int gb = 64 * (kDmaInstB * (wave - 4) + min(i, kDmaInstB - 1)) + lane;
-      const int r = gb / 5, part = gb - 5 * r;
-      const int q = GATED ? (r >> 7) : 0;
-      const int n = min(n0 + (GATED ? (r & 127) : r), N - 1);
-      src[i] = static_cast<const uint8_t*>(q ? g.W1 : g.W0) + (int64_t)e * g.expert_stride + (int64_t)n * g.row_bytes +
-               (part < 4 ? 16 * part : 52);
-    }
+  for (int i = 0; i < kDmaInstA; ++i) {
+    const int gi = 64 * (kDmaInstA * wave + i) + lane;
+    const int r = gi >> 3, kg = (gi & 7) ^ ((r >> 1) & 7);
+    const int p = p0 + min(r, rows - 1);
+    srcA[i] = reinterpret_cast<const uint8_t*>(g.A + (size_t)(g.perm ? g.perm[p] / g.k : p) * K + 8 * kg);
   }
-  // DMA of tile kt (clamped: tiles past the end reload the last, never multiplied), instructions
-  // [i0, i1) of this wave's share, so that the issue can be spread over the MFMAs of a tile
-  auto issue = [&](int kt, int i0, int i1) {
-    const int kc = min(kt, nk - 1);
+#pragma unroll
+  for (int i = 0; i < kDmaInstB; ++i) {
+    const int gb = 64 * min(kDmaInstB * wave + i, kDmaB / 1024 - 1) + lane;
+    const int r = gb / 5, part = gb - 5 * r;
+    const int q = GATED ? (r >> 7) : 0;
+    const int n = min(n0 + (GATED ? (r & 127) : r), N - 1);
+    srcB[i] = static_cast<const uint8_t*>(q ? g.W1 : g.W0) + (int64_t)e * g.expert_stride + (int64_t)n * g.row_bytes +
+              (part < 4 ? 16 * part : 52);
+  }
+  // DMA of tile kt (clamped: tiles past the end reload the last, never multiplied), part j of 4 so
+  // that the issue is spread over the K steps of a tile: activation instruction j, weight instruction j
+  auto issue = [&](int kt, int j) {
+    const int kc = kt0 + min(kt, nk - 1);
     uint8_t* st = dsm + (kt % kDmaStages) * kDmaStage;
-    if (a_loader) {
+    lds_dma16(srcA[j] + (size_t)kc * GBK * 2, st + 1024 * (kDmaInstA * wave + j));
+    if (j < kDmaInstB)
+      lds_dma16(srcB[j] + (size_t)kc * 68, st + kDmaA + 1024 * min(kDmaInstB * wave + j, kDmaB / 1024 - 1));
+  };
+  auto issue_all = [&](int kt) {
 #pragma unroll
-      for (int i = 0; i < kDmaInstA; ++i)
-        if (i >= i0 && i < i1) lds_dma16(src[i] + (size_t)kc * GBK * 2, st + 1024 * (kDmaInstA * wave + i));
-    } else {
-#pragma unroll
-      for (int i = 0; i < kDmaInstB; ++i)
-        if (i >= 2 * i0 / 3 && i < (i1 == kDmaInstA ? kDmaInstB : 2 * i1 / 3))
-          lds_dma16(src[i] + (size_t)kc * 68, st + kDmaA + 1024 * (kDmaInstB * (wave - 4) + i));
-    }
+    for (int j = 0; j < kDmaInstA; ++j) issue(kt, j);
   };
 
   floatx16 acc[4][2];
@@ -473,23 +482,24 @@ __global__ void __launch_bounds__(kDmaThreads) gemm_dma_q8_kernel(GemmArgs g, in
   const int h = lane >> 5;
   const half2_t off = h2(0xe480e480u);  // -1152 = -(1024 + 128) in each half
 
-  // Fragments of K step ks (compile time) of the tile in stage `st`. Lane's 8 elements: K granule
-  // gk = 2 ks + h of the 64 = Q8_0 block b = ks / 2, bytes X + 8 h .. + 8 of the row's 68 with
-  // X = 34 b + 2 + 16 (ks % 2); for b = 1 those are dword aligned and, past byte 52, read from the
-  // overlapping fifth granule (LDS byte = global byte + 12); for b = 0 they sit two bytes past a
-  // dword and are funnel-shifted out of three dwords.
+  // Fragments of K step ks (compile time) of the tile in stage `st`, for the first MS (compile time)
+  // 32-row subtiles. Lane's 8 elements: K granule gk = 2 ks + h of the 64 = Q8_0 block b = ks / 2,
+  // bytes X + 8 h .. + 8 of the row's 68 with X = 34 b + 2 + 16 (ks % 2); for b = 1 those are dword
+  // aligned and, past byte 52, read from the overlapping fifth granule (LDS byte = global byte + 12);
+  // for b = 0 they sit two bytes past a dword and are funnel-shifted out of three dwords.
   struct Frags {
     half8 a[4], b[2];
   };
-  auto load_frags = [&](const uint8_t* st, auto KS, Frags& f) {
+  auto load_frags = [&](const uint8_t* st, auto KS, auto MSc, Frags& f) {
     constexpr int ks = decltype(KS)::value;
+    constexpr int MS = decltype(MSc)::value;
     constexpr int b = ks >> 1;
     constexpr int X = 34 * b + 2 + 16 * (ks & 1);
     const int gk = 2 * ks + h;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < MS; ++i) {
       const int r = wm * 128 + 32 * i + (lane & 31);
-      f.a[i] = *reinterpret_cast<const half8*>(st + 16 * (8 * r + (gk ^ (r & 7))));
+      f.a[i] = *reinterpret_cast<const half8*>(st + 16 * (8 * r + (gk ^ ((r >> 1) & 7))));
     }
     const uint8_t* Bs = st + kDmaA;
 #pragma unroll
@@ -515,49 +525,69 @@ __global__ void __launch_bounds__(kDmaThreads) gemm_dma_q8_kernel(GemmArgs g, in
       f.b[jn] = __builtin_bit_cast(half8, u32x4{o0, o1, o2, o3});
     }
   };
-  auto mfmas = [&](const Frags& f) {
+  auto mfmas = [&](const Frags& f, auto MSc) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < decltype(MSc)::value; ++i)
 #pragma unroll
       for (int jn = 0; jn < 2; ++jn)
         acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[i], f.b[jn], acc[i][jn], 0, 0, 0);
   };
-  // the MFMAs of tile kt with the DMA of tile kt + 2 spread between its K steps (a VMEM instruction
-  // that stalls on a full memory queue then holds up this wave while the matrix core still has work)
-  auto compute = [&](int kt) {
-    const uint8_t* st = dsm + (kt % kDmaStages) * kDmaStage;
-    Frags f0, f1;
-    load_frags(st, std::integral_constant<int, 0>{}, f0);
-    issue(kt + 2, 0, 2);
-    load_frags(st, std::integral_constant<int, 1>{}, f1);
-    mfmas(f0);
-    issue(kt + 2, 2, 4);
-    load_frags(st, std::integral_constant<int, 2>{}, f0);
-    mfmas(f1);
-    issue(kt + 2, 4, 6);
-    load_frags(st, std::integral_constant<int, 3>{}, f1);
-    mfmas(f0);
-    issue(kt + 2, 6, kDmaInstA);
-    mfmas(f1);
-  };
-
-  static_assert(kDmaStages == 3, "the waits below assume one tile in flight beyond the current one");
-  issue(0, 0, kDmaInstA);
-  issue(1, 0, kDmaInstA);
-  for (int kt = 0; kt < nk; ++kt) {
-    // this wave's part of tile kt has landed (tile kt + 1 may still be in flight) ...
-    if (a_loader)
-      wait_vmcnt<kDmaInstA>();
-    else
-      wait_vmcnt<kDmaInstB>();
-    // ... and every wave's part; stage (kt + 2) % 3 is free again (its reads were consumed by the MFMAs
-    // of tile kt - 1 before each wave got here). A bare barrier: __syncthreads()'s release fence would
-    // wait for the DMA of tile kt + 1 as well. The empty asm statements keep the compiler from moving
-    // LDS accesses across it.
+  // A bare barrier: __syncthreads()'s release fence would wait for the DMA in flight as well. The
+  // empty asm statements keep the compiler from moving LDS accesses across it.
+  auto barrier = [] {
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    compute(kt);
+  };
+  // The K loop, rotated so that no tile starts cold: iteration kt runs the MFMAs of K steps 0-2 of
+  // tile kt with the DMA of tile kt + 2 spread between them, then waits for tile kt + 1 (this wave's
+  // DMA, then every wave's at the barrier, which also marks the reads of tile kt complete, so stage
+  // kt % 3 may be refilled next iteration), and reads and decodes K step 0 of tile kt + 1 while the
+  // MFMAs of K step 3 of tile kt run. (The last iteration reads tile nk, a clamped reload, unused.)
+  // A wave whose M half holds no tokens (MS = 0) only loads and keeps the barriers.
+  static_assert(kDmaStages == 3, "the waits below assume one tile in flight beyond the current one");
+  auto k_loop = [&](auto MSc) {
+    using K0 = std::integral_constant<int, 0>;
+    using K1 = std::integral_constant<int, 1>;
+    using K2 = std::integral_constant<int, 2>;
+    using K3 = std::integral_constant<int, 3>;
+    issue_all(0);
+    issue_all(1);
+    wait_vmcnt<kDmaInst>();
+    barrier();
+    Frags f0, f1;
+    if constexpr (decltype(MSc)::value > 0) load_frags(dsm, K0{}, MSc, f0);
+    for (int kt = 0; kt < nk; ++kt) {
+      if constexpr (decltype(MSc)::value == 0) {
+        issue_all(kt + 2);
+        wait_vmcnt<kDmaInst>();
+        barrier();
+      } else {
+        const uint8_t* st = dsm + (kt % kDmaStages) * kDmaStage;
+        load_frags(st, K1{}, MSc, f1);
+        issue(kt + 2, 0);
+        mfmas(f0, MSc);
+        load_frags(st, K2{}, MSc, f0);
+        issue(kt + 2, 1);
+        mfmas(f1, MSc);
+        load_frags(st, K3{}, MSc, f1);
+        issue(kt + 2, 2);
+        mfmas(f0, MSc);
+        issue(kt + 2, 3);
+        wait_vmcnt<kDmaInst>();
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of tile kt are complete
+        barrier();
+        load_frags(dsm + ((kt + 1) % kDmaStages) * kDmaStage, K0{}, MSc, f0);
+        mfmas(f1, MSc);
+      }
+    }
+  };
+  switch (msub) {  // wave-uniform
+    case 4: k_loop(std::integral_constant<int, 4>{}); break;
+    case 3: k_loop(std::integral_constant<int, 3>{}); break;
+    case 2: k_loop(std::integral_constant<int, 2>{}); break;
+    case 1: k_loop(std::integral_constant<int, 1>{}); break;
+    default: k_loop(std::integral_constant<int, 0>{}); break;
   }
   wait_vmcnt<0>();  // no DMA may still target LDS when the block exits
 
@@ -578,7 +608,7 @@ __global__ void __launch_bounds__(kDmaThreads) gemm_dma_q8_kernel(GemmArgs g, in
           if constexpr (GATED) {
             g.out_h[o] = (_Float16)swiglu_g(acc[i][0][4 * ii + jj], acc[i][1][4 * ii + jj]);
           } else {
-            g.out_y[o] = acc[i][jn][4 * ii + jj];
+            g.out_y[ks * g.part_stride + o] = acc[i][jn][4 * ii + jj];
           }
         }
     }
@@ -627,7 +657,7 @@ __global__ void __launch_bounds__(kD64Threads) gemm_dma64_q8_kernel(GemmArgs g, 
 #pragma unroll
   for (int i = 0; i < kD64InstA; ++i) {
     const int gi = 64 * (kD64InstA * wave + i) + lane;
-    const int r = gi >> 3, kg = (gi & 7) ^ (r & 7);
+    const int r = gi >> 3, kg = (gi & 7) ^ ((r >> 1) & 7);
     const int p = p0 + min(r, rows - 1);
     srcA[i] = reinterpret_cast<const uint8_t*>(g.A + (size_t)(g.perm ? g.perm[p] / g.k : p) * K + 8 * kg);
   }
@@ -679,7 +709,7 @@ __global__ void __launch_bounds__(kD64Threads) gemm_dma64_q8_kernel(GemmArgs g, 
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int r = 32 * i + (lane & 31);
-      f.a[i] = *reinterpret_cast<const half8*>(st + 16 * (8 * r + (gk ^ (r & 7))));
+      f.a[i] = *reinterpret_cast<const half8*>(st + 16 * (8 * r + (gk ^ ((r >> 1) & 7))));
     }
     const uint8_t* Bs = st + kD64A;
 #pragma unroll
@@ -908,6 +938,12 @@ __global__ void __launch_bounds__(256) gemm_skinny_kernel(GemmArgs g, int NT) {
     }
 }
 
+// EMBER_GEMM_DMA=0 routes Q8_0 to the register-staged kernels (a debugging switch); they have no K split
+static bool dma_enabled() {
+  static const bool on = [] { const char* v = std::getenv("EMBER_GEMM_DMA"); return !(v && atoi(v) == 0); }();
+  return on;
+}
+
 bool gemm_supported(int type, int K) {
   return (type == EMBER_TYPE_Q8_0 || type == EMBER_TYPE_Q4_K || type == EMBER_TYPE_BF16 || type == EMBER_TYPE_F16) &&
          K % GBK == 0;
@@ -926,13 +962,15 @@ int launch_gemm_fmt(const GemmArgs& g, int max_mtiles, hipStream_t st) {
   const int mgroups = (max_mtiles + 7) / 8;
   const unsigned blocks = (unsigned)(8 * mgroups * NT);
   if (max_mtiles == 0 || NT == 0) return EMBER_OK;
-  static const bool dma_off = [] { const char* v = std::getenv("EMBER_GEMM_DMA"); return v && atoi(v) == 0; }();
+  const bool dma_off = !dma_enabled();
   if (FMT == EMBER_TYPE_Q8_0 && !dma_off) {
     static const bool dma_ok =
         hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma_q8_kernel<GATED>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDmaLds) == hipSuccess;
     if (!dma_ok) return EMBER_ERR_LAUNCH;
-    gemm_dma_q8_kernel<GATED><<<blocks, kDmaThreads, kDmaLds, st>>>(g, NT);
+    GemmArgs gk = g;
+    if (GATED || gk.ksplit < 1) gk.ksplit = 1;
+    gemm_dma_q8_kernel<GATED><<<blocks * (unsigned)gk.ksplit, kDmaThreads, kDmaLds, st>>>(gk, NT);
     return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
   }
   gemm_kernel<FMT, GATED><<<blocks, kGemmThreads, kGemmLds, st>>>(g, NT);
@@ -960,7 +998,7 @@ int launch_skinny_fmt(GemmArgs g, int max_mtiles, hipStream_t st) {
   const int NT = (g.N + BN - 1) / BN;
   if (max_mtiles == 0 || NT == 0) return EMBER_OK;
   g.max_mt = max_mtiles;
-  static const bool dma_off = [] { const char* v = std::getenv("EMBER_GEMM_DMA"); return v && atoi(v) == 0; }();
+  const bool dma_off = !dma_enabled();
   if (FMT == EMBER_TYPE_Q8_0 && !dma_off) {
     static const bool ok = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma64_q8_kernel<GATED>),
                                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)kD64Lds) == hipSuccess;
@@ -990,8 +1028,18 @@ int launch_gemm_skinny(const GemmArgs& g, bool gated, int max_mtiles, hipStream_
 
 int gemm_skinny_max_tiles(int T, int k, int E) { return (T * k + SBM - 1) / SBM + std::min(E, T * k); }
 
+int gemm_ksplit(int type, int T, int k, int E, int N, int K) {
+  if (type != EMBER_TYPE_Q8_0 || !dma_enabled()) return 1;  // the split lives in the Q8_0 DMA kernel
+  // expected 256-token tiles (segments average T k / E tokens) times n-tiles: aim for >= 4 rounds
+  const int est_tiles = (T * k + GBM - 1) / GBM + E / 2;
+  const int blocks = est_tiles * ((N + 255) / 256);
+  int ks = 1;
+  while (ks < kMaxKSplit && blocks * ks < 4 * 256 && K / GBK >= 32 * ks * 2) ks *= 2;
+  return ks;
+}
+
 int gemm_skinny_ksplit(int type, int max_mtiles, int N, int K) {
-  if (type != EMBER_TYPE_Q8_0) return 1;  // the split lives in the Q8_0 DMA kernel
+  if (type != EMBER_TYPE_Q8_0 || !dma_enabled()) return 1;  // the split lives in the Q8_0 DMA kernel
   const int blocks = max_mtiles * ((N + 255) / 256);
   int ks = 1;
   while (ks < kMaxKSplit && blocks * ks < 512 && K / GBK >= 16 * ks * 2) ks *= 2;

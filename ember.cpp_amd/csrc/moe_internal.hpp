@@ -119,6 +119,8 @@ int gemm_skinny_max_tiles(int T, int k, int E);
 // blocks for the chip when the output is narrow
 constexpr int kMaxKSplit = 4;
 int gemm_skinny_ksplit(int type, int max_mtiles, int N, int K);
+// ... and of the 256-token-tile path's (the down launch of a long prefill has few blocks per n-tile row)
+int gemm_ksplit(int type, int T, int k, int E, int N, int K);
 
 int launch_combine(const float* y, int nparts, int64_t part_stride, const float* gates, const int32_t* pos,
                    const float* y_shared, float scale, int T,
