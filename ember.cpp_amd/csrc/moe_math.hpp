@@ -127,7 +127,10 @@ EMBER_HD uint32_t as_u32(float f) {
 
 // expf(x), binary32. exp(x) = 2^(k/32) * 2^(r/32) with k = round(x * 32/ln2) and r = x*32/ln2 - k
 // evaluated by one FMA, 2^(r/32) by a cubic, one final rounding to binary32.
-EMBER_HD float expf_glibc(float x) {
+EMBER_HD float expf_glibc_t(float x, const uint64_t* tab32);
+EMBER_HD float expf_glibc(float x) { return expf_glibc_t(x, kExp2Tab32); }
+// the same with the 32-entry table at tab32 (a copy of kExp2Tab32, e.g. staged in LDS)
+EMBER_HD float expf_glibc_t(float x, const uint64_t* tab32) {
   const uint32_t ux = as_u32(x);
   const uint32_t abstop = (ux >> 20) & 0x7ff;
   if (abstop >= 0x42b) {  // |x| >= 88, Inf or NaN
@@ -146,7 +149,7 @@ EMBER_HD float expf_glibc(float x) {
   const uint64_t ki = as_u64(kd);
   kd -= shift;
   const double r = __builtin_fma(inv_ln2_n, xd, -kd);
-  const uint64_t t = kExp2Tab32[ki % 32] + (ki << 47);
+  const uint64_t t = tab32[ki % 32] + (ki << 47);
   const double s = as_f64(t);
   const double z = __builtin_fma(c0, r, c1);
   const double r2 = r * r;
@@ -159,7 +162,10 @@ EMBER_HD float expf_glibc(float x) {
 // ln2/128), 2^(k/128) = scale * (1 + tail) from the table, exp(r) - 1 by a degree-5 polynomial.
 // Bit-exact with glibc for |x| < 512; beyond, the result is within an ulp of exp (the callers feed
 // only arguments <= 0, where anything below -512 rounds to a gate of exactly 0).
-EMBER_HD double exp_glibc(double x) {
+EMBER_HD double exp_glibc_t(double x, const uint64_t* tab128);
+EMBER_HD double exp_glibc(double x) { return exp_glibc_t(x, kExp2Tab128); }
+// the same with the 256-entry table at tab128 (a copy of kExp2Tab128, e.g. staged in LDS)
+EMBER_HD double exp_glibc_t(double x, const uint64_t* tab128) {
   const double inv_ln2_n = 0x1.71547652b82fep0 * 128;
   const double shift = 0x1.8p52;
   const double neg_ln2_hi_n = -0x1.62e42fefa0000p-8;
@@ -184,8 +190,8 @@ EMBER_HD double exp_glibc(double x) {
   const double r = __builtin_fma(kd, neg_ln2_lo_n, __builtin_fma(kd, neg_ln2_hi_n, x));
   const uint32_t idx = 2 * (uint32_t)(ki % 128);
   const uint64_t top = ki << 45;
-  const double tail = as_f64(kExp2Tab128[idx]);
-  uint64_t sbits = kExp2Tab128[idx + 1] + top;
+  const double tail = as_f64(tab128[idx]);
+  uint64_t sbits = tab128[idx + 1] + top;
   const double r2 = r * r;
   const double tmp = __builtin_fma(r2 * r2, __builtin_fma(r, c5, c4), __builtin_fma(r2, __builtin_fma(r, c3, c2), tail + r));
   if (special) {

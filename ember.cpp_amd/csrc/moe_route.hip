@@ -466,6 +466,12 @@ int launch_route_dispatch(const float* logits, int T, int E, int k, int renorm, 
     return s ? s : launch_dispatch(idx, T, k, E, ds, st);
   }
   const size_t lds = kSmallT * route_wave_lds(E) + (size_t)(2 * kSmallSlots + E + 16) * sizeof(int);
+  static const bool lds_ok = [] {
+    const size_t most = kSmallT * route_wave_lds(kSmallE) + (size_t)(2 * kSmallSlots + kSmallE + 16) * sizeof(int);
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(&route_dispatch_small),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)most) == hipSuccess;
+  }();
+  if (!lds_ok) return EMBER_ERR_LAUNCH;
   route_dispatch_small<<<1, 512, lds, st>>>(logits, T, E, k, renorm, routed, sigmoid, bias, groups_n, groups_top, idx,
                                             gates, ds);
   return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;

@@ -123,8 +123,11 @@ __device__ inline void route_routed_serial(const float* r, int E, int k, int ren
 }
 
 // Per-wave LDS footprint of route_kernel for E experts.
+// LDS bytes of one routing wave: the exp tables (copies of kExp2Tab128 and kExp2Tab32, staged with
+// the logits so that no exponential waits on a global table load), then the work arrays.
+constexpr size_t kRouteTabBytes = (256 + 32) * 8;
 __host__ __device__ inline size_t route_wave_lds(int E) {
-  const size_t bytes = (size_t)E * 8 /*ex*/ + (size_t)E * 4 /*s*/ + (size_t)2 * E * 4 /*c + group scores*/ +
+  const size_t bytes = kRouteTabBytes + (size_t)E * 8 /*ex*/ + (size_t)E * 4 /*s*/ + (size_t)2 * E * 4 /*c + group scores*/ +
                        (size_t)64 * 4 /*picks*/ + (size_t)((2 * E + 3) & ~3) /*cand, taken*/ + (size_t)E * 4 /*row*/;
   return (bytes + 15) & ~(size_t)15;
 }
@@ -160,7 +163,61 @@ __device__ inline int wave_topk_rank(const float* val, const char* cand, int E, 
   return n;
 }
 
+// Order key of a NaN-free float: key(a) > key(b) iff a > b, and both zeros share the key of +0 (they
+// compare equal, so they tie).
+__device__ inline uint32_t order_key(float f) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, f == 0.0f ? 0.0f : f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// The same selection as wave_topk_rank with the values in registers (E <= 64 Q, lane holds experts
+// lane + 64 q), by a radix select: the k-th largest key t is built bit by bit (the largest t with at
+// least k candidate keys >= t, 32 ballot counts), then the picks are the candidates above t and, of
+// those equal to t, the lowest-indexed ones up to k. That is the set the k strict-> argmax passes take
+// (larger value first, ties to the lower index); returned in ascending index order.
+template <int Q>
+__device__ inline int wave_topk_regs(const float* val, const char* cand, int E, int k, int* picks) {
+  const int lane = threadIdx.x & 63;
+  uint32_t key[Q];
+  bool c[Q];
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    const int e = lane + 64 * q;
+    c[q] = e < E && (!cand || cand[e]);
+    key[q] = c[q] ? order_key(val[e]) : 0u;  // a candidate's key is > 0 (-inf has 0x007fffff)
+  }
+  uint32_t t = 0;  // stays 0 when there are fewer than k candidates: then every candidate is above it
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t trial = t | (1u << bit);
+    int cnt = 0;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) cnt += __builtin_popcountll(__ballot(c[q] && key[q] >= trial));
+    if (cnt >= k) t = trial;
+  }
+  int gt = 0;
+#pragma unroll
+  for (int q = 0; q < Q; ++q) gt += __builtin_popcountll(__ballot(c[q] && key[q] > t));
+  const int need = k - gt;  // picks among the keys equal to t
+  const uint64_t below = (1ull << lane) - 1;
+  int n = 0, eq_before = 0;
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    const bool eq = c[q] && key[q] == t;
+    const uint64_t eqm = __ballot(eq);
+    const bool sel = (c[q] && key[q] > t) || (eq && eq_before + __builtin_popcountll(eqm & below) < need);
+    const uint64_t m = __ballot(sel);
+    if (sel) picks[n + __builtin_popcountll(m & below)] = lane + 64 * q;
+    n += __builtin_popcountll(m);
+    eq_before += __builtin_popcountll(eqm);
+  }
+  wave_sync_lds();
+  return n;
+}
+
 __device__ inline int wave_topk(const float* val, const char* cand, int E, int k, int* picks) {
+  if (E <= 64) return wave_topk_regs<1>(val, cand, E, k, picks);
+  if (E <= 128) return wave_topk_regs<2>(val, cand, E, k, picks);
+  if (E <= 256) return wave_topk_regs<4>(val, cand, E, k, picks);
   return k >= 4 ? wave_topk_rank(val, cand, E, k, picks) : wave_topk_passes(val, cand, E, k, picks);
 }
 
@@ -209,16 +266,16 @@ __device__ inline int wave_topk_passes(const float* val, const char* cand, int E
 // (nothing written) when a NaN appears in the scores, so the caller falls back to the serial scan.
 __device__ inline bool route_routed_wave(const float* row, int E, int k, int renorm, int sigmoid, const float* bias,
                                   int groups_n, int groups_top, float* s, float* c, char* cand, int* picks,
-                                  int32_t* idx_t, float* gate_t) {
+                                  int32_t* idx_t, float* gate_t, const uint64_t* tab32) {
   const int lane = threadIdx.x & 63;
   if (sigmoid) {
-    for (int e = lane; e < E; e += 64) s[e] = 1.0f / (1.0f + expf_glibc(-row[e]));
+    for (int e = lane; e < E; e += 64) s[e] = 1.0f / (1.0f + expf_glibc_t(-row[e], tab32));
   } else {
     float mx = -__builtin_inff();
     for (int e = lane; e < E; e += 64) mx = smax(mx, row[e]);
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) mx = smax(mx, __shfl_xor(mx, off, 64));
-    for (int e = lane; e < E; e += 64) s[e] = expf_glibc(row[e] - mx);
+    for (int e = lane; e < E; e += 64) s[e] = expf_glibc_t(row[e] - mx, tab32);
     wave_sync_lds();
     float z = 0.0f;
     if (lane == 0)
@@ -283,23 +340,36 @@ __device__ inline void route_token(const float* __restrict__ r, int E, int k, in
                             const float* __restrict__ bias, int groups_n, int groups_top, unsigned char* wl,
                             int32_t* __restrict__ idx_t, float* __restrict__ gate_t) {
   const int lane = threadIdx.x & 63;
-  double* ex = reinterpret_cast<double*>(wl);
-  float* s = reinterpret_cast<float*>(wl + (size_t)E * 8);
+  uint64_t* tab128 = reinterpret_cast<uint64_t*>(wl);
+  uint64_t* tab32 = tab128 + 256;
+  double* ex = reinterpret_cast<double*>(wl + kRouteTabBytes);
+  float* s = reinterpret_cast<float*>(wl + kRouteTabBytes + (size_t)E * 8);
   float* cbuf = s + E;
   int* picks = reinterpret_cast<int*>(cbuf + 2 * E);
   char* cand = reinterpret_cast<char*>(picks + 64);
   char* taken = cand + E;
   float* row = reinterpret_cast<float*>(wl + route_wave_lds(E) - (size_t)E * 4);
   bool has_nan = false;
-  for (int e = lane; e < E; e += 64) {
-    const float v = r[e];
-    row[e] = v;
-    has_nan |= (v != v);
+  {
+    // the tables and the logits in one round of loads
+    uint64_t t[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) t[i] = ember_math::kExp2Tab128[lane + 64 * i];
+    const uint64_t t32 = ember_math::kExp2Tab32[lane & 31];
+    for (int e = lane; e < E; e += 64) {
+      const float v = r[e];
+      row[e] = v;
+      has_nan |= (v != v);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) tab128[lane + 64 * i] = t[i];
+    if (lane < 32) tab32[lane] = t32;
   }
   has_nan = __any(has_nan);
   wave_sync_lds();
   if (routed && !has_nan && groups_n <= 64 &&
-      route_routed_wave(row, E, k, renorm, sigmoid, bias, groups_n, groups_top, s, cbuf, cand, picks, idx_t, gate_t))
+      route_routed_wave(row, E, k, renorm, sigmoid, bias, groups_n, groups_top, s, cbuf, cand, picks, idx_t, gate_t,
+                        tab32))
     return;
   if (routed || has_nan) {
     wave_sync_lds();
@@ -318,7 +388,7 @@ __device__ inline void route_token(const float* __restrict__ r, int E, int k, in
   if (renorm) {
     for (int j = 0; j < kk; ++j) mx = smax(mx, row[picks[j]]);
     // lane j evaluates the j-th exponential (all at once); every lane adds them in pick order
-    const double exj = lane < kk ? exp_glibc((double)(row[picks[lane]] - mx)) : 0.0;
+    const double exj = lane < kk ? exp_glibc_t((double)(row[picks[lane]] - mx), tab128) : 0.0;
     for (int j = 0; j < kk; ++j) z = z + __shfl(exj, j, 64);
     if (lane < k) {
       idx_t[lane] = lane < kk ? picks[lane] : -1;
@@ -331,7 +401,7 @@ __device__ inline void route_token(const float* __restrict__ r, int E, int k, in
     for (int e = lane; e < E; e += 64) mx = smax(mx, row[e]);
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) mx = smax(mx, __shfl_xor(mx, off, 64));
-    for (int e = lane; e < E; e += 64) ex[e] = exp_glibc((double)(row[e] - mx));
+    for (int e = lane; e < E; e += 64) ex[e] = exp_glibc_t((double)(row[e] - mx), tab128);
     wave_sync_lds();
     if (lane == 0)
       for (int e = 0; e < E; ++e) z = z + ex[e];  // ascending, as the reference sums
