@@ -3,7 +3,8 @@
 // Bit-exactness contract (reference: utils.cpp:704-836, cpu_dot.h:12-21):
 //  * logits are the FP64 fixed-order dot of the reference: eight FP64 chains over i = 8q + c,
 //    ((c0+c1)+(c2+c3)) + ((c4+c5)+(c6+c7)) + tail, rounded to f32. Products of two f32 are exact
-//    in f64, so FMA vs multiply-add cannot change a chain; the chains are kept strictly sequential.
+//    in f64, so one FMA per element rounds exactly as the reference's add of the product; the
+//    chains are kept strictly sequential.
 //  * top-k: k passes of argmax with strict > (ties to the lower index), picks sorted ascending.
 //  * gates: (float)(exp((double)(r - mx)) / z), z the ascending double sum, exp = glibc's algorithm
 //    (moe_math.hpp); the DeepSeek-style router runs the reference's float algorithm serially.
@@ -32,7 +33,7 @@ __global__ void __launch_bounds__(256) router_logits_direct(const float* __restr
   const int n8 = d - d % 8;
   double acc = 0.0;
   if (valid)
-    for (int i = c; i < n8; i += 8) acc = acc + (double)rr[i] * (double)xr[i];
+    for (int i = c; i < n8; i += 8) acc = __builtin_fma((double)rr[i], (double)xr[i], acc);
   const int lane = threadIdx.x & 63;
   const int base = lane & ~7;
   double a[8];
@@ -40,7 +41,7 @@ __global__ void __launch_bounds__(256) router_logits_direct(const float* __restr
   for (int j = 0; j < 8; ++j) a[j] = __shfl(acc, base + j, 64);
   if (valid && c == 0) {
     double tail = 0.0;
-    for (int i = n8; i < d; ++i) tail = tail + (double)rr[i] * (double)xr[i];
+    for (int i = n8; i < d; ++i) tail = __builtin_fma((double)rr[i], (double)xr[i], tail);
     const double v = (((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]))) + tail;
     logits[pair] = (float)v;
   }
@@ -75,7 +76,7 @@ __global__ void __launch_bounds__(256) router_logits_lds(const float* __restrict
   if (j < ne) {
     const float* rr = rs + j * ld;
 #pragma unroll 8
-    for (int i = c; i < n8; i += 8) acc = acc + (double)rr[i] * (double)xs[i];
+    for (int i = c; i < n8; i += 8) acc = __builtin_fma((double)rr[i], (double)xs[i], acc);
   }
   const int lane = threadIdx.x & 63;
   double a[8];
@@ -84,7 +85,7 @@ __global__ void __launch_bounds__(256) router_logits_lds(const float* __restrict
   if (j < ne && c == 0) {
     const float* rr = rs + j * ld;
     double tail = 0.0;
-    for (int i = n8; i < d; ++i) tail = tail + (double)rr[i] * (double)xs[i];
+    for (int i = n8; i < d; ++i) tail = __builtin_fma((double)rr[i], (double)xs[i], tail);
     const double v = (((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]))) + tail;
     logits[(size_t)t * E + e0 + j] = (float)v;
   }
@@ -165,7 +166,7 @@ __global__ void __launch_bounds__(256) router_logits_pt(const float* __restrict_
 #pragma unroll
         for (int j = 0; j < PE; ++j)
 #pragma unroll
-          for (int c = 0; c < 8; ++c) a[i][j][c] = a[i][j][c] + (double)rv[j][c] * (double)xv[i][c];
+          for (int c = 0; c < 8; ++c) a[i][j][c] = __builtin_fma((double)rv[j][c], (double)xv[i][c], a[i][j][c]);
     }
   }
 #pragma unroll
@@ -175,7 +176,7 @@ __global__ void __launch_bounds__(256) router_logits_pt(const float* __restrict_
       const int t = t0 + tq * PT + i, e = e0 + eq * PE + j;
       if (t >= T || e >= E) continue;
       double tail = 0.0;
-      for (int q = n8; q < d; ++q) tail = tail + (double)R[(size_t)e * d + q] * (double)x[(size_t)t * d + q];
+      for (int q = n8; q < d; ++q) tail = __builtin_fma((double)R[(size_t)e * d + q], (double)x[(size_t)t * d + q], tail);
       const double* c8 = a[i][j];
       const double v = (((c8[0] + c8[1]) + (c8[2] + c8[3])) + ((c8[4] + c8[5]) + (c8[6] + c8[7]))) + tail;
       logits[(size_t)t * E + e] = (float)v;
@@ -223,7 +224,7 @@ __global__ void __launch_bounds__(256) router_logits_tiled(const float* __restri
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = acc[i][j] + rv[j] * xv[i];
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fma(rv[j], xv[i], acc[i][j]);
     }
     __syncthreads();
   }
@@ -237,7 +238,7 @@ __global__ void __launch_bounds__(256) router_logits_tiled(const float* __restri
     if (t >= T || e >= E) continue;
     const double* a = part[p];
     double tail = 0.0;
-    for (int i = n8; i < d; ++i) tail = tail + (double)R[(size_t)e * d + i] * (double)x[(size_t)t * d + i];
+    for (int i = n8; i < d; ++i) tail = __builtin_fma((double)R[(size_t)e * d + i], (double)x[(size_t)t * d + i], tail);
     const double v = (((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]))) + tail;
     logits[(size_t)t * E + e] = (float)v;
   }
