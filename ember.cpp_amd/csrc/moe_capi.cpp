@@ -181,6 +181,8 @@ const char* ember_moe_strerror(int status) {
     case EMBER_ERR_NULL: return "null pointer";
     case EMBER_ERR_LAUNCH: return "kernel launch failed";
     case EMBER_ERR_ALIGN: return "pointer or row not 16-byte aligned";
+    case EMBER_ERR_FORMAT: return "malformed or unreadable GGUF file";
+    case EMBER_ERR_NOT_FOUND: return "no such tensor, key or MoE layer";
     default: return "unknown status";
   }
 }

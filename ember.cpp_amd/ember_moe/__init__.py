@@ -28,6 +28,7 @@ TYPE_IDS = {v: k for k, v in TYPE_NAMES.items()}
 SCORE_SOFTMAX, SCORE_SIGMOID = 0, 1
 
 OK, ERR_SHAPE, ERR_TYPE, ERR_SCRATCH, ERR_NULL, ERR_LAUNCH, ERR_ALIGN = 0, -1, -2, -3, -4, -5, -6
+ERR_FORMAT, ERR_NOT_FOUND = -7, -8
 
 
 class EmberError(RuntimeError):
@@ -58,6 +59,26 @@ class Layer(ctypes.Structure):
 
 _lib = None
 _host = None
+
+
+class GgufTensor(ctypes.Structure):
+    """ember_gguf_tensor (include/ember_gguf.h)."""
+
+    _fields_ = [("name", ctypes.c_char_p), ("type", ctypes.c_int), ("n_dims", ctypes.c_int),
+                ("ne", ctypes.c_int64 * 4), ("offset", ctypes.c_uint64), ("bytes", ctypes.c_uint64),
+                ("data", ctypes.c_void_p)]
+
+
+class GgufMoe(ctypes.Structure):
+    """ember_gguf_moe (include/ember_gguf.h)."""
+
+    _fields_ = [("layer", ctypes.c_int), ("d", ctypes.c_int), ("d_ff", ctypes.c_int), ("E", ctypes.c_int),
+                ("k", ctypes.c_int), ("renorm", ctypes.c_int), ("scoring", ctypes.c_int),
+                ("groups_n", ctypes.c_int), ("groups_top", ctypes.c_int), ("out_scale", ctypes.c_float),
+                ("d_ff_shared", ctypes.c_int),
+                ("router", GgufTensor), ("gate", GgufTensor), ("up", GgufTensor), ("down", GgufTensor),
+                ("bias", GgufTensor), ("gate_shared", GgufTensor), ("up_shared", GgufTensor),
+                ("down_shared", GgufTensor)]
 
 
 def lib_path() -> str:
@@ -91,6 +112,10 @@ def lib() -> ctypes.CDLL:
         L.ember_moe_route.restype = i
         L.ember_moe_strerror.argtypes = [i]
         L.ember_moe_strerror.restype = ctypes.c_char_p
+        L.ember_gguf_layer_bytes.argtypes = [ctypes.POINTER(GgufMoe)]
+        L.ember_gguf_layer_bytes.restype = sz
+        L.ember_gguf_upload_layer.argtypes = [ctypes.POINTER(GgufMoe), vp, sz, ctypes.POINTER(Layer), vp]
+        L.ember_gguf_upload_layer.restype = i
         _lib = L
     return _lib
 
@@ -117,6 +142,31 @@ def host() -> ctypes.CDLL:
         H.ember_f16_to_f32.restype = ctypes.c_float
         H.ember_f32_to_bf16.argtypes = [ctypes.c_float]
         H.ember_f32_to_bf16.restype = ctypes.c_uint16
+        pp = ctypes.POINTER(ctypes.c_void_p)
+        H.ember_gguf_open.argtypes = [ctypes.c_char_p, pp]
+        H.ember_gguf_open.restype = ctypes.c_int
+        H.ember_gguf_close.argtypes = [vp]
+        H.ember_gguf_close.restype = None
+        H.ember_gguf_version.argtypes = [vp]
+        H.ember_gguf_version.restype = ctypes.c_int
+        H.ember_gguf_n_tensors.argtypes = [vp]
+        H.ember_gguf_n_tensors.restype = i64
+        H.ember_gguf_tensor_at.argtypes = [vp, i64, ctypes.POINTER(GgufTensor)]
+        H.ember_gguf_tensor_at.restype = ctypes.c_int
+        H.ember_gguf_find_tensor.argtypes = [vp, ctypes.c_char_p, ctypes.POINTER(GgufTensor)]
+        H.ember_gguf_find_tensor.restype = ctypes.c_int
+        H.ember_gguf_meta_number.argtypes = [vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_double)]
+        H.ember_gguf_meta_number.restype = ctypes.c_int
+        H.ember_gguf_meta_string.argtypes = [vp, ctypes.c_char_p]
+        H.ember_gguf_meta_string.restype = ctypes.c_char_p
+        H.ember_gguf_arch.argtypes = [vp]
+        H.ember_gguf_arch.restype = ctypes.c_char_p
+        H.ember_gguf_n_layers.argtypes = [vp]
+        H.ember_gguf_n_layers.restype = ctypes.c_int
+        H.ember_gguf_moe_layer.argtypes = [vp, ctypes.c_int, ctypes.POINTER(GgufMoe)]
+        H.ember_gguf_moe_layer.restype = ctypes.c_int
+        H.ember_ggml_nbytes.argtypes = [ctypes.c_int, i64]
+        H.ember_ggml_nbytes.restype = i64
         _host = H
     return _host
 
@@ -361,3 +411,93 @@ class DeviceLayer:
         if s:
             raise EmberError(s, "ember_moe_ffn")
         return out, scratch
+
+
+# ----------------------------------------------------------------------------------------------
+# GGUF files (include/ember_gguf.h; the reader is in libember_moe_host.so, the upload in libember_moe.so)
+
+
+class Gguf:
+    """An open GGUF file (ember_gguf_open). The mapped tensor data stays valid until close()."""
+
+    def __init__(self, path: str):
+        h = ctypes.c_void_p()
+        st = host().ember_gguf_open(os.fsencode(path), ctypes.byref(h))
+        if st != OK:
+            raise EmberError(st, f"ember_gguf_open({path})")
+        self._h = h
+
+    def close(self):
+        if self._h:
+            host().ember_gguf_close(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    @property
+    def version(self) -> int:
+        return host().ember_gguf_version(self._h)
+
+    @property
+    def arch(self) -> str:
+        return host().ember_gguf_arch(self._h).decode()
+
+    @property
+    def n_layers(self) -> int:
+        return host().ember_gguf_n_layers(self._h)
+
+    def tensors(self):
+        out = []
+        for i in range(host().ember_gguf_n_tensors(self._h)):
+            t = GgufTensor()
+            st = host().ember_gguf_tensor_at(self._h, i, ctypes.byref(t))
+            if st != OK:
+                raise EmberError(st, "ember_gguf_tensor_at")
+            out.append(t)
+        return out
+
+    def find(self, name: str) -> Optional[GgufTensor]:
+        t = GgufTensor()
+        st = host().ember_gguf_find_tensor(self._h, name.encode(), ctypes.byref(t))
+        if st == ERR_NOT_FOUND:
+            return None
+        if st != OK:
+            raise EmberError(st, "ember_gguf_find_tensor")
+        return t
+
+    def tensor_bytes(self, t: GgufTensor) -> np.ndarray:
+        return np.ctypeslib.as_array(ctypes.cast(t.data, ctypes.POINTER(ctypes.c_uint8)), shape=(t.bytes,)).copy()
+
+    def number(self, key: str) -> Optional[float]:
+        v = ctypes.c_double()
+        return v.value if host().ember_gguf_meta_number(self._h, key.encode(), ctypes.byref(v)) == OK else None
+
+    def string(self, key: str) -> Optional[str]:
+        r = host().ember_gguf_meta_string(self._h, key.encode())
+        return None if r is None else r.decode()
+
+    def moe_layer(self, layer: int) -> GgufMoe:
+        m = GgufMoe()
+        st = host().ember_gguf_moe_layer(self._h, layer, ctypes.byref(m))
+        if st != OK:
+            raise EmberError(st, f"ember_gguf_moe_layer({layer})")
+        m._owner = self  # the view points into this file's mapping
+        return m
+
+
+def gguf_layer_bytes(m: GgufMoe) -> int:
+    return lib().ember_gguf_layer_bytes(ctypes.byref(m))
+
+
+def gguf_upload_layer(m: GgufMoe, dev, stream=None) -> Layer:
+    """Uploads a GGUF MoE layer into `dev` (a uint8 device tensor of at least gguf_layer_bytes(m))."""
+    L = Layer()
+    st = lib().ember_gguf_upload_layer(ctypes.byref(m), _ptr(dev), dev.numel(), ctypes.byref(L), _stream(stream))
+    if st != OK:
+        raise EmberError(st, "ember_gguf_upload_layer")
+    L._owner = dev
+    return L

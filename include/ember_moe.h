@@ -27,15 +27,12 @@
 #include <stdint.h>
 #include <hip/hip_runtime_api.h>
 #include "ember_moe_host.h"
+#include "ember_gguf.h"
 
 #ifdef __cplusplus
 extern "C" {
 #endif
 
-enum ember_moe_scoring {
-  EMBER_SCORE_SOFTMAX = 0, /* softmax of the router logits */
-  EMBER_SCORE_SIGMOID = 1  /* DeepSeek-V3 sigmoid scores (IR "scoring": "sigmoid") */
-};
 
 typedef struct ember_moe_layer {
   int d, d_ff, E, k;
@@ -91,6 +88,18 @@ int ember_moe_route(const float* logits, int T, int E, int k, int renorm, int sc
                     float* gates, int32_t* offsets, int32_t* perm, void* scratch,
                     size_t scratch_bytes, hipStream_t stream);
 
+/* Device bytes ember_gguf_upload_layer needs for a layer read by ember_gguf_moe_layer (ember_gguf.h),
+ * or 0 if the view is incomplete. */
+size_t ember_gguf_layer_bytes(const struct ember_gguf_moe* m);
+/* Copies the layer's tensors from the mapped file into `dev` (caller-owned device memory, 256-byte
+ * aligned, ember_gguf_layer_bytes long) in their GGUF encoding — the expert stacks are not dequantized,
+ * unlike the reference's MoE upload (weight_management.cpp:486-511, 1162-1176); only a non-F32 router
+ * (F16, BF16, Q8_0) is widened to F32, exactly — and fills *w with device pointers into `dev`, ready for
+ * ember_moe_ffn. Synchronises `stream` before returning (the host sources must outlive the copies).
+ * EMBER_ERR_TYPE for an encoding the FFN does not run (experts: F32, F16, BF16, Q8_0, Q4_K),
+ * EMBER_ERR_SCRATCH if dev_bytes is too small, EMBER_ERR_SHAPE if the descriptor fails validation. */
+int ember_gguf_upload_layer(const struct ember_gguf_moe* m, void* dev, size_t dev_bytes, ember_moe_layer* w,
+                            hipStream_t stream);
 /* Human-readable text for an ember_status. */
 const char* ember_moe_strerror(int status);
 

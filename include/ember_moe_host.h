@@ -24,6 +24,12 @@ enum ember_ggml_type {
   EMBER_TYPE_BF16 = 30
 };
 
+/* Router scoring of an MoE layer (ember_moe_layer.scoring, ember_gguf_moe.scoring). */
+enum ember_moe_scoring {
+  EMBER_SCORE_SOFTMAX = 0, /* softmax of the router logits */
+  EMBER_SCORE_SIGMOID = 1  /* DeepSeek-V3 sigmoid scores (IR "scoring": "sigmoid") */
+};
+
 /* Status codes shared by every entry point: 0 is success, errors are negative. */
 enum ember_status {
   EMBER_OK = 0,
@@ -32,7 +38,9 @@ enum ember_status {
   EMBER_ERR_SCRATCH = -3, /* scratch buffer missing or smaller than ember_moe_scratch_bytes */
   EMBER_ERR_NULL = -4,    /* a required pointer is NULL */
   EMBER_ERR_LAUNCH = -5,  /* a kernel launch failed (hipGetLastError) */
-  EMBER_ERR_ALIGN = -6    /* a weight pointer is not 16-byte aligned */
+  EMBER_ERR_ALIGN = -6,   /* a weight pointer is not 16-byte aligned */
+  EMBER_ERR_FORMAT = -7,  /* a malformed or unreadable GGUF file (ember_gguf.h) */
+  EMBER_ERR_NOT_FOUND = -8 /* no such tensor, key or MoE layer in the file */
 };
 
 /* n values ~ N(mean, stddev^2) from a counter-based generator: value i depends only on

@@ -41,6 +41,14 @@ def test_host_library_exports_every_declared_symbol():
     assert not missing, missing
 
 
+def test_gguf_reader_exports_every_declared_symbol():
+    names = declared("ember_gguf.h")
+    assert {"ember_gguf_open", "ember_gguf_moe_layer", "ember_gguf_find_tensor"} <= set(names)
+    missing = set(names) - exported(em.host_lib_path())
+    assert not missing, missing
+    assert {"ember_gguf_layer_bytes", "ember_gguf_upload_layer"} <= exported(em.lib_path())
+
+
 def _layer(**kw):
     L = em.Layer()
     base = dict(d=256, d_ff=512, E=8, k=2, renorm=1, scoring=0, groups_n=1, groups_top=1, out_scale=1.0,
@@ -87,5 +95,6 @@ def test_ffn_rejects_small_scratch_and_null_io():
 
 
 def test_strerror():
-    for s in (em.OK, em.ERR_SHAPE, em.ERR_TYPE, em.ERR_SCRATCH, em.ERR_NULL, em.ERR_LAUNCH, em.ERR_ALIGN):
+    for s in (em.OK, em.ERR_SHAPE, em.ERR_TYPE, em.ERR_SCRATCH, em.ERR_NULL, em.ERR_LAUNCH, em.ERR_ALIGN,
+              em.ERR_FORMAT, em.ERR_NOT_FOUND):
         assert em.strerror(s) and em.strerror(s) != "unknown status"
