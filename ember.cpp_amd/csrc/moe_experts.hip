@@ -333,8 +333,13 @@ int launch_proj_cfg(const ProjArgs& a_in, size_t act_lds, hipStream_t st) {
 template <int FMT, int MT, bool GATED>
 int launch_proj_mt(const ProjArgs& a, size_t lds, hipStream_t st) {
   // two register buffers, 512-thread blocks, four waves per SIMD (measured best of the ring depths
-  // 2-4 and block sizes 256 / 512 on MI355X for the Mixtral / Qwen / DeepSeek layer shapes)
-  return launch_proj_cfg<FMT, MT, GATED, 2, 512, 4>(a, lds, st);
+  // 2-4 and block sizes 256 / 512 on MI355X for the Mixtral / Qwen / DeepSeek layer shapes); the
+  // two-token gate/up pass needs more than the 128 registers four waves leave (it spilled), and runs
+  // best at three waves per SIMD in 256-thread blocks (C2 T = 2 / 4: -6 % / -4 %)
+  if constexpr (GATED && MT >= 2)
+    return launch_proj_cfg<FMT, MT, GATED, 2, 256, 3>(a, lds, st);
+  else
+    return launch_proj_cfg<FMT, MT, GATED, 2, 512, 4>(a, lds, st);
 }
 
 template <int FMT, bool GATED>
