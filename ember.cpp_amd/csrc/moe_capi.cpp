@@ -110,6 +110,7 @@ RouteLayout route_layout(int T, int E, int k, size_t base) {
 }
 
 struct Layout {
+  size_t flag;  // the fused routing's flag words (ProjArgs::Route), at a fixed place: offset 0
   size_t logits, idx, gates, offsets, perm, h, y, hs, ys;
   size_t x16, h16, hs16, tiles, n_tiles;  // MFMA paths
   int mode, mode_shared;                  // PathMode of the routed experts and of the shared expert
@@ -120,6 +121,7 @@ Layout layout(const ember_moe_layer* w, int T) {
   Layout l;
   const size_t slots = (size_t)T * w->k;
   size_t o = 0;
+  l.flag = o; o = align_up(o + (size_t)8 * (w->E + 1));
   l.logits = o; o = align_up(o + (size_t)T * w->E * 4);
   l.idx = o; o = align_up(o + slots * 4);
   l.gates = o; o = align_up(o + slots * 4);
@@ -224,11 +226,16 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
   const int groups_n = std::max(w->groups_n, 1), groups_top = std::max(w->groups_top, 1);
   const int renorm = w->renorm ? 1 : 0, routed = is_routed(w) ? 1 : 0;
   const int sigmoid = w->scoring == EMBER_SCORE_SIGMOID ? 1 : 0;
+  // one token on the decode path: the router, the routing and the dispatch run inside the gate/up launch
+  // (its block 0 publishes them; the other blocks wait), saving two launches on the latency path
+  static const bool fuse_ok = [] { const char* v = std::getenv("EMBER_FUSE_ROUTE"); return !(v && atoi(v) == 0); }();
+  const bool fuse_route = fuse_ok && l.mode == kGemv && T == 1 && k <= 64 && fused_route_fits(d, E);
+  auto* flag = at<unsigned long long>(scratch, l.flag);
   mark(ev, 0, st);
-  if ((s = launch_router_logits(x, T, d, E, w->router, logits, st))) return s;
+  if (!fuse_route && (s = launch_router_logits(x, T, d, E, w->router, logits, st))) return s;
   mark(ev, 1, st);
-  if ((s = launch_route_dispatch(logits, T, E, k, renorm, routed, sigmoid, w->selection_bias, groups_n, groups_top,
-                                 idx, gates, ds, st)))
+  if (!fuse_route && (s = launch_route_dispatch(logits, T, E, k, renorm, routed, sigmoid, w->selection_bias, groups_n,
+                                                groups_top, idx, gates, ds, st)))
     return s;
   mark(ev, 2, st);
   mark(ev, 3, st);
@@ -320,8 +327,33 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
       a.ev_stop = kev[1];
       *kev_used = true;
     }
+    if (fuse_route) {
+      ProjArgs::Route& r = a.route;
+      r.flag = flag;
+      r.x = x;
+      r.router = w->router;
+      r.d = d;
+      r.E = E;
+      r.renorm = renorm;
+      r.routed = routed;
+      r.sigmoid = sigmoid;
+      r.groups_n = groups_n;
+      r.groups_top = groups_top;
+      r.bias = w->selection_bias;
+      r.logits = logits;
+      r.idx = idx;
+      r.gates = gates;
+      r.pos = ds.pos;
+      r.offsets = offsets;
+      r.used = ds.used;
+      r.n_used = ds.n_used;
+      r.perm = perm;
+    }
     if ((s = launch_projection(a, st))) return s;
     mark(ev, 4, st);
+    a.route = ProjArgs::Route{};
+    a.clear_flag = fuse_route ? flag : nullptr;  // the down launch resets the flag words for the next call
+    a.clear_n = E + 1;
     a.type = w->down_type;
     a.gated = false;
     a.w0 = w->down;

@@ -25,6 +25,7 @@
 #include <hip/hip_ext.h>
 
 #include "moe_fmt.hpp"
+#include "moe_route_dev.hpp"
 
 namespace ember_moe {
 using namespace ember_math;
@@ -288,22 +289,188 @@ __device__ inline void proj_body(const ProjArgs& a, const Dispatch& dp, const Se
   }
 }
 
-template <int FMT, int MT, bool GATED, int NB, int NT, int WPE>
-__global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) proj_kernel(ProjArgs a) {
-  Dispatch dp{a.used ? *a.n_used : 0, a.used, a.offsets, a.perm};
-  SegView v;
-  const bool active = seg_view<GATED, MT>(a, dp, blockIdx.x, gridDim.x, v);
-  if (active) proj_body<FMT, MT, GATED, NB, NT>(a, dp, v);
+// ---- routing fused into a one-token gate/up launch (ProjArgs::route)
+// Words of the flag area: [0] the dispatch is published (kRouteReady); [1 + e] expert e's logit,
+// tagged: kLogitTag in the high half, the f32 bits in the low half.
+constexpr int kFusedMaxK = 64;
+constexpr uint32_t kLogitTag = 0x10617ed5u;
+// LDS bytes of a router block (x and the router row as f32, the products as f64) and of block 0's
+// routing (logits, picks, gates, one routing wave's work area)
+__host__ __device__ inline size_t fused_router_lds(int d) { return (size_t)16 * d + 256; }
+__host__ __device__ inline size_t fused_route_lds(int E) { return 2048 + 512 + route_wave_lds(E); }
+
+// Router block e (blocks 0..E-1): the logit of expert e as the reference computes it (cpu_dot.h:
+// eight FP64 chains over i = 8q + c, combined ((c0+c1)+(c2+c3))+((c4+c5)+(c6+c7)), plus the tail).
+// x and the router row are staged in LDS, every product (exact in f64) is formed in parallel and
+// stored chain-major, then eight lanes add their chain's products in order, which is the same
+// rounding sequence as acc += (double)r * (double)x. Returns the logit in thread 0.
+template <int NT>
+__device__ float router_block_logit(const ProjArgs& a, int e, uint8_t* lds) {
+  const ProjArgs::Route& r = a.route;
+  const int t = threadIdx.x, d = r.d, n8 = d - d % 8, nq = n8 / 8;
+  float* xs = reinterpret_cast<float*>(lds);
+  float* rs = xs + d;
+  double* pd = reinterpret_cast<double*>(lds + (((size_t)8 * d + 15) & ~(size_t)15));
+  const float* row = r.router + (size_t)e * d;
+  for (int i = t; i < d; i += NT) {
+    xs[i] = r.x[i];
+    rs[i] = row[i];
+  }
+  __syncthreads();
+  for (int i = t; i < n8; i += NT) pd[(i & 7) * nq + (i >> 3)] = (double)rs[i] * (double)xs[i];
+  __syncthreads();
+  double acc = 0.0;
+  if (t < 8) {
+    const double* p = pd + (size_t)t * nq;
+#pragma unroll 16
+    for (int q = 0; q < nq; ++q) acc = acc + p[q];
+  }
+  double c[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) c[j] = __shfl(acc, j, 64);
+  float v = 0.0f;
+  if (t == 0) {
+    double tail = 0.0;
+    for (int i = n8; i < d; ++i) tail = __builtin_fma((double)rs[i], (double)xs[i], tail);
+    v = (float)((((c[0] + c[1]) + (c[2] + c[3])) + ((c[4] + c[5]) + (c[6] + c[7]))) + tail);
+  }
+  __syncthreads();  // the staging area is reused by the caller
+  return v;
 }
 
-template <int FMT, int MT, bool GATED, int NB, int NT, int WPE>
+// Block 0 after its own logit: collects every expert's tagged logit (bounded wait), runs route_token
+// (the picks and gates) and the one-token dispatch (picks are ascending and distinct, so the stable
+// sort by expert is the identity), writes them out and into the block's arrays, then publishes.
+// Returns false when a logit never arrived (the block then does nothing; the layer is not computed).
+template <int NT>
+__device__ bool route_block(const ProjArgs& a, uint8_t* lds, int32_t* s_off, int32_t* s_used, int32_t* s_n,
+                            int32_t* s_perm) {
+  __shared__ int missing;
+  const ProjArgs::Route& r = a.route;
+  const int t = threadIdx.x;
+  float* lg = reinterpret_cast<float*>(lds);
+  int32_t* pidx = reinterpret_cast<int32_t*>(lds + 2048);
+  float* pgate = reinterpret_cast<float*>(lds + 2048 + 256);
+  uint8_t* wl = lds + 2048 + 512;
+  const int E = r.E, k = a.k;
+  if (t == 0) missing = 0;
+  __syncthreads();
+  for (int e = t; e < E; e += NT) {
+    unsigned long long w;
+    unsigned n = 0;
+    while (((w = __hip_atomic_load(r.flag + 1 + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) >> 32) != kLogitTag) {
+      if (++n > (1u << 22)) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    if ((w >> 32) != kLogitTag) missing = 1;
+    lg[e] = __builtin_bit_cast(float, (uint32_t)w);
+  }
+  __syncthreads();
+  if (missing) return false;
+  if (t < 64)
+    route_token(lg, E, k, r.renorm, r.routed, r.sigmoid, r.bias, r.groups_n, r.groups_top, wl, pidx, pgate);
+  __syncthreads();
+  int nv = 0;  // valid picks: a prefix (route_token puts the -1 entries last)
+  for (int j = 0; j < k; ++j) nv += pidx[j] >= 0;
+  if (t < k) {
+    r.idx[t] = pidx[t];
+    r.gates[t] = pgate[t];
+    r.pos[t] = t < nv ? t : -1;
+  }
+  if (t < nv) {
+    r.used[t] = s_used[t] = pidx[t];
+    r.perm[t] = s_perm[t] = t;
+  }
+  for (int e = t; e <= E; e += NT) {
+    int cnt = 0;
+    for (int j = 0; j < nv; ++j) cnt += pidx[j] < e;
+    r.offsets[e] = s_off[e] = cnt;
+  }
+  if (t == 0) *r.n_used = *s_n = nv;
+  __syncthreads();
+  if (t == 0) {
+    __threadfence();  // every store above reaches the device-wide coherence point before the flag
+    __hip_atomic_store(r.flag, kRouteReady, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  return true;
+}
+
+// The other blocks: wait for the flag (bounded: a block that gives up does nothing, it never hangs),
+// then copy the dispatch into the block's arrays with device-coherent loads. Returns false on give-up.
+__device__ inline bool route_wait(const ProjArgs& a, int32_t* s_off, int32_t* s_used, int32_t* s_n,
+                                  int32_t* s_perm) {
+  __shared__ int ok_s;
+  const ProjArgs::Route& r = a.route;
+  if (threadIdx.x == 0) {
+    int ok = 1;
+    unsigned n = 0;
+    while (__hip_atomic_load(r.flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != kRouteReady) {
+      if (++n > (1u << 22)) {
+        ok = 0;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+    ok_s = ok;
+  }
+  __syncthreads();
+  if (!ok_s) return false;
+  auto ld = [](const int32_t* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+  const int t = threadIdx.x;
+  const int nv = ld(r.n_used);
+  for (int e = t; e <= r.E; e += blockDim.x) s_off[e] = ld(r.offsets + e);
+  if (t < nv) {
+    s_used[t] = ld(r.used + t);
+    s_perm[t] = ld(r.perm + t);
+  }
+  if (t == 0) *s_n = nv;
+  __syncthreads();
+  return true;
+}
+
+template <int FMT, int MT, bool GATED, int NB, int NT, int WPE, bool ROUTE>
+__global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) proj_kernel(ProjArgs a) {
+  if (a.clear_flag && blockIdx.x == 0)
+    for (int i = threadIdx.x; i < a.clear_n; i += NT)
+      __hip_atomic_store(a.clear_flag + i, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if constexpr (ROUTE) {
+    extern __shared__ __align__(16) uint8_t act_lds[];
+    __shared__ int32_t s_off[kMaxRouteE + 1], s_used[kFusedMaxK], s_perm[kFusedMaxK], s_n;
+    const int b = blockIdx.x;
+    if (b < a.route.E) {  // router block: its expert's logit, published tagged
+      const float v = router_block_logit<NT>(a, b, act_lds);
+      if (threadIdx.x == 0) {
+        a.route.logits[b] = v;
+        __hip_atomic_store(a.route.flag + 1 + b, ((unsigned long long)kLogitTag << 32) | __builtin_bit_cast(uint32_t, v),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    if (b == 0) {
+      if (!route_block<NT>(a, act_lds, s_off, s_used, &s_n, s_perm)) return;
+    } else if (!route_wait(a, s_off, s_used, &s_n, s_perm)) {
+      return;
+    }
+    __syncthreads();  // block 0: its routing work area (act_lds) is free for the activations
+    Dispatch dp{s_n, s_used, s_off, s_perm};
+    SegView v;
+    if (seg_view<GATED, MT>(a, dp, blockIdx.x, gridDim.x, v)) proj_body<FMT, MT, GATED, NB, NT>(a, dp, v);
+  } else {
+    Dispatch dp{a.used ? *a.n_used : 0, a.used, a.offsets, a.perm};
+    SegView v;
+    const bool active = seg_view<GATED, MT>(a, dp, blockIdx.x, gridDim.x, v);
+    if (active) proj_body<FMT, MT, GATED, NB, NT>(a, dp, v);
+  }
+}
+
+template <int FMT, int MT, bool GATED, int NB, int NT, int WPE, bool ROUTE = false>
 int launch_proj_cfg(const ProjArgs& a_in, size_t act_lds, hipStream_t st) {
-  const void* fn = reinterpret_cast<const void*>(&proj_kernel<FMT, MT, GATED, NB, NT, WPE>);
+  const void* fn = reinterpret_cast<const void*>(&proj_kernel<FMT, MT, GATED, NB, NT, WPE, ROUTE>);
   static const bool attr_ok =
       hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kProjLdsBytes) == hipSuccess;
   if (!attr_ok) return EMBER_ERR_LAUNCH;
   const ProjArgs& a = a_in;
-  const size_t lds = act_lds;
+  const size_t lds =
+      ROUTE ? std::max(act_lds, std::max(fused_route_lds(a.route.E), fused_router_lds(a.route.d))) : act_lds;
   // blocks per CU at this LDS size (cached per size; the launch is sized to one resident wave of blocks)
   static size_t cached_lds = (size_t)-1;
   static int cached_bpc = 1;
@@ -320,12 +487,13 @@ int launch_proj_cfg(const ProjArgs& a_in, size_t act_lds, hipStream_t st) {
   static const int bpc_override = [] { const char* e = std::getenv("EMBER_PROJ_BPC"); return e ? atoi(e) : 0; }();
   const int bpc = bpc_override > 0 ? std::min(bpc_override, cached_bpc) : cached_bpc;
   const int segs = (a.used ? std::max(a.max_segments, 1) : 0) + (a.s_w0 ? 1 : 0);
-  const int G = std::max(cus * bpc, segs);
+  const int G = std::max(std::max(cus * bpc, segs), ROUTE ? a.route.E : 0);
+  if (ROUTE && a.route.E > cus) return EMBER_ERR_SHAPE;  // the router blocks could not all be resident
   if (a.ev_start) {
-    hipExtLaunchKernelGGL(proj_kernel<FMT, MT, GATED, NB, NT, WPE>, dim3(G), dim3(NT), lds, st, a.ev_start, a.ev_stop,
-                          0, a);
+    hipExtLaunchKernelGGL(proj_kernel<FMT, MT, GATED, NB, NT, WPE, ROUTE>, dim3(G), dim3(NT), lds, st, a.ev_start,
+                          a.ev_stop, 0, a);
   } else {
-    proj_kernel<FMT, MT, GATED, NB, NT, WPE><<<G, NT, lds, st>>>(a);
+    proj_kernel<FMT, MT, GATED, NB, NT, WPE, ROUTE><<<G, NT, lds, st>>>(a);
   }
   return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
 }
@@ -354,6 +522,11 @@ int launch_proj_fmt(const ProjArgs& a, hipStream_t st) {
   int MT = a.T <= 1 ? 1 : (a.T <= 2 || GATED ? 2 : 4);
   while (MT > 1 && MT * row_lds > kProjLdsBytes) MT >>= 1;
   const size_t lds = (size_t)MT * row_lds;
+  if (a.route.flag) {  // routing fused into a one-token gate/up launch
+    if (!GATED || a.T != 1 || a.k > kFusedMaxK || a.route.E > kMaxRouteE || !fused_route_fits(a.route.d, a.route.E))
+      return EMBER_ERR_SHAPE;
+    if constexpr (GATED) return launch_proj_cfg<FMT, 1, GATED, 2, 512, 4, true>(a, (size_t)row_lds, st);
+  }
   if (MT == 1) return launch_proj_mt<FMT, 1, GATED>(a, lds, st);
   if (MT == 2) return launch_proj_mt<FMT, 2, GATED>(a, lds, st);
   return launch_proj_mt<FMT, 4, GATED>(a, lds, st);
@@ -376,6 +549,12 @@ int launch_projection(const ProjArgs& a, hipStream_t st) {
 }
 
 int proj_max_row_bytes() { return kProjLdsBytes; }
+
+// The router blocks (0..E-1) must be resident together with block 0, which waits for them while they
+// wait for it: at most one block per CU is assumed (MI355X: 256 CUs), so E <= 256.
+bool fused_route_fits(int d, int E) {
+  return E <= 256 && fused_router_lds(d) <= (size_t)kProjLdsBytes && fused_route_lds(E) <= (size_t)kProjLdsBytes;
+}
 
 bool type_quantizes_activations(int type) { return type == EMBER_TYPE_Q8_0 || type == EMBER_TYPE_Q4_K; }
 

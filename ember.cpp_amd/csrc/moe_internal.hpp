@@ -82,7 +82,31 @@ struct ProjArgs {
   int T;
   // host side only: when set, the launch records these events in its dispatch packet (kernel timing)
   hipEvent_t ev_start, ev_stop;
+  // Routing fused into a one-token gate/up launch (route.flag non-null): blocks 0..E-1 each compute
+  // one expert's router logit and publish it tagged in flag[1 + e]; block 0 collects them, computes the
+  // picks, gates and dispatch (offsets, used, n_used, perm, pos) and publishes them by setting flag[0]
+  // to kRouteReady; every block waits for that. A later launch of the same call (clear_flag) zeroes
+  // the E + 1 words, so stale words never look ready (a word of uninitialised scratch matches a tag
+  // by chance with probability 2^-32 per expert, 2^-64 for flag[0]).
+  struct Route {
+    unsigned long long* flag;
+    const float* x;       // the token [d]
+    const float* router;  // [E][d]
+    int d, E, renorm, routed, sigmoid, groups_n, groups_top;
+    const float* bias;
+    float* logits;        // [E]
+    int32_t* idx;         // [k]
+    float* gates;         // [k]
+    int32_t* pos;         // [k]
+    int32_t *offsets, *used, *n_used, *perm;  // the dispatch (the launch's read-only views alias these)
+  } route;
+  unsigned long long* clear_flag;  // non-null: block 0 of this launch zeroes clear_n words of the flag area
+  int clear_n;
 };
+// the fused routing's shape limits (the router blocks' and block 0's LDS)
+bool fused_route_fits(int d, int E);
+constexpr unsigned long long kRouteReady = 0x5e11a7ed0ddba11full;
+constexpr int kMaxRouteE = 512;  // experts a fused routing block handles
 
 int launch_projection(const ProjArgs& a, hipStream_t st);
 
