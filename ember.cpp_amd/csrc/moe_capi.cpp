@@ -121,7 +121,7 @@ Layout layout(const ember_moe_layer* w, int T) {
   Layout l;
   const size_t slots = (size_t)T * w->k;
   size_t o = 0;
-  l.flag = o; o = align_up(o + (size_t)8 * (w->E + 1));
+  l.flag = o; o = align_up(o + (size_t)8 * (w->E + 2));
   l.logits = o; o = align_up(o + (size_t)T * w->E * 4);
   l.idx = o; o = align_up(o + slots * 4);
   l.gates = o; o = align_up(o + slots * 4);
@@ -229,7 +229,7 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
   // one token on the decode path: the router, the routing and the dispatch run inside the gate/up launch
   // (its block 0 publishes them; the other blocks wait), saving two launches on the latency path
   static const bool fuse_ok = [] { const char* v = std::getenv("EMBER_FUSE_ROUTE"); return !(v && atoi(v) == 0); }();
-  const bool fuse_route = fuse_ok && l.mode == kGemv && T == 1 && k <= 64 && fused_route_fits(d, E);
+  const bool fuse_route = fuse_ok && l.mode == kGemv && T == 1 && fused_route_fits(d, E, k);
   auto* flag = at<unsigned long long>(scratch, l.flag);
   mark(ev, 0, st);
   if (!fuse_route && (s = launch_router_logits(x, T, d, E, w->router, logits, st))) return s;
@@ -353,7 +353,7 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     mark(ev, 4, st);
     a.route = ProjArgs::Route{};
     a.clear_flag = fuse_route ? flag : nullptr;  // the down launch resets the flag words for the next call
-    a.clear_n = E + 1;
+    a.clear_n = E + 2;
     a.type = w->down_type;
     a.gated = false;
     a.w0 = w->down;

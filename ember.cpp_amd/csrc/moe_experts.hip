@@ -290,34 +290,55 @@ __device__ inline void proj_body(const ProjArgs& a, const Dispatch& dp, const Se
 }
 
 // ---- routing fused into a one-token gate/up launch (ProjArgs::route)
-// Words of the flag area: [0] the dispatch is published (kRouteReady); [1 + e] expert e's logit,
-// tagged: kLogitTag in the high half, the f32 bits in the low half.
-constexpr int kFusedMaxK = 64;
+// Words of the flag area: [0], [1] the picks (expert ids 0..254 as bytes, 0xff: none; four per word)
+// under kPickTag[0] / kPickTag[1] in the high half; [2 + e] expert e's logit under kLogitTag (the f32
+// bits in the low half). A word is read with one device-coherent load and carries its own data, so
+// no ordering between a payload and a flag is needed.
+constexpr int kFusedMaxK = 8;
 constexpr uint32_t kLogitTag = 0x10617ed5u;
-// LDS bytes of a router block (x and the router row as f32, the products as f64) and of block 0's
-// routing (logits, picks, gates, one routing wave's work area)
-__host__ __device__ inline size_t fused_router_lds(int d) { return (size_t)16 * d + 256; }
+constexpr uint32_t kPickTag[2] = {0x91c5a11du, 0x91c5b22eu};
+// LDS of a router block (the products, f64, chain-major) and, after it, block 0's routing area
+// (logits, picks, gates, one routing wave's work area)
+__host__ __device__ inline size_t fused_router_lds(int d) { return (size_t)8 * d + 256; }
 __host__ __device__ inline size_t fused_route_lds(int E) { return 2048 + 512 + route_wave_lds(E); }
 
 // Router block e (blocks 0..E-1): the logit of expert e as the reference computes it (cpu_dot.h:
 // eight FP64 chains over i = 8q + c, combined ((c0+c1)+(c2+c3))+((c4+c5)+(c6+c7)), plus the tail).
-// x and the router row are staged in LDS, every product (exact in f64) is formed in parallel and
-// stored chain-major, then eight lanes add their chain's products in order, which is the same
-// rounding sequence as acc += (double)r * (double)x. Returns the logit in thread 0.
+// Every product (exact in f64) is formed from one round of 16-byte loads and stored chain-major, then
+// eight lanes add their chain's products in order — the rounding sequence of acc += (double)r * (double)x.
+// Returns the logit in thread 0.
 template <int NT>
 __device__ float router_block_logit(const ProjArgs& a, int e, uint8_t* lds) {
   const ProjArgs::Route& r = a.route;
   const int t = threadIdx.x, d = r.d, n8 = d - d % 8, nq = n8 / 8;
-  float* xs = reinterpret_cast<float*>(lds);
-  float* rs = xs + d;
-  double* pd = reinterpret_cast<double*>(lds + (((size_t)8 * d + 15) & ~(size_t)15));
+  double* pd = reinterpret_cast<double*>(lds);
   const float* row = r.router + (size_t)e * d;
-  for (int i = t; i < d; i += NT) {
-    xs[i] = r.x[i];
-    rs[i] = row[i];
+  if (d % 4 == 0) {
+    constexpr int PER = 4;  // float4s per thread: d <= 16 * NT
+    const int n4 = n8 / 4;
+    const float4* x4 = reinterpret_cast<const float4*>(r.x);
+    const float4* r4 = reinterpret_cast<const float4*>(row);
+    float4 xv[PER], rv[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int i4 = min(t + j * NT, n4 - 1);
+      xv[j] = x4[i4];
+      rv[j] = r4[i4];
+    }
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int i4 = t + j * NT;
+      if (i4 < n4) {
+        const int c0 = (4 * i4) & 7, q = i4 >> 1;
+        pd[(c0 + 0) * nq + q] = (double)rv[j].x * (double)xv[j].x;
+        pd[(c0 + 1) * nq + q] = (double)rv[j].y * (double)xv[j].y;
+        pd[(c0 + 2) * nq + q] = (double)rv[j].z * (double)xv[j].z;
+        pd[(c0 + 3) * nq + q] = (double)rv[j].w * (double)xv[j].w;
+      }
+    }
+  } else {
+    for (int i = t; i < n8; i += NT) pd[(i & 7) * nq + (i >> 3)] = (double)row[i] * (double)r.x[i];
   }
-  __syncthreads();
-  for (int i = t; i < n8; i += NT) pd[(i & 7) * nq + (i >> 3)] = (double)rs[i] * (double)xs[i];
   __syncthreads();
   double acc = 0.0;
   if (t < 8) {
@@ -331,34 +352,51 @@ __device__ float router_block_logit(const ProjArgs& a, int e, uint8_t* lds) {
   float v = 0.0f;
   if (t == 0) {
     double tail = 0.0;
-    for (int i = n8; i < d; ++i) tail = __builtin_fma((double)rs[i], (double)xs[i], tail);
+    for (int i = n8; i < d; ++i) tail = __builtin_fma((double)row[i], (double)r.x[i], tail);
     v = (float)((((c[0] + c[1]) + (c[2] + c[3])) + ((c[4] + c[5]) + (c[6] + c[7]))) + tail);
   }
-  __syncthreads();  // the staging area is reused by the caller
+  __syncthreads();  // the products area is reused by the caller
   return v;
 }
 
+// The one-token dispatch from the picks (ascending, distinct, nv valid): used = the picks, perm the
+// identity (a stable sort of the slots by expert), offsets[e] = picks below e.
+__device__ inline void fused_dispatch(const int* picks, int nv, int E, int32_t* s_off, int32_t* s_used, int32_t* s_n,
+                                      int32_t* s_perm) {
+  const int t = threadIdx.x;
+  if (t < nv) {
+    s_used[t] = picks[t];
+    s_perm[t] = t;
+  }
+  for (int e = t; e <= E; e += blockDim.x) {
+    int cnt = 0;
+    for (int j = 0; j < nv; ++j) cnt += picks[j] < e;
+    s_off[e] = cnt;
+  }
+  if (t == 0) *s_n = nv;
+}
+
 // Block 0 after its own logit: collects every expert's tagged logit (bounded wait), runs route_token
-// (the picks and gates) and the one-token dispatch (picks are ascending and distinct, so the stable
-// sort by expert is the identity), writes them out and into the block's arrays, then publishes.
-// Returns false when a logit never arrived (the block then does nothing; the layer is not computed).
+// (exp tables staged at the start of the launch), writes the routing and dispatch for the later
+// launches, publishes the picks and fills the block's dispatch arrays. False: a logit never arrived
+// (the block then does nothing; the layer is not computed).
 template <int NT>
-__device__ bool route_block(const ProjArgs& a, uint8_t* lds, int32_t* s_off, int32_t* s_used, int32_t* s_n,
+__device__ bool route_block(const ProjArgs& a, uint8_t* ra, int32_t* s_off, int32_t* s_used, int32_t* s_n,
                             int32_t* s_perm) {
   __shared__ int missing;
   const ProjArgs::Route& r = a.route;
   const int t = threadIdx.x;
-  float* lg = reinterpret_cast<float*>(lds);
-  int32_t* pidx = reinterpret_cast<int32_t*>(lds + 2048);
-  float* pgate = reinterpret_cast<float*>(lds + 2048 + 256);
-  uint8_t* wl = lds + 2048 + 512;
+  float* lg = reinterpret_cast<float*>(ra);
+  int32_t* pidx = reinterpret_cast<int32_t*>(ra + 2048);
+  float* pgate = reinterpret_cast<float*>(ra + 2048 + 256);
+  uint8_t* wl = ra + 2048 + 512;
   const int E = r.E, k = a.k;
   if (t == 0) missing = 0;
   __syncthreads();
   for (int e = t; e < E; e += NT) {
     unsigned long long w;
     unsigned n = 0;
-    while (((w = __hip_atomic_load(r.flag + 1 + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) >> 32) != kLogitTag) {
+    while (((w = __hip_atomic_load(r.flag + 2 + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) >> 32) != kLogitTag) {
       if (++n > (1u << 22)) break;
       __builtin_amdgcn_s_sleep(1);
     }
@@ -368,62 +406,74 @@ __device__ bool route_block(const ProjArgs& a, uint8_t* lds, int32_t* s_off, int
   __syncthreads();
   if (missing) return false;
   if (t < 64)
-    route_token(lg, E, k, r.renorm, r.routed, r.sigmoid, r.bias, r.groups_n, r.groups_top, wl, pidx, pgate);
+    route_token(lg, E, k, r.renorm, r.routed, r.sigmoid, r.bias, r.groups_n, r.groups_top, wl, pidx, pgate, true);
   __syncthreads();
   int nv = 0;  // valid picks: a prefix (route_token puts the -1 entries last)
   for (int j = 0; j < k; ++j) nv += pidx[j] >= 0;
+  if (t < 2) {
+    uint32_t lo = 0;
+    for (int j = 0; j < 4; ++j) {
+      const int q = 4 * t + j;
+      lo |= (uint32_t)(q < nv ? pidx[q] : 0xff) << (8 * j);
+    }
+    __hip_atomic_store(r.flag + t, ((unsigned long long)kPickTag[t] << 32) | lo, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  }
   if (t < k) {
     r.idx[t] = pidx[t];
     r.gates[t] = pgate[t];
     r.pos[t] = t < nv ? t : -1;
   }
   if (t < nv) {
-    r.used[t] = s_used[t] = pidx[t];
-    r.perm[t] = s_perm[t] = t;
+    r.used[t] = pidx[t];
+    r.perm[t] = t;
   }
   for (int e = t; e <= E; e += NT) {
     int cnt = 0;
     for (int j = 0; j < nv; ++j) cnt += pidx[j] < e;
-    r.offsets[e] = s_off[e] = cnt;
+    r.offsets[e] = cnt;
   }
-  if (t == 0) *r.n_used = *s_n = nv;
+  if (t == 0) *r.n_used = nv;
+  fused_dispatch(pidx, nv, E, s_off, s_used, s_n, s_perm);
   __syncthreads();
-  if (t == 0) {
-    __threadfence();  // every store above reaches the device-wide coherence point before the flag
-    __hip_atomic_store(r.flag, kRouteReady, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
   return true;
 }
 
-// The other blocks: wait for the flag (bounded: a block that gives up does nothing, it never hangs),
-// then copy the dispatch into the block's arrays with device-coherent loads. Returns false on give-up.
-__device__ inline bool route_wait(const ProjArgs& a, int32_t* s_off, int32_t* s_used, int32_t* s_n,
-                                  int32_t* s_perm) {
+// The other blocks: wait for both pick words (bounded: a block that gives up does nothing, it never
+// hangs), then build the dispatch from them. Returns false on give-up.
+__device__ inline bool route_wait(const ProjArgs& a, int32_t* s_off, int32_t* s_used, int32_t* s_n, int32_t* s_perm) {
   __shared__ int ok_s;
+  __shared__ int picks[kFusedMaxK];
+  __shared__ int nv_s;
   const ProjArgs::Route& r = a.route;
   if (threadIdx.x == 0) {
     int ok = 1;
     unsigned n = 0;
-    while (__hip_atomic_load(r.flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != kRouteReady) {
+    unsigned long long w0, w1;
+    for (;;) {
+      w0 = __hip_atomic_load(r.flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      w1 = __hip_atomic_load(r.flag + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if ((w0 >> 32) == kPickTag[0] && (w1 >> 32) == kPickTag[1]) break;
       if (++n > (1u << 22)) {
         ok = 0;
         break;
       }
       __builtin_amdgcn_s_sleep(2);
     }
+    int nv = 0;
+    for (int j = 0; j < kFusedMaxK; ++j) {
+      const int p = (int)(((j < 4 ? w0 : w1) >> (8 * (j & 3))) & 0xff);
+      if (p != 0xff && nv == j) {
+        picks[j] = p;
+        ++nv;
+      }
+    }
+    nv_s = nv;
     ok_s = ok;
   }
   __syncthreads();
   if (!ok_s) return false;
-  auto ld = [](const int32_t* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
-  const int t = threadIdx.x;
-  const int nv = ld(r.n_used);
-  for (int e = t; e <= r.E; e += blockDim.x) s_off[e] = ld(r.offsets + e);
-  if (t < nv) {
-    s_used[t] = ld(r.used + t);
-    s_perm[t] = ld(r.perm + t);
-  }
-  if (t == 0) *s_n = nv;
+  fused_dispatch(picks, nv_s, a.route.E, s_off, s_used, s_n, s_perm);
   __syncthreads();
   return true;
 }
@@ -437,16 +487,18 @@ __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) 
     extern __shared__ __align__(16) uint8_t act_lds[];
     __shared__ int32_t s_off[kMaxRouteE + 1], s_used[kFusedMaxK], s_perm[kFusedMaxK], s_n;
     const int b = blockIdx.x;
+    uint8_t* ra = act_lds + fused_router_lds(a.route.d);  // block 0's routing area, after the products
+    if (b == 0 && threadIdx.x < 64) route_stage_tables(ra + 2048 + 512);
     if (b < a.route.E) {  // router block: its expert's logit, published tagged
       const float v = router_block_logit<NT>(a, b, act_lds);
       if (threadIdx.x == 0) {
         a.route.logits[b] = v;
-        __hip_atomic_store(a.route.flag + 1 + b, ((unsigned long long)kLogitTag << 32) | __builtin_bit_cast(uint32_t, v),
+        __hip_atomic_store(a.route.flag + 2 + b, ((unsigned long long)kLogitTag << 32) | __builtin_bit_cast(uint32_t, v),
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
     if (b == 0) {
-      if (!route_block<NT>(a, act_lds, s_off, s_used, &s_n, s_perm)) return;
+      if (!route_block<NT>(a, ra, s_off, s_used, &s_n, s_perm)) return;
     } else if (!route_wait(a, s_off, s_used, &s_n, s_perm)) {
       return;
     }
@@ -469,8 +521,7 @@ int launch_proj_cfg(const ProjArgs& a_in, size_t act_lds, hipStream_t st) {
       hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kProjLdsBytes) == hipSuccess;
   if (!attr_ok) return EMBER_ERR_LAUNCH;
   const ProjArgs& a = a_in;
-  const size_t lds =
-      ROUTE ? std::max(act_lds, std::max(fused_route_lds(a.route.E), fused_router_lds(a.route.d))) : act_lds;
+  const size_t lds = ROUTE ? std::max(act_lds, fused_router_lds(a.route.d) + fused_route_lds(a.route.E)) : act_lds;
   // blocks per CU at this LDS size (cached per size; the launch is sized to one resident wave of blocks)
   static size_t cached_lds = (size_t)-1;
   static int cached_bpc = 1;
@@ -523,7 +574,7 @@ int launch_proj_fmt(const ProjArgs& a, hipStream_t st) {
   while (MT > 1 && MT * row_lds > kProjLdsBytes) MT >>= 1;
   const size_t lds = (size_t)MT * row_lds;
   if (a.route.flag) {  // routing fused into a one-token gate/up launch
-    if (!GATED || a.T != 1 || a.k > kFusedMaxK || a.route.E > kMaxRouteE || !fused_route_fits(a.route.d, a.route.E))
+    if (!GATED || a.T != 1 || !fused_route_fits(a.route.d, a.route.E, a.k))
       return EMBER_ERR_SHAPE;
     if constexpr (GATED) return launch_proj_cfg<FMT, 1, GATED, 2, 512, 4, true>(a, (size_t)row_lds, st);
   }
@@ -551,9 +602,9 @@ int launch_projection(const ProjArgs& a, hipStream_t st) {
 int proj_max_row_bytes() { return kProjLdsBytes; }
 
 // The router blocks (0..E-1) must be resident together with block 0, which waits for them while they
-// wait for it: at most one block per CU is assumed (MI355X: 256 CUs), so E <= 256.
-bool fused_route_fits(int d, int E) {
-  return E <= 256 && fused_router_lds(d) <= (size_t)kProjLdsBytes && fused_route_lds(E) <= (size_t)kProjLdsBytes;
+// wait for it: at least one block per CU is resident (MI355X: 256 CUs), so E <= 255 (ids fit a byte).
+bool fused_route_fits(int d, int E, int k) {
+  return E <= 255 && k <= kFusedMaxK && d >= 8 && d <= 16 * 512 && fused_router_lds(d) + fused_route_lds(E) <= (size_t)kProjLdsBytes;
 }
 
 bool type_quantizes_activations(int type) { return type == EMBER_TYPE_Q8_0 || type == EMBER_TYPE_Q4_K; }

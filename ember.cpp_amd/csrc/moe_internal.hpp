@@ -83,13 +83,14 @@ struct ProjArgs {
   // host side only: when set, the launch records these events in its dispatch packet (kernel timing)
   hipEvent_t ev_start, ev_stop;
   // Routing fused into a one-token gate/up launch (route.flag non-null): blocks 0..E-1 each compute
-  // one expert's router logit and publish it tagged in flag[1 + e]; block 0 collects them, computes the
-  // picks, gates and dispatch (offsets, used, n_used, perm, pos) and publishes them by setting flag[0]
-  // to kRouteReady; every block waits for that. A later launch of the same call (clear_flag) zeroes
-  // the E + 1 words, so stale words never look ready (a word of uninitialised scratch matches a tag
-  // by chance with probability 2^-32 per expert, 2^-64 for flag[0]).
+  // one expert's router logit and publish it in a tagged word of the flag area; block 0 collects them,
+  // computes the picks and gates, writes the routing and dispatch (idx, gates, pos, offsets, used,
+  // n_used, perm) for the later launches and publishes the picks in two tagged words, from which every
+  // block builds the one-token dispatch. A later launch of the same call (clear_flag) zeroes the E + 2
+  // words, so stale words never carry a tag (a word of uninitialised scratch matches a 32-bit tag by
+  // chance with probability 2^-32).
   struct Route {
-    unsigned long long* flag;
+    unsigned long long* flag;  // E + 2 words
     const float* x;       // the token [d]
     const float* router;  // [E][d]
     int d, E, renorm, routed, sigmoid, groups_n, groups_top;
@@ -104,9 +105,9 @@ struct ProjArgs {
   int clear_n;
 };
 // the fused routing's shape limits (the router blocks' and block 0's LDS)
-bool fused_route_fits(int d, int E);
+bool fused_route_fits(int d, int E, int k);
 constexpr unsigned long long kRouteReady = 0x5e11a7ed0ddba11full;
-constexpr int kMaxRouteE = 512;  // experts a fused routing block handles
+constexpr int kMaxRouteE = 256;  // experts a fused routing block handles (E <= 255)
 
 int launch_projection(const ProjArgs& a, hipStream_t st);
 

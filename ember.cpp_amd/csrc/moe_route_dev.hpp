@@ -336,9 +336,18 @@ __device__ inline bool route_routed_wave(const float* row, int E, int k, int ren
 // results equal the reference's serial scans; rows with a NaN (in the logits or in the DeepSeek-style
 // scores) run the reference's serial algorithm on lane 0. wl: route_wave_lds(E) bytes of LDS owned by
 // this wave.
+__device__ inline void route_stage_tables(unsigned char* wl) {
+  const int lane = threadIdx.x & 63;
+  uint64_t* tab128 = reinterpret_cast<uint64_t*>(wl);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) tab128[lane + 64 * i] = ember_math::kExp2Tab128[lane + 64 * i];
+  if (lane < 32) tab128[256 + lane] = ember_math::kExp2Tab32[lane];
+}
+
+// tables_ready: the exp tables are already in wl (route_stage_tables ran earlier on this wave)
 __device__ inline void route_token(const float* __restrict__ r, int E, int k, int renorm, int routed, int sigmoid,
                             const float* __restrict__ bias, int groups_n, int groups_top, unsigned char* wl,
-                            int32_t* __restrict__ idx_t, float* __restrict__ gate_t) {
+                            int32_t* __restrict__ idx_t, float* __restrict__ gate_t, bool tables_ready = false) {
   const int lane = threadIdx.x & 63;
   uint64_t* tab128 = reinterpret_cast<uint64_t*>(wl);
   uint64_t* tab32 = tab128 + 256;
@@ -352,18 +361,22 @@ __device__ inline void route_token(const float* __restrict__ r, int E, int k, in
   bool has_nan = false;
   {
     // the tables and the logits in one round of loads
-    uint64_t t[4];
+    uint64_t t[4], t32 = 0;
+    if (!tables_ready) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) t[i] = ember_math::kExp2Tab128[lane + 64 * i];
-    const uint64_t t32 = ember_math::kExp2Tab32[lane & 31];
+      for (int i = 0; i < 4; ++i) t[i] = ember_math::kExp2Tab128[lane + 64 * i];
+      t32 = ember_math::kExp2Tab32[lane & 31];
+    }
     for (int e = lane; e < E; e += 64) {
       const float v = r[e];
       row[e] = v;
       has_nan |= (v != v);
     }
+    if (!tables_ready) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) tab128[lane + 64 * i] = t[i];
-    if (lane < 32) tab32[lane] = t32;
+      for (int i = 0; i < 4; ++i) tab128[lane + 64 * i] = t[i];
+      if (lane < 32) tab32[lane] = t32;
+    }
   }
   has_nan = __any(has_nan);
   wave_sync_lds();
