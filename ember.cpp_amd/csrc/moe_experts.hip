@@ -299,7 +299,7 @@ constexpr uint32_t kLogitTag = 0x10617ed5u;
 constexpr uint32_t kPickTag[2] = {0x91c5a11du, 0x91c5b22eu};
 // LDS of a router block (the products, f64, chain-major) and, after it, block 0's routing area
 // (logits, picks, gates, one routing wave's work area)
-__host__ __device__ inline size_t fused_router_lds(int d) { return (size_t)8 * d + 256; }
+__host__ __device__ inline size_t fused_router_lds(int d) { return (size_t)8 * d + 8 * 8 + 256; }
 __host__ __device__ inline size_t fused_route_lds(int E) { return 2048 + 512 + route_wave_lds(E); }
 
 // Router block e (blocks 0..E-1): the logit of expert e as the reference computes it (cpu_dot.h:
@@ -311,6 +311,7 @@ template <int NT>
 __device__ float router_block_logit(const ProjArgs& a, int e, uint8_t* lds) {
   const ProjArgs::Route& r = a.route;
   const int t = threadIdx.x, d = r.d, n8 = d - d % 8, nq = n8 / 8;
+  const int ld = nq + 1;  // chain stride in doubles, odd: the eight chains' reads fall on distinct banks
   double* pd = reinterpret_cast<double*>(lds);
   const float* row = r.router + (size_t)e * d;
   if (d % 4 == 0) {
@@ -330,19 +331,19 @@ __device__ float router_block_logit(const ProjArgs& a, int e, uint8_t* lds) {
       const int i4 = t + j * NT;
       if (i4 < n4) {
         const int c0 = (4 * i4) & 7, q = i4 >> 1;
-        pd[(c0 + 0) * nq + q] = (double)rv[j].x * (double)xv[j].x;
-        pd[(c0 + 1) * nq + q] = (double)rv[j].y * (double)xv[j].y;
-        pd[(c0 + 2) * nq + q] = (double)rv[j].z * (double)xv[j].z;
-        pd[(c0 + 3) * nq + q] = (double)rv[j].w * (double)xv[j].w;
+        pd[(c0 + 0) * ld + q] = (double)rv[j].x * (double)xv[j].x;
+        pd[(c0 + 1) * ld + q] = (double)rv[j].y * (double)xv[j].y;
+        pd[(c0 + 2) * ld + q] = (double)rv[j].z * (double)xv[j].z;
+        pd[(c0 + 3) * ld + q] = (double)rv[j].w * (double)xv[j].w;
       }
     }
   } else {
-    for (int i = t; i < n8; i += NT) pd[(i & 7) * nq + (i >> 3)] = (double)row[i] * (double)r.x[i];
+    for (int i = t; i < n8; i += NT) pd[(i & 7) * ld + (i >> 3)] = (double)row[i] * (double)r.x[i];
   }
   __syncthreads();
   double acc = 0.0;
   if (t < 8) {
-    const double* p = pd + (size_t)t * nq;
+    const double* p = pd + (size_t)t * ld;
 #pragma unroll 16
     for (int q = 0; q < nq; ++q) acc = acc + p[q];
   }
