@@ -6,7 +6,8 @@ selects the other single-layer configs.
 One step = one ember_moe_ffn call over one batch of T tokens resident in HBM (the headline T is
 --tokens, default the config's first = decode). Prints ONE JSON line. Besides the contract fields it
 carries:
-  roofline      the dominant kernel (gate/up + SwiGLU, HBM-bound): algorithmic bytes per launch over
+  roofline      the dominant kernel (gate/up + SwiGLU, HBM-bound; at one token it also runs the router,
+                routing and dispatch before streaming): algorithmic bytes per launch over
                 its average duration, timed with HIP events that the launch records in the kernel's
                 own dispatch packet on the launch stream; `traffic` is the kernel's HBM bytes per launch from the
                 committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary of the same workload (profiles/)
@@ -87,6 +88,8 @@ def algorithmic(spec, T, U):
     bpw = BPW[em.TYPE_NAMES[spec.wtype]]
     dsh = spec.d_ff_shared
     gu = U * 2 * d * dff * bpw + T * k * d * 4 + T * k * dff * 4
+    if T == 1:
+        gu += E * d * 4  # one token: the router, routing and dispatch run inside the gate/up launch
     layer = (U * 3 * d * dff + 3 * d * dsh) * bpw + E * d * 4 + 2 * T * d * 4
     flops = 2.0 * T * (k * 3 * d * dff + 3 * d * dsh) + 2.0 * T * E * d
     return gu, layer, flops
@@ -287,7 +290,8 @@ def main():
         "config": {"workload": f"{desc}, T={args.tokens}",
                    "tokens": args.tokens, "d": spec.d, "d_ff": spec.d_ff, "E": spec.E, "k": spec.k,
                    "mode": "hipgraph" if h["graph_us"] is not None and h["graph_us"] <= h["eager_us"] else "eager"},
-        "roofline": {"kernel": f"gate/up + SwiGLU expert kernel ({em.TYPE_NAMES[spec.wtype]})", "bound": "hbm",
+        "roofline": {"kernel": f"gate/up + SwiGLU expert kernel ({em.TYPE_NAMES[spec.wtype]})"
+                               + (", router + routing fused in (one token)" if args.tokens == 1 else ""), "bound": "hbm",
                      "achieved": h["gate_up_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": h["gate_up_gbs"] / HBM_PEAK_GBS, "traffic": profiled_traffic(args.config, args.tokens),
                      "bytes_per_launch": gu_bytes, "avg_launch_us": h["gate_up_us"]},
