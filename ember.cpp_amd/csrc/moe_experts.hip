@@ -299,7 +299,7 @@ constexpr uint32_t kLogitTag = 0x10617ed5u;
 constexpr uint32_t kPickTag[2] = {0x91c5a11du, 0x91c5b22eu};
 // LDS of a router block (the products, f64, chain-major) and, after it, block 0's routing area
 // (logits, picks, gates, one routing wave's work area)
-__host__ __device__ inline size_t fused_router_lds(int d) { return (size_t)8 * d + 8 * 8 + 256; }
+__host__ __device__ inline size_t fused_router_lds(int d) { return (size_t)8 * d + 8 * 8 * 6 + 256; }
 __host__ __device__ inline size_t fused_route_lds(int E) { return 2048 + 512 + route_wave_lds(E); }
 
 // Router block e (blocks 0..E-1): the logit of expert e as the reference computes it (cpu_dot.h:
@@ -311,7 +311,9 @@ template <int NT>
 __device__ float router_block_logit(const ProjArgs& a, int e, uint8_t* lds) {
   const ProjArgs::Route& r = a.route;
   const int t = threadIdx.x, d = r.d, n8 = d - d % 8, nq = n8 / 8;
-  const int ld = nq + 1;  // chain stride in doubles, odd: the eight chains' reads fall on distinct banks
+  // chain stride in doubles: even (16-byte pair reads stay aligned) and 2 mod 4 doubles past a multiple
+  // of 64 banks' worth, so the eight chains' pair reads fall on distinct banks
+  const int ld = (nq + 3) / 4 * 4 + 2;
   double* pd = reinterpret_cast<double*>(lds);
   const float* row = r.router + (size_t)e * d;
   if (d % 4 == 0) {
@@ -343,9 +345,41 @@ __device__ float router_block_logit(const ProjArgs& a, int e, uint8_t* lds) {
   __syncthreads();
   double acc = 0.0;
   if (t < 8) {
+    // the chain in order, in bursts of 16 products (8 pair reads) held in two alternating buffers: one
+    // burst's reads are in flight while the other is added
     const double* p = pd + (size_t)t * ld;
-#pragma unroll 16
-    for (int q = 0; q < nq; ++q) acc = acc + p[q];
+    const int n32 = nq / 32;
+    double2 A[8], B[8];
+    if (n32 > 0) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) A[j] = *reinterpret_cast<const double2*>(p + 2 * j);
+    }
+    for (int i = 0; i < n32; ++i) {
+      const double* pb = p + 32 * i;
+      // the scheduling barriers keep each burst's reads ahead of the other burst's adds
+#pragma unroll
+      for (int j = 0; j < 8; ++j) B[j] = *reinterpret_cast<const double2*>(pb + 16 + 2 * j);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        acc = acc + A[j].x;
+        acc = acc + A[j].y;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      // the next burst, unconditionally (after the last one these reads are unused; they stay inside the
+      // block's LDS, which the launch sizes with room past the products)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) A[j] = *reinterpret_cast<const double2*>(pb + 32 + 2 * j);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        acc = acc + B[j].x;
+        acc = acc + B[j].y;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    int q = 32 * n32;
+    for (; q < nq; ++q) acc = acc + p[q];
   }
   double c[8];
 #pragma unroll
@@ -412,13 +446,14 @@ __device__ bool route_block(const ProjArgs& a, uint8_t* ra, int32_t* s_off, int3
   int nv = 0;  // valid picks: a prefix (route_token puts the -1 entries last)
   for (int j = 0; j < k; ++j) nv += pidx[j] >= 0;
   if (t < 2) {
-    uint32_t lo = 0;
-    for (int j = 0; j < 4; ++j) {
-      const int q = 4 * t + j;
-      lo |= (uint32_t)(q < nv ? pidx[q] : 0xff) << (8 * j);
-    }
-    __hip_atomic_store(r.flag + t, ((unsigned long long)kPickTag[t] << 32) | lo, __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
+    // picks 4t..4t+3 (entries at or past nv are stale and masked), one byte each; the tag is selected
+    // in registers, not read from a table (a global load here would wait on the block's earlier stores)
+    const int4 q4 = *reinterpret_cast<const int4*>(pidx + 4 * t);
+    const int b0 = 4 * t;
+    const uint32_t lo = (uint32_t)(b0 + 0 < nv ? q4.x : 0xff) | (uint32_t)(b0 + 1 < nv ? q4.y : 0xff) << 8 |
+                        (uint32_t)(b0 + 2 < nv ? q4.z : 0xff) << 16 | (uint32_t)(b0 + 3 < nv ? q4.w : 0xff) << 24;
+    const uint32_t tag = t ? kPickTag[1] : kPickTag[0];
+    __hip_atomic_store(r.flag + t, ((unsigned long long)tag << 32) | lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   if (t < k) {
     r.idx[t] = pidx[t];

@@ -176,35 +176,43 @@ __device__ inline uint32_t order_key(float f) {
 // those equal to t, the lowest-indexed ones up to k. That is the set the k strict-> argmax passes take
 // (larger value first, ties to the lower index); returned in ascending index order.
 template <int Q>
-__device__ inline int wave_topk_regs(const float* val, const char* cand, int E, int k, int* picks) {
+__device__ __attribute__((always_inline)) inline int wave_topk_regs(const float* val, const char* cand, int E, int k,
+                                                                    int* picks) {
   const int lane = threadIdx.x & 63;
+  // E and k are wave-uniform: kept in scalar registers, the search below runs on the scalar unit except
+  // for one compare per register slot and step
+  E = __builtin_amdgcn_readfirstlane(E);
+  k = __builtin_amdgcn_readfirstlane(k);
   uint32_t key[Q];
-  bool c[Q];
+  uint64_t cm[Q];  // candidate masks
 #pragma unroll
   for (int q = 0; q < Q; ++q) {
     const int e = lane + 64 * q;
-    c[q] = e < E && (!cand || cand[e]);
-    key[q] = c[q] ? order_key(val[e]) : 0u;  // a candidate's key is > 0 (-inf has 0x007fffff)
+    const bool c = e < E && (!cand || cand[e]);
+    key[q] = c ? order_key(val[e]) : 0u;  // a candidate's key is > 0 (-inf has 0x007fffff), others 0
+    cm[q] = __ballot(c);
   }
-  uint32_t t = 0;  // stays 0 when there are fewer than k candidates: then every candidate is above it
+  // t stays 0 when there are fewer than k candidates: then every candidate is above it. Every trial is
+  // >= 1, so the zero keys of non-candidates never count.
+  uint32_t t = 0;
   for (int bit = 31; bit >= 0; --bit) {
     const uint32_t trial = t | (1u << bit);
     int cnt = 0;
 #pragma unroll
-    for (int q = 0; q < Q; ++q) cnt += __builtin_popcountll(__ballot(c[q] && key[q] >= trial));
-    if (cnt >= k) t = trial;
+    for (int q = 0; q < Q; ++q) cnt += __builtin_popcountll(__ballot(key[q] >= trial));
+    t = cnt >= k ? trial : t;
   }
   int gt = 0;
 #pragma unroll
-  for (int q = 0; q < Q; ++q) gt += __builtin_popcountll(__ballot(c[q] && key[q] > t));
-  const int need = k - gt;  // picks among the keys equal to t
+  for (int q = 0; q < Q; ++q) gt += __builtin_popcountll(__ballot(key[q] > t));
+  const int need = k - gt;  // picks among the candidate keys equal to t
   const uint64_t below = (1ull << lane) - 1;
   int n = 0, eq_before = 0;
 #pragma unroll
   for (int q = 0; q < Q; ++q) {
-    const bool eq = c[q] && key[q] == t;
-    const uint64_t eqm = __ballot(eq);
-    const bool sel = (c[q] && key[q] > t) || (eq && eq_before + __builtin_popcountll(eqm & below) < need);
+    const uint64_t eqm = __ballot(key[q] == t) & cm[q];
+    const bool eq = (eqm >> lane) & 1;
+    const bool sel = key[q] > t || (eq && eq_before + __builtin_popcountll(eqm & below) < need);
     const uint64_t m = __ballot(sel);
     if (sel) picks[n + __builtin_popcountll(m & below)] = lane + 64 * q;
     n += __builtin_popcountll(m);
@@ -214,7 +222,7 @@ __device__ inline int wave_topk_regs(const float* val, const char* cand, int E, 
   return n;
 }
 
-__device__ inline int wave_topk(const float* val, const char* cand, int E, int k, int* picks) {
+__device__ __attribute__((always_inline)) inline int wave_topk(const float* val, const char* cand, int E, int k, int* picks) {
   if (E <= 64) return wave_topk_regs<1>(val, cand, E, k, picks);
   if (E <= 128) return wave_topk_regs<2>(val, cand, E, k, picks);
   if (E <= 256) return wave_topk_regs<4>(val, cand, E, k, picks);
@@ -345,7 +353,7 @@ __device__ inline void route_stage_tables(unsigned char* wl) {
 }
 
 // tables_ready: the exp tables are already in wl (route_stage_tables ran earlier on this wave)
-__device__ inline void route_token(const float* __restrict__ r, int E, int k, int renorm, int routed, int sigmoid,
+__device__ __attribute__((always_inline)) inline void route_token(const float* __restrict__ r, int E, int k, int renorm, int routed, int sigmoid,
                             const float* __restrict__ bias, int groups_n, int groups_top, unsigned char* wl,
                             int32_t* __restrict__ idx_t, float* __restrict__ gate_t, bool tables_ready = false) {
   const int lane = threadIdx.x & 63;
