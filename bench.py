@@ -214,6 +214,8 @@ def main():
     ap.add_argument("--tokens", type=int, default=None, help="headline token count (default: the config's first)")
     ap.add_argument("--sweep", type=str, default=None, help="comma-separated token counts (default: the config's)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-pack", action="store_true",
+                    help="run prefill on the ggml rows instead of the prefill pack (all-Q8_0 layers)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device-to-device copies of MIB MiB (the reference kernel that scales "
                          "rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes), then exit")
@@ -250,6 +252,14 @@ def main():
     hl = em.make_host_layer(spec)
     log(f"[bench] generated + quantized the Q8_0 layer in {time.time() - t0:.1f}s")
     dl = em.DeviceLayer.upload(hl)
+    # the prefill pack (tile-contiguous copy of the Q8_0 stacks for the 256-token-tile GEMM), prepared
+    # once at load as a model loader would; decode does not read it
+    packed = False
+    if not args.no_pack and em.prefill_pack_bytes(dl.desc) > 0:
+        dl.tensors["pack"] = torch.empty(em.prefill_pack_bytes(dl.desc), dtype=torch.uint8, device="cuda")
+        em.prefill_pack(dl.desc, dl.tensors["pack"])
+        packed = True
+        log(f"[bench] prefill pack: {dl.tensors['pack'].numel() / 1e9:.2f} GB")
     torch.cuda.synchronize()
 
     sweep_T = sorted(set([args.tokens] + [int(t) for t in args.sweep.split(",") if t]))
@@ -289,7 +299,8 @@ def main():
         "data": "synthetic (seeded N(0,0.02) experts in the config's encoding, F32 router N(0,1/sqrt(d)), x ~ N(0,1))",
         "config": {"workload": f"{desc}, T={args.tokens}",
                    "tokens": args.tokens, "d": spec.d, "d_ff": spec.d_ff, "E": spec.E, "k": spec.k,
-                   "mode": "hipgraph" if h["graph_us"] is not None and h["graph_us"] <= h["eager_us"] else "eager"},
+                   "mode": "hipgraph" if h["graph_us"] is not None and h["graph_us"] <= h["eager_us"] else "eager",
+                   "prefill_pack": packed},
         "roofline": {"kernel": f"gate/up + SwiGLU expert kernel ({em.TYPE_NAMES[spec.wtype]})"
                                + (", router + routing fused in (one token)" if args.tokens == 1 else ""), "bound": "hbm",
                      "achieved": h["gate_up_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",

@@ -62,6 +62,12 @@ bool is_routed(const ember_moe_layer* w) {
   return w->scoring == EMBER_SCORE_SIGMOID || w->selection_bias != nullptr || w->groups_n > 1;
 }
 
+// The prefill pack covers layers whose routed stacks are all Q8_0 with whole 64-column tiles.
+bool packable(const ember_moe_layer* w) {
+  return w->gate_type == EMBER_TYPE_Q8_0 && w->up_type == EMBER_TYPE_Q8_0 && w->down_type == EMBER_TYPE_Q8_0 &&
+         w->d % 64 == 0 && w->d_ff % 64 == 0;
+}
+
 int validate(const ember_moe_layer* w) {
   if (!w) return EMBER_ERR_NULL;
   if (w->d <= 0 || w->d_ff <= 0 || w->E <= 0 || w->k <= 0 || w->E > kMaxE || w->k > kMaxK) return EMBER_ERR_SHAPE;
@@ -88,6 +94,10 @@ int validate(const ember_moe_layer* w) {
       return s;
     if (w->gate_shared_type != w->up_shared_type) return EMBER_ERR_TYPE;
     if (w->d_ff_shared % 4) return EMBER_ERR_SHAPE;
+  }
+  if (w->prefill_pack) {
+    if (!packable(w)) return EMBER_ERR_TYPE;
+    if (reinterpret_cast<uintptr_t>(w->prefill_pack) % 256) return EMBER_ERR_ALIGN;
   }
   return EMBER_OK;
 }
@@ -276,6 +286,10 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     g.n_tiles = n_tiles;
     g.offsets = offsets;
     g.out_h = h16;
+    // the prefill pack serves the 256-token tiles of the Q8_0 kernel
+    const PackLayout pl = pack_layout(d, d_ff, E);
+    const uint8_t* pack = !skinny && w->prefill_pack ? static_cast<const uint8_t*>(w->prefill_pack) : nullptr;
+    g.Wp = pack ? pack + pl.gu : nullptr;
     const int mt = skinny ? gemm_skinny_max_tiles(T, k, E) : gemm_max_tiles(T, k, E);
     if ((s = gemm(g, true, mt))) return s;
     mark(ev, 4, st);
@@ -290,6 +304,7 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     g.K = d_ff;
     g.out_h = nullptr;
     g.out_y = y;
+    g.Wp = pack ? pack + pl.dn : nullptr;
     g.ksplit = ksplit = skinny ? gemm_skinny_ksplit(g.type, mt, d, d_ff) : gemm_ksplit(g.type, T, k, E, d, d_ff);
     g.part_stride = (int64_t)T * k * d;
     if ((s = gemm(g, false, mt))) return s;
@@ -461,6 +476,25 @@ int ember_moe_ffn_timed(const ember_moe_layer* w, const float* x, int T, float* 
   }
   for (int i = 0; i < 12; ++i) hipEventDestroy(ev[i]);
   return s;
+}
+
+size_t ember_moe_prefill_pack_bytes(const ember_moe_layer* w) {
+  if (validate(w) != EMBER_OK || !packable(w)) return 0;
+  return (size_t)pack_layout(w->d, w->d_ff, w->E).end;
+}
+
+int ember_moe_prefill_pack(const ember_moe_layer* w, void* pack, size_t pack_bytes, hipStream_t st) {
+  int s = validate(w);
+  if (s) return s;
+  if (!packable(w)) return EMBER_ERR_TYPE;
+  if (!pack) return EMBER_ERR_NULL;
+  if (reinterpret_cast<uintptr_t>(pack) % 256) return EMBER_ERR_ALIGN;
+  const PackLayout pl = pack_layout(w->d, w->d_ff, w->E);
+  if (pack_bytes < (size_t)pl.end) return EMBER_ERR_SCRATCH;
+  uint8_t* p = static_cast<uint8_t*>(pack);
+  const int64_t rb_gu = row_bytes(w->gate_type, w->d), rb_dn = row_bytes(w->down_type, w->d_ff);
+  if ((s = launch_prefill_pack(w->gate, w->up, rb_gu * w->d_ff, rb_gu, w->E, w->d_ff, w->d, p + pl.gu, st))) return s;
+  return launch_prefill_pack(w->down, nullptr, rb_dn * w->d, rb_dn, w->E, w->d, w->d_ff, p + pl.dn, st);
 }
 
 int ember_moe_router_logits(const float* x, int T, int d, int E, const float* router, float* logits, hipStream_t st) {

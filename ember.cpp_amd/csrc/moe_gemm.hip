@@ -392,9 +392,14 @@ __device__ inline void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-template <bool GATED>
+// PACKED: the weight tiles come from the prefill pack (GemmArgs::Wp): one tile is 17 KiB contiguous,
+// loaded as 17 whole-kilobyte DMA instructions and laid out in LDS as 68-byte rows (17 dwords: the 32
+// rows a B fragment read touches fall on distinct banks).
+template <bool GATED, bool PACKED>
 __global__ void __launch_bounds__(kDmaThreads) gemm_dma_q8_kernel(GemmArgs g, int NT) {
   constexpr int BN = GATED ? 128 : 256;
+  constexpr int kRowB = PACKED ? kPackRowB : kDmaRowB;             // LDS bytes per weight row
+  constexpr int kLastB = PACKED ? (int)(kPackTileB / 1024) - 1 : kDmaB / 1024 - 1;  // last weight DMA instruction
   extern __shared__ __align__(16) uint8_t dsm[];
 
   // block -> (m-tile, n-tile, K split part): XCD b % 8 runs m-tile (b % 8) + 8 ((b / 8) / (NT KS)), so
@@ -445,12 +450,16 @@ __global__ void __launch_bounds__(kDmaThreads) gemm_dma_q8_kernel(GemmArgs g, in
   }
 #pragma unroll
   for (int i = 0; i < kDmaInstB; ++i) {
-    const int gb = 64 * min(kDmaInstB * wave + i, kDmaB / 1024 - 1) + lane;
-    const int r = gb / 5, part = gb - 5 * r;
-    const int q = GATED ? (r >> 7) : 0;
-    const int n = min(n0 + (GATED ? (r & 127) : r), N - 1);
-    srcB[i] = static_cast<const uint8_t*>(q ? g.W1 : g.W0) + (int64_t)e * g.expert_stride + (int64_t)n * g.row_bytes +
-              (part < 4 ? 16 * part : 52);
+    const int gb = 64 * min(kDmaInstB * wave + i, kLastB) + lane;
+    if constexpr (PACKED) {
+      srcB[i] = g.Wp + ((int64_t)e * NT + nt) * nk_all * kPackTileB + 16 * gb;
+    } else {
+      const int r = gb / 5, part = gb - 5 * r;
+      const int q = GATED ? (r >> 7) : 0;
+      const int n = min(n0 + (GATED ? (r & 127) : r), N - 1);
+      srcB[i] = static_cast<const uint8_t*>(q ? g.W1 : g.W0) + (int64_t)e * g.expert_stride + (int64_t)n * g.row_bytes +
+                (part < 4 ? 16 * part : 52);
+    }
   }
   // DMA of tile kt (clamped: tiles past the end reload the last, never multiplied), part j of 4 so
   // that the issue is spread over the K steps of a tile: activation instruction j, weight instruction j
@@ -459,7 +468,7 @@ __global__ void __launch_bounds__(kDmaThreads) gemm_dma_q8_kernel(GemmArgs g, in
     uint8_t* st = dsm + (kt % kDmaStages) * kDmaStage;
     lds_dma16(srcA[j] + (size_t)kc * GBK * 2, st + 1024 * (kDmaInstA * wave + j));
     if (j < kDmaInstB)
-      lds_dma16(srcB[j] + (size_t)kc * 68, st + kDmaA + 1024 * min(kDmaInstB * wave + j, kDmaB / 1024 - 1));
+      lds_dma16(srcB[j] + (size_t)kc * (PACKED ? kPackTileB : 68), st + kDmaA + 1024 * min(kDmaInstB * wave + j, kLastB));
   };
   auto issue_all = [&](int kt) {
 #pragma unroll
@@ -504,7 +513,7 @@ __global__ void __launch_bounds__(kDmaThreads) gemm_dma_q8_kernel(GemmArgs g, in
     const uint8_t* Bs = st + kDmaA;
 #pragma unroll
     for (int jn = 0; jn < 2; ++jn) {
-      const uint8_t* row = Bs + kDmaRowB * brow_of(jn);
+      const uint8_t* row = Bs + kRowB * brow_of(jn);
       const uint32_t dbits = b ? (*reinterpret_cast<const uint32_t*>(row + 32) >> 16)
                                : (*reinterpret_cast<const uint32_t*>(row) & 0xffffu);
       const half2_t d = h2(dbits * 0x10001u);
@@ -515,7 +524,8 @@ __global__ void __launch_bounds__(kDmaThreads) gemm_dma_q8_kernel(GemmArgs g, in
         w1 = __builtin_amdgcn_alignbit(qw[2], qw[1], 16);
       } else {
         const int byte = X + 8 * h;
-        const uint32_t* qw = reinterpret_cast<const uint32_t*>(row + (byte + 8 > 64 ? byte + 12 : byte));
+        // row slices: bytes past 64 sit in the overlapping fifth granule, 12 bytes further on
+        const uint32_t* qw = reinterpret_cast<const uint32_t*>(row + (PACKED || byte + 8 <= 64 ? byte : byte + 12));
         w0 = qw[0];
         w1 = qw[1];
       }
@@ -965,12 +975,17 @@ int launch_gemm_fmt(const GemmArgs& g, int max_mtiles, hipStream_t st) {
   const bool dma_off = !dma_enabled();
   if (FMT == EMBER_TYPE_Q8_0 && !dma_off) {
     static const bool dma_ok =
-        hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma_q8_kernel<GATED>),
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma_q8_kernel<GATED, false>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDmaLds) == hipSuccess &&
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma_q8_kernel<GATED, true>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDmaLds) == hipSuccess;
     if (!dma_ok) return EMBER_ERR_LAUNCH;
     GemmArgs gk = g;
     if (GATED || gk.ksplit < 1) gk.ksplit = 1;
-    gemm_dma_q8_kernel<GATED><<<blocks * (unsigned)gk.ksplit, kDmaThreads, kDmaLds, st>>>(gk, NT);
+    if (gk.Wp)
+      gemm_dma_q8_kernel<GATED, true><<<blocks * (unsigned)gk.ksplit, kDmaThreads, kDmaLds, st>>>(gk, NT);
+    else
+      gemm_dma_q8_kernel<GATED, false><<<blocks * (unsigned)gk.ksplit, kDmaThreads, kDmaLds, st>>>(gk, NT);
     return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
   }
   gemm_kernel<FMT, GATED><<<blocks, kGemmThreads, kGemmLds, st>>>(g, NT);
@@ -1084,6 +1099,39 @@ __global__ void build_tiles_kernel(const int32_t* __restrict__ offsets, int E, i
 
 int launch_build_tiles(const int32_t* offsets, int E, bool skinny, int32_t* tiles, int32_t* n_tiles, hipStream_t st) {
   build_tiles_kernel<<<1, 64, 0, st>>>(offsets, E, skinny ? SBM : GBM, tiles, n_tiles);
+  return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
+}
+
+
+// ---- prefill pack: one thread per (tile, row), 17 dwords each (a one-time copy at weight load)
+__global__ void __launch_bounds__(256) prefill_pack_kernel(const uint8_t* __restrict__ W0, const uint8_t* __restrict__ W1,
+                                                           int64_t expert_stride, int64_t row_bytes, int N, int NT,
+                                                           int nk, int64_t total_rows, uint8_t* __restrict__ dst) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total_rows) return;
+  const int r = (int)(i % 256);
+  int64_t t = i / 256;
+  const int kc = (int)(t % nk);
+  t /= nk;
+  const int nt = (int)(t % NT), e = (int)(t / NT);
+  const bool gated = W1 != nullptr;
+  const int q = gated ? (r >> 7) : 0;
+  const int n = min(nt * (gated ? 128 : 256) + (gated ? (r & 127) : r), N - 1);
+  const uint32_t* src = reinterpret_cast<const uint32_t*>((q ? W1 : W0) + (int64_t)e * expert_stride +
+                                                          (int64_t)n * row_bytes + (int64_t)kc * kPackRowB);
+  uint32_t* d = reinterpret_cast<uint32_t*>(dst + i * kPackRowB);
+#pragma unroll
+  for (int w = 0; w < kPackRowB / 4; ++w) d[w] = src[w];
+}
+
+int launch_prefill_pack(const void* W0, const void* W1, int64_t expert_stride, int64_t row_bytes, int E, int N, int K,
+                        uint8_t* dst, hipStream_t st) {
+  const int NT = W1 ? (N + 127) / 128 : (N + 255) / 256, nk = K / 64;
+  const int64_t total = (int64_t)E * NT * nk * 256;
+  if (total == 0) return EMBER_OK;
+  const int64_t blocks = (total + 255) / 256;
+  prefill_pack_kernel<<<dim3((unsigned)blocks), 256, 0, st>>>(static_cast<const uint8_t*>(W0), static_cast<const uint8_t*>(W1),
+                                                             expert_stride, row_bytes, N, NT, nk, total, dst);
   return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
 }
 

@@ -131,7 +131,32 @@ struct GemmArgs {
   int max_mt;              // m-tile slots of the launch (set by the launcher)
   int ksplit;              // plain projections: K split over this many blocks, partial sums to
   int64_t part_stride;     // out_y + s * part_stride (floats), summed in order by the combine
+  const uint8_t* Wp;       // non-null: this projection's tiles in the prefill pack (Q8_0, 256-token tiles)
 };
+// Prefill pack (ember_moe_prefill_pack): Q8_0 tiles of 256 weight rows x 64 columns, 68-byte rows,
+// one tile contiguous; the gate/up section [E][ceil(d_ff / 128)][d / 64] (each tile: the 128 gate rows
+// of an n-tile, then its 128 up rows), then the down section [E][ceil(d / 256)][d_ff / 64]; rows past a
+// matrix's end repeat its last row (as the GEMM's clamped loads would).
+constexpr int kPackRowB = 68;
+constexpr int64_t kPackTileB = (int64_t)256 * kPackRowB;
+struct PackLayout {
+  int nt_gu, nk_gu, nt_dn, nk_dn;
+  int64_t gu, dn, end;  // byte offsets of the sections, total
+};
+inline PackLayout pack_layout(int d, int d_ff, int E) {
+  PackLayout p;
+  p.nt_gu = (d_ff + 127) / 128;
+  p.nk_gu = d / 64;
+  p.nt_dn = (d + 255) / 256;
+  p.nk_dn = d_ff / 64;
+  p.gu = 0;
+  p.dn = (int64_t)E * p.nt_gu * p.nk_gu * kPackTileB;
+  p.end = p.dn + (int64_t)E * p.nt_dn * p.nk_dn * kPackTileB;
+  return p;
+}
+// Fills one section of the pack from ggml Q8_0 rows (W1 non-null: the gate/up section).
+int launch_prefill_pack(const void* W0, const void* W1, int64_t expert_stride, int64_t row_bytes, int E, int N, int K,
+                        uint8_t* dst, hipStream_t st);
 bool gemm_supported(int type, int K);
 int gemm_max_tiles(int T, int k, int E);
 int launch_gemm(const GemmArgs& g, bool gated, int max_mtiles, hipStream_t st);

@@ -54,6 +54,7 @@ class Layer(ctypes.Structure):
         ("gate_shared", ctypes.c_void_p), ("gate_shared_type", ctypes.c_int),
         ("up_shared", ctypes.c_void_p), ("up_shared_type", ctypes.c_int),
         ("down_shared", ctypes.c_void_p), ("down_shared_type", ctypes.c_int),
+        ("prefill_pack", ctypes.c_void_p),
     ]
 
 
@@ -110,6 +111,10 @@ def lib() -> ctypes.CDLL:
         L.ember_moe_route_scratch_bytes.restype = sz
         L.ember_moe_route.argtypes = [vp, i, i, i, i, i, vp, i, i, vp, vp, vp, vp, vp, sz, vp]
         L.ember_moe_route.restype = i
+        L.ember_moe_prefill_pack_bytes.argtypes = [ctypes.POINTER(Layer)]
+        L.ember_moe_prefill_pack_bytes.restype = sz
+        L.ember_moe_prefill_pack.argtypes = [ctypes.POINTER(Layer), vp, sz, vp]
+        L.ember_moe_prefill_pack.restype = i
         L.ember_moe_strerror.argtypes = [i]
         L.ember_moe_strerror.restype = ctypes.c_char_p
         L.ember_gguf_layer_bytes.argtypes = [ctypes.POINTER(GgufMoe)]
@@ -235,6 +240,21 @@ def _stream(stream) -> int:
 
 def scratch_bytes(layer: Layer, T: int) -> int:
     return int(lib().ember_moe_scratch_bytes(ctypes.byref(layer), T))
+
+
+def prefill_pack_bytes(layer: Layer) -> int:
+    """Bytes of the layer's prefill pack (0: the layer has none — not all-Q8_0, or an invalid descriptor)."""
+    return int(lib().ember_moe_prefill_pack_bytes(ctypes.byref(layer)))
+
+
+def prefill_pack(layer: Layer, pack, stream=None) -> None:
+    """Fills `pack` (a device tensor of prefill_pack_bytes(layer) bytes) and points layer.prefill_pack
+    at it. Raises EmberError on failure."""
+    n = pack.numel() * pack.element_size()
+    st = int(lib().ember_moe_prefill_pack(ctypes.byref(layer), _ptr(pack), n, _stream(stream)))
+    if st:
+        raise EmberError(st, "ember_moe_prefill_pack")
+    layer.prefill_pack = _ptr(pack)
 
 
 def moe_ffn(layer: Layer, x, T: int, out, scratch, scratch_nbytes: Optional[int] = None, stream=None) -> int:

@@ -49,11 +49,27 @@ typedef struct ember_moe_layer {
   const void* gate_shared; int gate_shared_type;
   const void* up_shared;   int up_shared_type;
   const void* down_shared; int down_shared_type;
+  /* Optional (NULL: none): the routed Q8_0 stacks repacked for the prefill MFMA path by
+   * ember_moe_prefill_pack. Appended last, so descriptors that zero-initialise keep working. */
+  const void* prefill_pack;
 } ember_moe_layer;
 
 /* Scratch bytes ember_moe_ffn needs for T tokens of this layer (moe_ffn_scratch_floats' role,
  * cuda_kernels.h:678, in bytes). Returns 0 for an invalid descriptor. */
 size_t ember_moe_scratch_bytes(const ember_moe_layer* w, int T);
+
+/* Prefill weight packing (no counterpart in the reference, which dequantizes every stack to F32 at
+ * load, weight_management.cpp:486-511). The prefill expert GEMM (T k / E > 96 tokens per expert) reads
+ * its weights in 256-row x 64-column tiles; ggml rows give it 68-byte row slices 4 KiB-plus apart. A
+ * packed copy stores each tile contiguously (gate/up: the tile's 128 gate and 128 up rows; rows past
+ * the end repeat the last), which the GEMM then loads as whole tiles and reads at a bank-conflict-free
+ * stride. Same values, same arithmetic: outputs are bit-identical with or without the pack.
+ * Only for layers whose gate, up and down stacks are all Q8_0 (d and d_ff multiples of 64); for others
+ * ember_moe_prefill_pack_bytes returns 0. The pack is as large as the three stacks (it does not
+ * replace them: decode streams the ggml rows). ember_moe_prefill_pack fills a caller-owned, 256-byte
+ * aligned device buffer on `stream`; set the descriptor's prefill_pack to it afterwards. */
+size_t ember_moe_prefill_pack_bytes(const ember_moe_layer* w);
+int ember_moe_prefill_pack(const ember_moe_layer* w, void* pack, size_t pack_bytes, hipStream_t stream);
 
 /* out[T][d] = the MoE FFN of x[T][d] (moe_ffn_cuda, cuda_kernels.cu:3628-3684; per token the
  * result of moe_ffn_f32_cpu / moe_ffn_routed_f32_cpu, utils.cpp:704-836). T = 0 is a no-op.

@@ -98,3 +98,27 @@ def test_strerror():
     for s in (em.OK, em.ERR_SHAPE, em.ERR_TYPE, em.ERR_SCRATCH, em.ERR_NULL, em.ERR_LAUNCH, em.ERR_ALIGN,
               em.ERR_FORMAT, em.ERR_NOT_FOUND):
         assert em.strerror(s) and em.strerror(s) != "unknown status"
+
+
+def test_prefill_pack_sizes_and_validation():
+    # the pack holds every 256-row x 64-column tile of 68-byte rows: gate/up tiles per 128 columns of
+    # h, down tiles per 256 output rows (partial tiles counted whole)
+    def expect(d, d_ff, E):
+        return E * (-(-d_ff // 128) * (d // 64) + -(-d // 256) * (d_ff // 64)) * 256 * 68
+
+    L = _layer(d=512, d_ff=704, E=4)
+    assert em.prefill_pack_bytes(L) == expect(512, 704, 4)
+    assert em.prefill_pack_bytes(_layer(d=4096, d_ff=14336, E=8)) == expect(4096, 14336, 8)
+    # only all-Q8_0 layers with whole 64-column tiles have a pack
+    assert em.prefill_pack_bytes(_layer(gate_type=em.BF16, up_type=em.BF16, down_type=em.BF16)) == 0
+    assert em.prefill_pack_bytes(_layer(down_type=em.BF16)) == 0
+    assert em.prefill_pack_bytes(_layer(d=512, d_ff=736)) == 0  # d_ff not a multiple of 64
+    lib = em.lib()
+    assert lib.ember_moe_prefill_pack(ctypes.byref(_layer(down_type=em.BF16)), 0x100000, 1 << 30, None) == em.ERR_TYPE
+    assert lib.ember_moe_prefill_pack(ctypes.byref(L), 0, 1 << 30, None) == em.ERR_NULL
+    assert lib.ember_moe_prefill_pack(ctypes.byref(L), 0x100080, 1 << 30, None) == em.ERR_ALIGN
+    assert lib.ember_moe_prefill_pack(ctypes.byref(L), 0x100000, expect(512, 704, 4) - 1, None) == em.ERR_SCRATCH
+    # a descriptor carrying a pack must be packable and the pack 256-byte aligned
+    assert em.scratch_bytes(_layer(prefill_pack=0x100000), 1) > 0
+    assert em.scratch_bytes(_layer(prefill_pack=0x100010), 1) == 0
+    assert em.scratch_bytes(_layer(prefill_pack=0x100000, down_type=em.BF16), 1) == 0
