@@ -286,9 +286,9 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     g.n_tiles = n_tiles;
     g.offsets = offsets;
     g.out_h = h16;
-    // the prefill pack serves the 256-token tiles of the Q8_0 kernel
+    // the prefill pack serves the Q8_0 tile kernels (256- and 64-token tiles alike)
     const PackLayout pl = pack_layout(d, d_ff, E);
-    const uint8_t* pack = !skinny && w->prefill_pack ? static_cast<const uint8_t*>(w->prefill_pack) : nullptr;
+    const uint8_t* pack = static_cast<const uint8_t*>(w->prefill_pack);
     g.Wp = pack ? pack + pl.gu : nullptr;
     const int mt = skinny ? gemm_skinny_max_tiles(T, k, E) : gemm_max_tiles(T, k, E);
     if ((s = gemm(g, true, mt))) return s;

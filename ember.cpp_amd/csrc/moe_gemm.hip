@@ -635,9 +635,12 @@ constexpr size_t kD64Lds = (size_t)kD64Stages * kD64Stage;
 constexpr int kD64InstA = kD64A / 16 / 64 / 4;     // 2 per wave
 constexpr int kD64InstB = kDmaB / 16 / 64 / 4;     // 5 per wave
 
-template <bool GATED>
+// PACKED: weight tiles from the prefill pack, as in gemm_dma_q8_kernel.
+template <bool GATED, bool PACKED>
 __global__ void __launch_bounds__(kD64Threads) gemm_dma64_q8_kernel(GemmArgs g, int NT) {
   constexpr int BN = GATED ? 128 : 256;
+  constexpr int kRowB = PACKED ? kPackRowB : kDmaRowB;
+  constexpr int kLastB = PACKED ? (int)(kPackTileB / 1024) - 1 : kDmaB / 1024 - 1;
   extern __shared__ __align__(16) uint8_t dsm[];
 
   // block -> (m-tile, n-tile, K split part); part ks covers K tiles [kt0, kt0 + nk)
@@ -673,12 +676,16 @@ __global__ void __launch_bounds__(kD64Threads) gemm_dma64_q8_kernel(GemmArgs g, 
   }
 #pragma unroll
   for (int i = 0; i < kD64InstB; ++i) {
-    const int gb = 64 * (kD64InstB * wave + i) + lane;
-    const int r = gb / 5, part = gb - 5 * r;
-    const int q = GATED ? (r >> 7) : 0;
-    const int n = min(n0 + (GATED ? (r & 127) : r), N - 1);
-    srcB[i] = static_cast<const uint8_t*>(q ? g.W1 : g.W0) + (int64_t)e * g.expert_stride + (int64_t)n * g.row_bytes +
-              (part < 4 ? 16 * part : 52);
+    const int gb = 64 * min(kD64InstB * wave + i, kLastB) + lane;
+    if constexpr (PACKED) {
+      srcB[i] = g.Wp + ((int64_t)e * NT + nt) * nk_all * kPackTileB + 16 * gb;
+    } else {
+      const int r = gb / 5, part = gb - 5 * r;
+      const int q = GATED ? (r >> 7) : 0;
+      const int n = min(n0 + (GATED ? (r & 127) : r), N - 1);
+      srcB[i] = static_cast<const uint8_t*>(q ? g.W1 : g.W0) + (int64_t)e * g.expert_stride + (int64_t)n * g.row_bytes +
+                (part < 4 ? 16 * part : 52);
+    }
   }
   // DMA of tile kt (clamped past the end), part j of 4: A granule j / 2 on even parts, weight
   // granules spread over the four parts
@@ -691,7 +698,8 @@ __global__ void __launch_bounds__(kD64Threads) gemm_dma64_q8_kernel(GemmArgs g, 
     }
 #pragma unroll
     for (int i = 0; i < kD64InstB; ++i)
-      if ((i * 4) / kD64InstB == j) lds_dma16(srcB[i] + (size_t)kc * 68, st + kD64A + 1024 * (kD64InstB * wave + i));
+      if ((i * 4) / kD64InstB == j)
+        lds_dma16(srcB[i] + (size_t)kc * (PACKED ? kPackTileB : 68), st + kD64A + 1024 * min(kD64InstB * wave + i, kLastB));
   };
 
   floatx16 acc[2][2];
@@ -724,7 +732,7 @@ __global__ void __launch_bounds__(kD64Threads) gemm_dma64_q8_kernel(GemmArgs g, 
     const uint8_t* Bs = st + kD64A;
 #pragma unroll
     for (int jn = 0; jn < 2; ++jn) {
-      const uint8_t* row = Bs + kDmaRowB * brow_of(jn);
+      const uint8_t* row = Bs + kRowB * brow_of(jn);
       const uint32_t dbits = b ? (*reinterpret_cast<const uint32_t*>(row + 32) >> 16)
                                : (*reinterpret_cast<const uint32_t*>(row) & 0xffffu);
       const half2_t d = h2(dbits * 0x10001u);
@@ -735,7 +743,7 @@ __global__ void __launch_bounds__(kD64Threads) gemm_dma64_q8_kernel(GemmArgs g, 
         w1 = __builtin_amdgcn_alignbit(qw[2], qw[1], 16);
       } else {
         const int byte = X + 8 * h;
-        const uint32_t* qw = reinterpret_cast<const uint32_t*>(row + (byte + 8 > 64 ? byte + 12 : byte));
+        const uint32_t* qw = reinterpret_cast<const uint32_t*>(row + (PACKED || byte + 8 <= 64 ? byte : byte + 12));
         w0 = qw[0];
         w1 = qw[1];
       }
@@ -1015,11 +1023,18 @@ int launch_skinny_fmt(GemmArgs g, int max_mtiles, hipStream_t st) {
   g.max_mt = max_mtiles;
   const bool dma_off = !dma_enabled();
   if (FMT == EMBER_TYPE_Q8_0 && !dma_off) {
-    static const bool ok = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma64_q8_kernel<GATED>),
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)kD64Lds) == hipSuccess;
+    static const bool ok =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma64_q8_kernel<GATED, false>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kD64Lds) == hipSuccess &&
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma64_q8_kernel<GATED, true>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kD64Lds) == hipSuccess;
     if (!ok) return EMBER_ERR_LAUNCH;
     if (GATED || g.ksplit < 1) g.ksplit = 1;
-    gemm_dma64_q8_kernel<GATED><<<(unsigned)(max_mtiles * NT * g.ksplit), kD64Threads, kD64Lds, st>>>(g, NT);
+    const unsigned blocks = (unsigned)(max_mtiles * NT * g.ksplit);
+    if (g.Wp)
+      gemm_dma64_q8_kernel<GATED, true><<<blocks, kD64Threads, kD64Lds, st>>>(g, NT);
+    else
+      gemm_dma64_q8_kernel<GATED, false><<<blocks, kD64Threads, kD64Lds, st>>>(g, NT);
     return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
   }
   gemm_skinny_kernel<FMT, GATED><<<(unsigned)(max_mtiles * NT), 256, 0, st>>>(g, NT);

@@ -1,4 +1,4 @@
-"""GPU tests of the prefill pack (ember_moe_prefill_pack): the Q8_0 prefill GEMM reading packed tiles
+"""GPU tests of the prefill pack (ember_moe_prefill_pack): the Q8_0 tile GEMMs reading packed tiles
 gives the same output bits as reading the ggml rows (same values, same arithmetic), on tile-aligned
 and partial-tile shapes, with ragged expert segments, through the down projection's K split; and the
 oracle agrees at the Q8_0 bar."""
@@ -27,8 +27,10 @@ def _run(hl, x, pack: bool):
     return out.cpu().numpy()
 
 
-# T k / E > 96 tokens per expert: the 256-token-tile GEMM; d_ff 704 and d 576 leave partial n-tiles
-@pytest.mark.parametrize("d,d_ff,E,k,T", [(512, 1024, 4, 2, 320), (576, 704, 4, 2, 300), (256, 512, 8, 2, 1024)])
+# T k / E > 96 tokens per expert: the 256-token-tile GEMM; 2 < T k / E <= 96: the 64-token-tile GEMM;
+# d_ff 704 and d 576 leave partial n-tiles
+@pytest.mark.parametrize("d,d_ff,E,k,T", [(512, 1024, 4, 2, 320), (576, 704, 4, 2, 300), (256, 512, 8, 2, 1024),
+                                          (512, 1024, 4, 2, 64), (576, 704, 4, 2, 37), (256, 512, 8, 2, 150)])
 def test_pack_same_bits_as_rows(gpu, d, d_ff, E, k, T):
     spec = em.LayerSpec(d=d, d_ff=d_ff, E=E, k=k, wtype=em.Q8_0, seed=21)
     hl = em.make_host_layer(spec)
