@@ -290,14 +290,12 @@ __device__ inline void proj_body(const ProjArgs& a, const Dispatch& dp, const Se
 }
 
 // ---- routing fused into a one-token gate/up launch (ProjArgs::route)
-// Words of the flag area: [0], [1] the picks (expert ids 0..254 as bytes, 0xff: none; four per word)
-// under kPickTag[0] / kPickTag[1] in the high half; [2 + e] expert e's logit under kLogitTag (the f32
-// bits in the low half). A word is read with one device-coherent load and carries its own data, so
-// no ordering between a payload and a flag is needed.
+// Words of the flag area: [0], [1] unused; [2 + e] expert e's logit under kLogitTag (the f32 bits in
+// the low half). A word is read with one device-coherent load and carries its own data, so no
+// ordering between a payload and a flag is needed.
 constexpr int kFusedMaxK = 8;
 constexpr uint32_t kLogitTag = 0x10617ed5u;
-constexpr uint32_t kPickTag[2] = {0x91c5a11du, 0x91c5b22eu};
-// LDS of a router block (the products, f64, chain-major) and, after it, block 0's routing area
+// LDS of a router block (the products, f64, chain-major) and, after it, every block's routing area
 // (logits, picks, gates, one routing wave's work area)
 __host__ __device__ inline size_t fused_router_lds(int d) { return (size_t)8 * d + 8 * 8 * 6 + 256; }
 __host__ __device__ inline size_t fused_route_lds(int E) { return 2048 + 512 + route_wave_lds(E); }
@@ -411,10 +409,11 @@ __device__ inline void fused_dispatch(const int* picks, int nv, int E, int32_t* 
   if (t == 0) *s_n = nv;
 }
 
-// Block 0 after its own logit: collects every expert's tagged logit (bounded wait), runs route_token
-// (exp tables staged at the start of the launch), writes the routing and dispatch for the later
-// launches, publishes the picks and fills the block's dispatch arrays. False: a logit never arrived
-// (the block then does nothing; the layer is not computed).
+// Every block (router blocks after their own logit): collects every expert's tagged logit (bounded
+// wait), runs route_token (exp tables staged at the start of the launch; every block computes the same
+// routing, so no second hop through one block is needed) and fills its dispatch arrays; block 0 also
+// writes the routing and dispatch for the later launches. False: a logit never arrived (the block then
+// does nothing; the layer is not computed).
 template <int NT>
 __device__ bool route_block(const ProjArgs& a, uint8_t* ra, int32_t* s_off, int32_t* s_used, int32_t* s_n,
                             int32_t* s_perm) {
@@ -445,71 +444,24 @@ __device__ bool route_block(const ProjArgs& a, uint8_t* ra, int32_t* s_off, int3
   __syncthreads();
   int nv = 0;  // valid picks: a prefix (route_token puts the -1 entries last)
   for (int j = 0; j < k; ++j) nv += pidx[j] >= 0;
-  if (t < 2) {
-    // picks 4t..4t+3 (entries at or past nv are stale and masked), one byte each; the tag is selected
-    // in registers, not read from a table (a global load here would wait on the block's earlier stores)
-    const int4 q4 = *reinterpret_cast<const int4*>(pidx + 4 * t);
-    const int b0 = 4 * t;
-    const uint32_t lo = (uint32_t)(b0 + 0 < nv ? q4.x : 0xff) | (uint32_t)(b0 + 1 < nv ? q4.y : 0xff) << 8 |
-                        (uint32_t)(b0 + 2 < nv ? q4.z : 0xff) << 16 | (uint32_t)(b0 + 3 < nv ? q4.w : 0xff) << 24;
-    const uint32_t tag = t ? kPickTag[1] : kPickTag[0];
-    __hip_atomic_store(r.flag + t, ((unsigned long long)tag << 32) | lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (blockIdx.x == 0) {
+    if (t < k) {
+      r.idx[t] = pidx[t];
+      r.gates[t] = pgate[t];
+      r.pos[t] = t < nv ? t : -1;
+    }
+    if (t < nv) {
+      r.used[t] = pidx[t];
+      r.perm[t] = t;
+    }
+    for (int e = t; e <= E; e += NT) {
+      int cnt = 0;
+      for (int j = 0; j < nv; ++j) cnt += pidx[j] < e;
+      r.offsets[e] = cnt;
+    }
+    if (t == 0) *r.n_used = nv;
   }
-  if (t < k) {
-    r.idx[t] = pidx[t];
-    r.gates[t] = pgate[t];
-    r.pos[t] = t < nv ? t : -1;
-  }
-  if (t < nv) {
-    r.used[t] = pidx[t];
-    r.perm[t] = t;
-  }
-  for (int e = t; e <= E; e += NT) {
-    int cnt = 0;
-    for (int j = 0; j < nv; ++j) cnt += pidx[j] < e;
-    r.offsets[e] = cnt;
-  }
-  if (t == 0) *r.n_used = nv;
   fused_dispatch(pidx, nv, E, s_off, s_used, s_n, s_perm);
-  __syncthreads();
-  return true;
-}
-
-// The other blocks: wait for both pick words (bounded: a block that gives up does nothing, it never
-// hangs), then build the dispatch from them. Returns false on give-up.
-__device__ inline bool route_wait(const ProjArgs& a, int32_t* s_off, int32_t* s_used, int32_t* s_n, int32_t* s_perm) {
-  __shared__ int ok_s;
-  __shared__ int picks[kFusedMaxK];
-  __shared__ int nv_s;
-  const ProjArgs::Route& r = a.route;
-  if (threadIdx.x == 0) {
-    int ok = 1;
-    unsigned n = 0;
-    unsigned long long w0, w1;
-    for (;;) {
-      w0 = __hip_atomic_load(r.flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      w1 = __hip_atomic_load(r.flag + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if ((w0 >> 32) == kPickTag[0] && (w1 >> 32) == kPickTag[1]) break;
-      if (++n > (1u << 22)) {
-        ok = 0;
-        break;
-      }
-      __builtin_amdgcn_s_sleep(2);
-    }
-    int nv = 0;
-    for (int j = 0; j < kFusedMaxK; ++j) {
-      const int p = (int)(((j < 4 ? w0 : w1) >> (8 * (j & 3))) & 0xff);
-      if (p != 0xff && nv == j) {
-        picks[j] = p;
-        ++nv;
-      }
-    }
-    nv_s = nv;
-    ok_s = ok;
-  }
-  __syncthreads();
-  if (!ok_s) return false;
-  fused_dispatch(picks, nv_s, a.route.E, s_off, s_used, s_n, s_perm);
   __syncthreads();
   return true;
 }
@@ -523,8 +475,8 @@ __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) 
     extern __shared__ __align__(16) uint8_t act_lds[];
     __shared__ int32_t s_off[kMaxRouteE + 1], s_used[kFusedMaxK], s_perm[kFusedMaxK], s_n;
     const int b = blockIdx.x;
-    uint8_t* ra = act_lds + fused_router_lds(a.route.d);  // block 0's routing area, after the products
-    if (b == 0 && threadIdx.x < 64) route_stage_tables(ra + 2048 + 512);
+    uint8_t* ra = act_lds + fused_router_lds(a.route.d);  // the routing area, after the products
+    if (threadIdx.x < 64) route_stage_tables(ra + 2048 + 512);
     if (b < a.route.E) {  // router block: its expert's logit, published tagged
       const float v = router_block_logit<NT>(a, b, act_lds);
       if (threadIdx.x == 0) {
@@ -533,12 +485,8 @@ __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) 
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
-    if (b == 0) {
-      if (!route_block<NT>(a, ra, s_off, s_used, &s_n, s_perm)) return;
-    } else if (!route_wait(a, s_off, s_used, &s_n, s_perm)) {
-      return;
-    }
-    __syncthreads();  // block 0: its routing work area (act_lds) is free for the activations
+    if (!route_block<NT>(a, ra, s_off, s_used, &s_n, s_perm)) return;
+    __syncthreads();  // the routing work area (act_lds) is free for the activations
     Dispatch dp{s_n, s_used, s_off, s_perm};
     SegView v;
     if (seg_view<GATED, MT>(a, dp, blockIdx.x, gridDim.x, v)) proj_body<FMT, MT, GATED, NB, NT>(a, dp, v);

@@ -83,10 +83,10 @@ struct ProjArgs {
   // host side only: when set, the launch records these events in its dispatch packet (kernel timing)
   hipEvent_t ev_start, ev_stop;
   // Routing fused into a one-token gate/up launch (route.flag non-null): blocks 0..E-1 each compute
-  // one expert's router logit and publish it in a tagged word of the flag area; block 0 collects them,
-  // computes the picks and gates, writes the routing and dispatch (idx, gates, pos, offsets, used,
-  // n_used, perm) for the later launches and publishes the picks in two tagged words, from which every
-  // block builds the one-token dispatch. A later launch of the same call (clear_flag) zeroes the E + 2
+  // one expert's router logit and publish it in a tagged word of the flag area; every block collects
+  // them, computes the same picks and gates and builds the one-token dispatch; block 0 also writes the
+  // routing and dispatch (idx, gates, pos, offsets, used, n_used, perm) for the later launches. A
+  // later launch of the same call (clear_flag) zeroes the E + 2
   // words, so stale words never carry a tag (a word of uninitialised scratch matches a 32-bit tag by
   // chance with probability 2^-32).
   struct Route {
