@@ -27,7 +27,9 @@ int path_mode(int type_in, int K_in, int type_out, int K_out, double avg_m) {
     return s == "gemv" ? kGemv : s == "skinny" ? kSkinny : s == "gemm" ? kGemm : -1;
   }();
   if (forced >= 0) return forced;
-  if (avg_m <= 2.0) return kGemv;
+  // Q8_0 (its DMA tile kernels): measured crossover between 1 and 2 tokens per expert (C2 T = 4: GEMV
+  // 255 vs 291 us; T = 8: 382 vs 342 us with the prefill pack, about even without it)
+  if (avg_m <= (type_in == EMBER_TYPE_Q8_0 && type_out == EMBER_TYPE_Q8_0 ? 1.5 : 2.0)) return kGemv;
   if (avg_m <= 96.0) return kSkinny;
   return kGemm;
 }
