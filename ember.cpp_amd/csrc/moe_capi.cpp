@@ -20,16 +20,21 @@ constexpr int kMaxK = 64;   // picks live in a 64-entry LDS array per wave
 enum PathMode { kGemv = 0, kSkinny = 1, kGemm = 2 };
 int path_mode(int type_in, int K_in, int type_out, int K_out, double avg_m) {
   if (!gemm_supported(type_in, K_in) || !gemm_supported(type_out, K_out)) return kGemv;
-  static const int forced = [] {
-    const char* v = std::getenv("EMBER_MOE_PATH");  // tuning override: gemv | skinny | gemm
+  // tuning override: gemv | skinny | gemm (read per call, so a test can select each kernel)
+  const int forced = [] {
+    const char* v = std::getenv("EMBER_MOE_PATH");
     if (!v) return -1;
     const std::string s(v);
     return s == "gemv" ? kGemv : s == "skinny" ? kSkinny : s == "gemm" ? kGemm : -1;
   }();
   if (forced >= 0) return forced;
-  // Q8_0 (its DMA tile kernels): measured crossover between 1 and 2 tokens per expert (C2 T = 4: GEMV
-  // 255 vs 291 us; T = 8: 382 vs 342 us with the prefill pack, about even without it)
-  if (avg_m <= (type_in == EMBER_TYPE_Q8_0 && type_out == EMBER_TYPE_Q8_0 ? 1.5 : 2.0)) return kGemv;
+  // Q8_0 (its DMA tile kernels): the GEMV up to 1.5 tokens per expert (C2 T = 4: GEMV 255 vs 291 us;
+  // T = 8: 382 vs 342-359 us), then the 256-token-tile kernel, which skips the empty 32-row subtiles of
+  // a short segment and measured even with or ahead of the 64-token tiles from T = 8 on (C2 T = 32: 361
+  // vs 387 us with the prefill pack, 447 vs 483 without; T = 256: 498 vs 612)
+  const bool q8 = type_in == EMBER_TYPE_Q8_0 && type_out == EMBER_TYPE_Q8_0;
+  if (q8) return avg_m <= 1.5 ? kGemv : kGemm;
+  if (avg_m <= 2.0) return kGemv;
   if (avg_m <= 96.0) return kSkinny;
   return kGemm;
 }

@@ -71,8 +71,8 @@ def test_deepseek_shared_bias_scale(gpu, T):
 
 @pytest.mark.parametrize("wtype,T", [(em.Q8_0, 64), (em.Q8_0, 300), (em.Q4_K, 200), (em.BF16, 130), (em.F16, 96)])
 def test_grouped_gemm_path(gpu, wtype, T):
-    """A few dozen tokens per expert: the skinny MFMA GEMM (64-token tiles); skewed routing (E 32,
-    top-8) leaves ragged expert tiles."""
+    """A few dozen tokens per expert: the 64-token-tile MFMA GEMM (Q8_0: the 256-token-tile kernel,
+    which it takes from 1.5 tokens per expert on); skewed routing (E 32, top-8) leaves ragged tiles."""
     check(em.LayerSpec(d=512, d_ff=768, E=32, k=8, wtype=wtype, seed=11), T)
 
 

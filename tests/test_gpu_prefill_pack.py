@@ -27,7 +27,7 @@ def _run(hl, x, pack: bool):
     return out.cpu().numpy()
 
 
-# T k / E > 96 tokens per expert: the 256-token-tile GEMM; 2 < T k / E <= 96: the 64-token-tile GEMM;
+# more than 1.5 tokens per expert: the 256-token-tile GEMM (short segments skip their empty subtiles);
 # d_ff 704 and d 576 leave partial n-tiles
 @pytest.mark.parametrize("d,d_ff,E,k,T", [(512, 1024, 4, 2, 320), (576, 704, 4, 2, 300), (256, 512, 8, 2, 1024),
                                           (512, 1024, 4, 2, 64), (576, 704, 4, 2, 37), (256, 512, 8, 2, 150)])
@@ -59,3 +59,19 @@ def test_pack_rejected_for_other_layers(gpu):
     out = torch.empty_like(x)
     scratch = torch.empty(need, dtype=torch.uint8, device="cuda")
     assert em.moe_ffn(dl.desc, x, 4, out, scratch) == em.ERR_TYPE
+
+
+@pytest.mark.parametrize("pack", [False, True])
+def test_64_token_tiles_forced(gpu, monkeypatch, pack):
+    """The 64-token-tile Q8_0 kernel (a tuning choice, EMBER_MOE_PATH=skinny) agrees with the default
+    kernel on the oracle's bar, with and without the pack."""
+    spec = em.LayerSpec(d=512, d_ff=704, E=8, k=2, wtype=em.Q8_0, seed=23)
+    hl = em.make_host_layer(spec)
+    x = em.make_input(spec, 90)
+    print(f"64-token tiles forced, pack={pack}", flush=True)
+    monkeypatch.setenv("EMBER_MOE_PATH", "skinny")
+    y = _run(hl, x, pack=pack)
+    if pack:
+        assert same_bits(y, _run(hl, x, pack=False))  # packed and row-sliced tiles: the same bits
+    monkeypatch.delenv("EMBER_MOE_PATH")
+    assert rel_l2(y, run_oracle(hl, x)) < 2e-3
