@@ -42,6 +42,19 @@ def test_pack_same_bits_as_rows(gpu, d, d_ff, E, k, T):
     assert rel_l2(y_pack, run_oracle(hl, x)) < 2e-3
 
 
+def test_pack_deepseek_style_with_shared_expert(gpu):
+    """Sigmoid scoring, selection bias, groups, an output scale and a Q8_0 shared expert (its own GEMM,
+    not in the pack): the routed experts read the pack, same bits."""
+    spec = em.LayerSpec(d=512, d_ff=512, E=16, k=4, wtype=em.Q8_0, scoring=em.SCORE_SIGMOID, renorm=True,
+                        bias_std=1.0, groups_n=4, groups_top=2, out_scale=2.5, d_ff_shared=1024, seed=29)
+    hl = em.make_host_layer(spec)
+    x = em.make_input(spec, 400)
+    print("prefill pack deepseek-style", flush=True)
+    y_pack = _run(hl, x, pack=True)
+    assert same_bits(y_pack, _run(hl, x, pack=False))
+    assert rel_l2(y_pack, run_oracle(hl, x)) < 2e-3
+
+
 def test_pack_rejected_for_other_layers(gpu):
     import torch
 
