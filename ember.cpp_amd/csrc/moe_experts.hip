@@ -31,7 +31,6 @@ namespace ember_moe {
 using namespace ember_math;
 
 
-constexpr int kProjThreads = 512;            // 8 waves per block
 constexpr int kProjLdsBytes = 80 * 1024;     // staged activation rows per block (two blocks per CU)
 
 // f(integral_constant<int, j>) for j = 0 .. N-1 (compile-time ring positions)
