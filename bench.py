@@ -221,8 +221,8 @@ def main():
                          "rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes), then exit")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py runs on one GPU only (asked for {args.gpus}); the multi-GPU layout is a design "
-              f"(DESIGN.md, 'More than one GPU'), not a measured path in this build.", file=sys.stderr)
+        print(f"bench.py runs on one GPU only (asked for {args.gpus}): the multi-GPU layout (tensor parallel "
+              f"decode, expert parallel prefill) is designed, not built or measured.", file=sys.stderr)
         sys.exit(2)
 
     import torch
