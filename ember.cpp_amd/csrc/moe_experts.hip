@@ -225,7 +225,7 @@ __device__ inline void proj_body(const ProjArgs& a, const Dispatch& dp, const Se
     }
     __syncthreads();
     if constexpr (F::QX)
-      stage_rows_quant(v.in, K, rows_idx, nvalid, act_lds, row_lds);
+      stage_rows_quant<F::PLANES>(v.in, K, rows_idx, nvalid, act_lds, row_lds);
     else
       stage_rows_f32<F::NGL>(v.in, K, rows_idx, nvalid, act_lds, row_lds);
     __syncthreads();

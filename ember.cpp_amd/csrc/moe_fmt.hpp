@@ -55,7 +55,7 @@ struct Fmt;
 template <>
 struct Fmt<EMBER_TYPE_F32> {
   static constexpr int CE = 16, NW = 16, NGL = 2;  // activation chunk: 16 floats = 4 granules
-  static constexpr bool QX = false;
+  static constexpr bool QX = false, PLANES = false;
   __host__ __device__ static int64_t row_bytes(int K) { return 4 * (int64_t)K; }
   __device__ static void load(const uint8_t* row, int c, int K, uint32_t* raw) {
     const int n = K - c * CE;  // valid elements (multiple of 4)
@@ -87,7 +87,7 @@ struct Fmt<EMBER_TYPE_F32> {
 template <int FMT>
 struct FmtHalf {
   static constexpr int CE = 32, NW = 16, NGL = 3;  // activation chunk: 32 floats = 8 granules
-  static constexpr bool QX = false;
+  static constexpr bool QX = false, PLANES = false;
   __host__ __device__ static int64_t row_bytes(int K) { return 2 * (int64_t)K; }
   __device__ static void load(const uint8_t* row, int c, int K, uint32_t* raw) {
     const int n = K - c * CE;  // multiple of 8
@@ -132,7 +132,7 @@ struct Fmt<EMBER_TYPE_F16> : FmtHalf<EMBER_TYPE_F16> {};
 template <>
 struct Fmt<EMBER_TYPE_Q8_0> {
   static constexpr int CE = 64, NW = 17, NGL = 3;  // activation chunk: 64 int16 = 8 granules
-  static constexpr bool QX = true;
+  static constexpr bool QX = true, PLANES = false;
   __host__ __device__ static int64_t row_bytes(int K) { return (int64_t)K / 32 * 34; }
   __device__ static void load(const uint8_t* row, int c, int, uint32_t* raw) {
     const uint8_t* p = row + (size_t)c * 68;
@@ -197,8 +197,11 @@ struct Fmt<EMBER_TYPE_Q8_0> {
 // {d, dmin, scales[12]} plus the quarter's 32 bytes of nibbles (low: group 2q, high: group 2q+1).
 template <>
 struct Fmt<EMBER_TYPE_Q4_K> {
+  // PLANES: the int16 activations are staged as byte planes (granule: 8 low bytes x & 0xff, then 8 high
+  // bytes x >> 8), so the nibbles enter v_dot4 as they are: dot(w, x) = 256 dot4(w, x_hi) + dot4(w, x_lo),
+  // exact in int32, instead of being widened to 16-bit pairs for v_dot2
   static constexpr int CE = 64, NW = 12, NGL = 3;
-  static constexpr bool QX = true;
+  static constexpr bool QX = true, PLANES = true;
   __host__ __device__ static int64_t row_bytes(int K) { return (int64_t)K / 256 * 144; }
   __device__ static void load(const uint8_t* row, int c, int, uint32_t* raw) {
     const uint8_t* sb = row + (size_t)(c >> 2) * 144;
@@ -225,37 +228,37 @@ struct Fmt<EMBER_TYPE_Q4_K> {
     int scA, mA, scB, mB;
     scale_min(raw, 2 * q, &scA, &mA);
     scale_min(raw, 2 * q + 1, &scB, &mB);
-    int ia[MT], ib[MT];
+    int ha[MT], hb[MT];
+    uint32_t la[MT], lb[MT];
 #pragma unroll
-    for (int m = 0; m < MT; ++m) ia[m] = ib[m] = 0;
+    for (int m = 0; m < MT; ++m) ha[m] = hb[m] = 0, la[m] = lb[m] = 0u;
 #pragma unroll
     for (int k2 = 0; k2 < 8; k2 += 2) {
-      uint32_t ua[4], ub[4];
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        const uint32_t w = raw[4 + k2 + kk];
-        const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
-        ua[2 * kk] = u16pair(lo, 0);
-        ua[2 * kk + 1] = u16pair(lo, 1);
-        ub[2 * kk] = u16pair(hi, 0);
-        ub[2 * kk + 1] = u16pair(hi, 1);
-      }
+      const uint32_t w0 = raw[4 + k2], w1 = raw[5 + k2];
+      const uint32_t a0 = w0 & 0x0f0f0f0fu, a1 = w1 & 0x0f0f0f0fu;                // group 2q, 8 elements
+      const uint32_t b0 = (w0 >> 4) & 0x0f0f0f0fu, b1 = (w1 >> 4) & 0x0f0f0f0fu;  // group 2q + 1
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
         if (m < nvalid) {
           const uint8_t* xr = lds + m * row_lds;
           const u32x4 xa = *reinterpret_cast<const u32x4*>(lds_granule<3>(xr, c, k2 >> 1));
           const u32x4 xb = *reinterpret_cast<const u32x4*>(lds_granule<3>(xr, c, 4 + (k2 >> 1)));
-          ia[m] = sdot2(ua[0], xa.x, ia[m]);
-          ia[m] = sdot2(ua[1], xa.y, ia[m]);
-          ia[m] = sdot2(ua[2], xa.z, ia[m]);
-          ia[m] = sdot2(ua[3], xa.w, ia[m]);
-          ib[m] = sdot2(ub[0], xb.x, ib[m]);
-          ib[m] = sdot2(ub[1], xb.y, ib[m]);
-          ib[m] = sdot2(ub[2], xb.z, ib[m]);
-          ib[m] = sdot2(ub[3], xb.w, ib[m]);
+          la[m] = __builtin_amdgcn_udot4(a0, xa.x, la[m], false);
+          la[m] = __builtin_amdgcn_udot4(a1, xa.y, la[m], false);
+          ha[m] = __builtin_amdgcn_sdot4((int)a0, (int)xa.z, ha[m], false);
+          ha[m] = __builtin_amdgcn_sdot4((int)a1, (int)xa.w, ha[m], false);
+          lb[m] = __builtin_amdgcn_udot4(b0, xb.x, lb[m], false);
+          lb[m] = __builtin_amdgcn_udot4(b1, xb.y, lb[m], false);
+          hb[m] = __builtin_amdgcn_sdot4((int)b0, (int)xb.z, hb[m], false);
+          hb[m] = __builtin_amdgcn_sdot4((int)b1, (int)xb.w, hb[m], false);
         }
       }
+    }
+    int ia[MT], ib[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      ia[m] = 256 * ha[m] + (int)la[m];
+      ib[m] = 256 * hb[m] + (int)lb[m];
     }
     const float dA = d * (float)scA, mAf = dmin * (float)mA, dB = d * (float)scB, mBf = dmin * (float)mB;
 #pragma unroll
@@ -361,6 +364,7 @@ __device__ inline void quant_block32(const float* src, uint32_t* packed, float* 
 // Stages f32 activation rows rows[0..nrows) of [*][K] into LDS already quantized (act_lds_bytes
 // layout for the quantizing formats: int16 values in rotated 64-element chunks, then the per-block
 // scales, then the per-block sums). One thread per 32-element block.
+template <bool PLANES = false>
 __device__ inline void stage_rows_quant(const float* in, int K, const int* rows, int nrows, uint8_t* lds, int row_lds) {
   const int nb = K / 32;
   const int n = nrows * nb;
@@ -372,9 +376,15 @@ __device__ inline void stage_rows_quant(const float* in, int K, const int* rows,
     quant_block32(in + (size_t)rows[m] * K + (size_t)b * 32, packed, &sc, &sm);
     uint8_t* row = lds + m * row_lds;
 #pragma unroll
-    for (int g = 0; g < 4; ++g)
-      *reinterpret_cast<u32x4*>(row + 16 * swz_granule<3>(b >> 1, (b & 1) * 4 + g)) =
-          u32x4{packed[4 * g], packed[4 * g + 1], packed[4 * g + 2], packed[4 * g + 3]};
+    for (int g = 0; g < 4; ++g) {
+      u32x4 gr{packed[4 * g], packed[4 * g + 1], packed[4 * g + 2], packed[4 * g + 3]};
+      if constexpr (PLANES) {
+        // eight int16 (pairs in .x .. .w) -> eight low bytes, then eight high bytes
+        gr = u32x4{__builtin_amdgcn_perm(gr.y, gr.x, 0x06040200u), __builtin_amdgcn_perm(gr.w, gr.z, 0x06040200u),
+                   __builtin_amdgcn_perm(gr.y, gr.x, 0x07050301u), __builtin_amdgcn_perm(gr.w, gr.z, 0x07050301u)};
+      }
+      *reinterpret_cast<u32x4*>(row + 16 * swz_granule<3>(b >> 1, (b & 1) * 4 + g)) = gr;
+    }
     reinterpret_cast<float*>(row + K * 2)[b] = sc;
     reinterpret_cast<int*>(row + K * 2 + nb * 4)[b] = sm;
   }
