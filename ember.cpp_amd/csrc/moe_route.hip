@@ -405,6 +405,123 @@ __global__ void __launch_bounds__(512) route_dispatch_small(const float* __restr
   }
 }
 
+// Router logits, many tokens x many experts: lane (chain c = lane & 7, pair group g = tid >> 3) runs
+// chain c of PT x PE (token, expert) pairs, tokens tq + GT*i and experts eq + GE*j of the block's
+// tile; the 32 pair groups of a 256-thread block form a GT x GE grid, so a block covers GT*PT tokens x
+// GE*PE experts and a launch has ceil(T / (GT*PT)) x
+// ceil(E / (GE*PE)) blocks (one lane per chain instead of one per pair keeps several hundred blocks
+// in flight at T ~ 100). x and R rows stream through LDS in KT-element K tiles (two buffers, the next
+// tile's loads in flight while this tile's chains run; every tile waits for one memory latency, so
+// the tiles are long); each chain visits its elements 8q + c in
+// increasing q and the eight chains of a pair sit in eight consecutive lanes, combined by shuffles
+// in the reference's order. The eight pair groups of a wave read eight consecutive R rows per step,
+// padded to start 8 banks apart. Each thread converts PT + PE staged floats to double per PT * PE
+// FMAs, so the large-T variant takes 4 x 4 pairs.
+template <int GT, int GE, int PT, int PE, int KT>
+__global__ void __launch_bounds__(256) router_logits_chains(const float* __restrict__ x, const float* __restrict__ R,
+                                                            float* __restrict__ logits, int T, int d, int E) {
+  static_assert(GT * GE == 32, "32 pair groups of 8 chains");
+  constexpr int TT = GT * PT, TE = GE * PE, ROWS = TT + TE;
+  constexpr int LD = KT + 8;
+  constexpr int Q4 = KT / 4;
+  constexpr int PER = (ROWS * Q4 + 255) / 256;
+  __shared__ __align__(16) float buf2[2][ROWS * LD];
+  const int c = threadIdx.x & 7, g = threadIdx.x >> 3;
+  const int tq = g / GE, eq = g % GE;
+  const int t0 = blockIdx.x * TT, e0 = blockIdx.y * TE;
+  const int n8 = d - d % 8;
+  const int ntiles = (n8 + KT - 1) / KT;
+  float4 pre[PER];
+  auto fetch = [&](int kt) {
+    const int k0 = kt * KT, kn = min(KT, n8 - k0);
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const int i = threadIdx.x + u * 256;
+      const int row = i / Q4, col = i % Q4;
+      pre[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (row < ROWS && 4 * col < kn) {
+        if (row < TT) {
+          if (t0 + row < T) pre[u] = *reinterpret_cast<const float4*>(x + (size_t)(t0 + row) * d + k0 + 4 * col);
+        } else if (e0 + row - TT < E) {
+          pre[u] = *reinterpret_cast<const float4*>(R + (size_t)(e0 + row - TT) * d + k0 + 4 * col);
+        }
+      }
+    }
+  };
+  double a[PT][PE];
+#pragma unroll
+  for (int i = 0; i < PT; ++i)
+#pragma unroll
+    for (int j = 0; j < PE; ++j) a[i][j] = 0.0;
+  if (ntiles > 0) fetch(0);
+  for (int kt = 0; kt < ntiles; ++kt) {
+    const int kn = min(KT, n8 - kt * KT);
+    float* buf = buf2[kt & 1];
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const int i = threadIdx.x + u * 256;
+      if (i < ROWS * Q4) *reinterpret_cast<float4*>(buf + (i / Q4) * LD + 4 * (i % Q4)) = pre[u];
+    }
+    __syncthreads();  // two buffers alternate, so one barrier per tile suffices
+    if (kt + 1 < ntiles) fetch(kt + 1);
+    const float* xb = buf + tq * LD + c;
+    const float* rb = buf + (TT + eq) * LD + c;
+    if (kn == KT) {
+      // bursts of NB steps in two register slots: the next burst's LDS reads are issued before this
+      // burst's FMAs (the scheduling barriers keep the compiler from interleaving them into one
+      // read-wait-FMA sequence per step, which waits for one LDS latency every step or two)
+      constexpr int NB = 32 / (PT + PE), NBURST = KT / 8 / NB;
+      static_assert(KT / 8 % NB == 0, "whole bursts per tile");
+      float xs[2][PT][NB], rs[2][PE][NB];
+      auto load = [&](int slot, int b) {
+#pragma unroll
+        for (int q = 0; q < NB; ++q) {
+#pragma unroll
+          for (int i = 0; i < PT; ++i) xs[slot][i][q] = xb[i * GT * LD + 8 * (b * NB + q)];
+#pragma unroll
+          for (int j = 0; j < PE; ++j) rs[slot][j][q] = rb[j * GE * LD + 8 * (b * NB + q)];
+        }
+      };
+      load(0, 0);
+#pragma unroll
+      for (int b = 0; b < NBURST; ++b) {
+        if (b + 1 < NBURST) load((b + 1) & 1, b + 1);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int q = 0; q < NB; ++q)
+#pragma unroll
+          for (int i = 0; i < PT; ++i)
+#pragma unroll
+            for (int j = 0; j < PE; ++j)
+              a[i][j] = __builtin_fma((double)rs[b & 1][j][q], (double)xs[b & 1][i][q], a[i][j]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+      for (int k8 = 0; k8 < kn; k8 += 8)
+#pragma unroll
+        for (int i = 0; i < PT; ++i)
+#pragma unroll
+          for (int j = 0; j < PE; ++j)
+            a[i][j] = __builtin_fma((double)rb[j * GE * LD + k8], (double)xb[i * GT * LD + k8], a[i][j]);
+    }
+  }
+  const int base = (threadIdx.x & 63) & ~7;
+#pragma unroll
+  for (int i = 0; i < PT; ++i)
+#pragma unroll
+    for (int j = 0; j < PE; ++j) {
+      double ch[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) ch[q] = __shfl(a[i][j], base + q, 64);
+      const int t = t0 + tq + GT * i, e = e0 + eq + GE * j;
+      if (c != 0 || t >= T || e >= E) continue;
+      double tail = 0.0;
+      for (int q = n8; q < d; ++q) tail = __builtin_fma((double)R[(size_t)e * d + q], (double)x[(size_t)t * d + q], tail);
+      const double v = (((ch[0] + ch[1]) + (ch[2] + ch[3])) + ((ch[4] + ch[5]) + (ch[6] + ch[7]))) + tail;
+      logits[(size_t)t * E + e] = (float)v;
+    }
+}
+
 // ---------------------------------------------------------------------------------------------
 // Host-side launchers.
 
@@ -413,7 +530,14 @@ int launch_router_logits(const float* x, int T, int d, int E, const float* R, fl
   // rows per block: as many as fit, but no more than keeps >= 256 blocks in flight
   const int EG = max(1, min(router_lds_rows(d), (int)(((int64_t)T * E + 255) / 256)));
   const int64_t lds_blocks = (int64_t)T * ((E + EG - 1) / EG);
-  if (2 * (d + 8) <= kRouterLdsFloats && (lds_blocks <= 1024 || d % 4)) {
+  if (d % 4 == 0 && E >= 16 && T >= 4) {
+    // many experts: one lane per chain; 4 x 8 pairs per block, or 16 x 32 once that still gives 256 blocks
+    if ((int64_t)((T + 15) / 16) * ((E + 31) / 32) < 256) {
+      router_logits_chains<4, 8, 1, 1, 512><<<dim3((T + 3) / 4, (E + 7) / 8), 256, 0, st>>>(x, R, logits, T, d, E);
+    } else {
+      router_logits_chains<4, 8, 4, 4, 128><<<dim3((T + 15) / 16, (E + 31) / 32), 256, 0, st>>>(x, R, logits, T, d, E);
+    }
+  } else if (2 * (d + 8) <= kRouterLdsFloats && (lds_blocks <= 1024 || d % 4)) {
     // few blocks: each stages whole rows once and runs its chains from LDS (one memory latency)
     static const bool lds_ok =
         hipFuncSetAttribute(reinterpret_cast<const void*>(&router_logits_lds), hipFuncAttributeMaxDynamicSharedMemorySize,
