@@ -73,7 +73,7 @@ def _edge_logits(rng, T, E):
 
 @pytest.mark.parametrize("T,E,k", [(1, 8, 2), (8, 8, 2), (13, 64, 6), (128, 128, 8), (7, 200, 5), (9, 16, 16),
                                    (4096, 128, 8), (2048, 8, 2), (6, 4, 7), (3, 256, 8), (40, 256, 8), (5, 300, 10),
-                                   (2, 512, 4), (33, 512, 12)])
+                                   (2, 512, 4), (33, 512, 12), (1000, 256, 8), (1025, 64, 8), (700, 16, 17)])
 @pytest.mark.parametrize("renorm", [True, False])
 def test_route_softmax_bit_exact(gpu, T, E, k, renorm):
     rng = np.random.default_rng(T * 131 + E * 7 + k)
