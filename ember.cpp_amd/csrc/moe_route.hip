@@ -615,9 +615,10 @@ int launch_router_logits(const float* x, int T, int d, int E, const float* R, fl
   // rows per block: as many as fit, but no more than keeps >= 256 blocks in flight
   const int EG = max(1, min(router_lds_rows(d), (int)(((int64_t)T * E + 255) / 256)));
   const int64_t lds_blocks = (int64_t)T * ((E + EG - 1) / EG);
-  if (d % 4 == 0 && E >= 16 && T >= 4) {
-    // many experts: one lane per chain; 4 x 8 pairs per block, or 16 x 32 once that still gives 256 blocks
-    if ((int64_t)((T + 15) / 16) * ((E + 31) / 32) < 256) {
+  if (d % 4 == 0 && ((E >= 16 && T >= 4) || (E >= 8 && T >= 64))) {
+    // one lane per chain; 4 x 8 pairs per block, or (E >= 32) 16 x 32 once that still gives 256 blocks
+    // (with 8 to 15 experts the staged-row kernels below stay ahead up to a few dozen tokens)
+    if (E < 32 || (int64_t)((T + 15) / 16) * ((E + 31) / 32) < 256) {
       router_logits_chains<4, 8, 1, 1, 512><<<dim3((T + 3) / 4, (E + 7) / 8), 256, 0, st>>>(x, R, logits, T, d, E);
     } else {
       router_logits_chains<4, 8, 4, 4, 128><<<dim3((T + 15) / 16, (E + 31) / 32), 256, 0, st>>>(x, R, logits, T, d, E);
