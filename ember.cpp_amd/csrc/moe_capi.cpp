@@ -154,6 +154,12 @@ Layout layout(const ember_moe_layer* w, int T) {
   l.mode_shared = w->d_ff_shared > 0
                       ? path_mode(w->gate_shared_type, w->d, w->down_shared_type, w->d_ff_shared, (double)T)
                       : kGemv;
+  // a shared expert of the routed experts' types rides in the routed decode launches as one more segment
+  // (a few µs), while on its own its T rows make a dense MFMA launch of only d_ff_shared / 128 blocks
+  // (C4, T = 4: 205 µs with it on the MFMA path, 100 µs in the routed launches)
+  if (w->d_ff_shared > 0 && l.mode == kGemv && w->gate_shared_type == w->gate_type &&
+      w->down_shared_type == w->down_type)
+    l.mode_shared = kGemv;
   const size_t tiles = l.mode == kGemm     ? (size_t)gemm_max_tiles(T, w->k, w->E)
                        : l.mode == kSkinny ? (size_t)gemm_skinny_max_tiles(T, w->k, w->E)
                                            : 0;
