@@ -6,6 +6,7 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <cmath>
 #include <string>
 
 #include "moe_internal.hpp"
@@ -18,7 +19,7 @@ constexpr int kMaxK = 64;   // picks live in a 64-entry LDS array per wave
 // Expert-product kernels by tokens per expert (M): the int16-dot GEMV while M is at most a few tokens,
 // the skinny MFMA GEMM (64-token tiles) for up to ~100, the 256-token-tile MFMA GEMM beyond.
 enum PathMode { kGemv = 0, kSkinny = 1, kGemm = 2 };
-int path_mode(int type_in, int K_in, int type_out, int K_out, double avg_m) {
+int path_mode(int type_in, int K_in, int type_out, int K_out, double avg_m, int E) {
   if (!gemm_supported(type_in, K_in) || !gemm_supported(type_out, K_out)) return kGemv;
   // tuning override: gemv | skinny | gemm (read per call, so a test can select each kernel)
   const int forced = [] {
@@ -34,7 +35,19 @@ int path_mode(int type_in, int K_in, int type_out, int K_out, double avg_m) {
   // vs 387 us with the prefill pack, 447 vs 483 without; T = 256: 498 vs 612)
   const bool q8 = type_in == EMBER_TYPE_Q8_0 && type_out == EMBER_TYPE_Q8_0;
   if (q8) return avg_m <= 1.5 ? kGemv : kGemm;
-  if (avg_m <= 2.0) return kGemv;
+  // BF16 / F16: by the expected tokens per expert HIT, T*k / (E (1 - (1 - 1/E)^(T*k))), since the GEMV's
+  // cost follows the token passes over the hit experts and the MFMA tiles' the hit experts' weights; the
+  // GEMV wins up to ~1.5 (C4-shaped routed experts: T = 8 183 vs 184 us, T = 12 254 vs 202; Qwen-shaped
+  // E = 128: T = 12 204 vs 206, T = 16 243 vs 210; Mixtral-shaped: T = 4 430 vs 671, T = 8 821 vs 691)
+  const bool half = (type_in == EMBER_TYPE_BF16 || type_in == EMBER_TYPE_F16) &&
+                    (type_out == EMBER_TYPE_BF16 || type_out == EMBER_TYPE_F16);
+  if (half && E > 1) {  // (one matrix, the shared expert: its T rows, the threshold below)
+    const double slots = avg_m * E;
+    const double hit = slots > 0.0 ? E * (1.0 - std::pow(1.0 - 1.0 / E, slots)) : 0.0;
+    if (hit <= 0.0 || slots / hit <= 1.55) return kGemv;
+  } else if (avg_m <= 2.0) {
+    return kGemv;
+  }
   if (avg_m <= 96.0) return kSkinny;
   return kGemm;
 }
@@ -150,9 +163,9 @@ Layout layout(const ember_moe_layer* w, int T) {
   l.y = o; o = align_up(o + slots * w->d * 4 * kMaxKSplit);
   l.hs = o; o = align_up(o + (size_t)T * w->d_ff_shared * 4);
   l.ys = o; o = align_up(o + (w->d_ff_shared > 0 ? (size_t)T * w->d * 4 : 0));
-  l.mode = path_mode(w->gate_type, w->d, w->down_type, w->d_ff, (double)T * w->k / w->E);
+  l.mode = path_mode(w->gate_type, w->d, w->down_type, w->d_ff, (double)T * w->k / w->E, w->E);
   l.mode_shared = w->d_ff_shared > 0
-                      ? path_mode(w->gate_shared_type, w->d, w->down_shared_type, w->d_ff_shared, (double)T)
+                      ? path_mode(w->gate_shared_type, w->d, w->down_shared_type, w->d_ff_shared, (double)T, 1)
                       : kGemv;
   // a shared expert of the routed experts' types rides in the routed decode launches as one more segment
   // (a few µs), while on its own its T rows make a dense MFMA launch of only d_ff_shared / 128 blocks
