@@ -5,6 +5,10 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
+#include <map>
+#include <mutex>
+#include <tuple>
 #include <cstdlib>
 #include <cmath>
 #include <string>
@@ -204,6 +208,43 @@ DispatchScratch dispatch_scratch(void* scratch, const RouteLayout& r, int32_t* o
 }
 
 }  // namespace
+
+// Compute units of the current device (cached per device; the table is filled once per device).
+int device_cus() {
+  constexpr int kMaxDev = 64;
+  static std::atomic<int> cus[kMaxDev];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+  if (dev >= kMaxDev) {
+    int n = 0;
+    return hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess ? n : 0;
+  }
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n == 0 && hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
+    cus[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
+// Blocks per CU of a kernel at a dynamic LDS size on the current device (hipFuncSetAttribute for the
+// LDS size, then the occupancy query), cached per (kernel, device, LDS bytes) under a lock.
+int blocks_per_cu(const void* fn, int threads, size_t lds, size_t max_lds) {
+  static std::mutex mu;
+  static std::map<std::tuple<const void*, int, size_t>, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  std::lock_guard<std::mutex> g(mu);
+  const auto key = std::make_tuple(fn, dev, lds);
+  auto it = cache.find(key);
+  if (it != cache.end()) return it->second;
+  int n = 0;
+  if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)max_lds) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, threads, lds) != hipSuccess)
+    return 0;
+  n = std::max(n, 1);
+  cache.emplace(key, n);
+  return n;
+}
+
 }  // namespace ember_moe
 
 using namespace ember_moe;
@@ -265,7 +306,9 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
   // one token on the decode path: the router, the routing and the dispatch run inside the gate/up launch
   // (its block 0 publishes them; the other blocks wait), saving two launches on the latency path
   static const bool fuse_ok = [] { const char* v = std::getenv("EMBER_FUSE_ROUTE"); return !(v && atoi(v) == 0); }();
-  const bool fuse_route = fuse_ok && l.mode == kGemv && T == 1 && fused_route_fits(d, E, k);
+  // (the router blocks are one per expert and must fit the device's CUs: fewer CUs than experts take the
+  // unfused launches)
+  const bool fuse_route = fuse_ok && l.mode == kGemv && T == 1 && fused_route_fits(d, E, k) && E <= device_cus();
   auto* flag = at<unsigned long long>(scratch, l.flag);
   mark(ev, 0, st);
   if (!fuse_route && (s = launch_router_logits(x, T, d, E, w->router, logits, st))) return s;
@@ -389,12 +432,19 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
       r.used = ds.used;
       r.n_used = ds.n_used;
       r.perm = perm;
+      // A poll is one device-coherent load (an L2 round trip) plus a short sleep; the router blocks
+      // publish within a few microseconds, so 4096 polls only run out when a router block is not
+      // resident. The test hook makes every block compute every logit itself.
+      const char* tv = std::getenv("EMBER_MOE_TEST_ROUTE_NOPUBLISH");  // read per call: tests toggle it
+      const bool test_nopub = tv && atoi(tv) != 0;
+      r.no_publish = test_nopub ? 1 : 0;
+      r.spin_limit = test_nopub ? 4u : 4096u;
     }
     if ((s = launch_projection(a, st))) return s;
     mark(ev, 4, st);
     a.route = ProjArgs::Route{};
-    a.clear_flag = fuse_route ? flag : nullptr;  // the down launch resets the flag words for the next call
-    a.clear_n = E + 2;
+    a.clear_flag = fuse_route ? flag + 2 : nullptr;  // the down launch resets the logit words for the next call
+    a.clear_n = E;
     a.type = w->down_type;
     a.gated = false;
     a.w0 = w->down;
@@ -502,6 +552,24 @@ int ember_moe_ffn_timed(const ember_moe_layer* w, const float* x, int T, float* 
   }
   for (int i = 0; i < 12; ++i) hipEventDestroy(ev[i]);
   return s;
+}
+
+int ember_moe_scratch_routing(const ember_moe_layer* w, int T, ember_moe_routing_view* v) {
+  const int s = validate(w);
+  if (s) return s;
+  if (T < 0) return EMBER_ERR_SHAPE;
+  if (!v) return EMBER_ERR_NULL;
+  const Layout l = layout(w, std::max(T, 1));
+  v->logits = l.logits;
+  v->idx = l.idx;
+  v->gates = l.gates;
+  v->offsets = l.offsets;
+  v->perm = l.perm;
+  v->pos = l.r.pos;
+  v->used = l.r.used;
+  v->n_used = l.r.n_used;
+  v->fallbacks = l.flag;
+  return EMBER_OK;
 }
 
 size_t ember_moe_prefill_pack_bytes(const ember_moe_layer* w) {

@@ -411,12 +411,16 @@ __device__ inline void fused_dispatch(const int* picks, int nv, int E, int32_t* 
 // Every block (router blocks after their own logit): collects every expert's tagged logit (bounded
 // wait), runs route_token (exp tables staged at the start of the launch; every block computes the same
 // routing, so no second hop through one block is needed) and fills its dispatch arrays; block 0 also
-// writes the routing and dispatch for the later launches. False: a logit never arrived (the block then
-// does nothing; the layer is not computed).
+// writes the routing and dispatch for the later launches. A logit that has not arrived when the wait's
+// bound runs out (its router block not resident, e.g. while other work holds the CUs) is computed by
+// the waiting block itself with the same code the router block runs, so the picks never depend on the
+// other blocks being resident; each block that does so adds one to the flag area's word 0 (a
+// diagnostic count for the host, never cleared by the library).
 template <int NT>
-__device__ bool route_block(const ProjArgs& a, uint8_t* ra, int32_t* s_off, int32_t* s_used, int32_t* s_n,
-                            int32_t* s_perm) {
-  __shared__ int missing;
+__device__ void route_block(const ProjArgs& a, uint8_t* lds, uint8_t* ra, int32_t* s_off, int32_t* s_used,
+                            int32_t* s_n, int32_t* s_perm) {
+  __shared__ uint8_t missing[kMaxRouteE];
+  __shared__ int any_missing;
   const ProjArgs::Route& r = a.route;
   const int t = threadIdx.x;
   float* lg = reinterpret_cast<float*>(ra);
@@ -424,26 +428,37 @@ __device__ bool route_block(const ProjArgs& a, uint8_t* ra, int32_t* s_off, int3
   float* pgate = reinterpret_cast<float*>(ra + 2048 + 256);
   uint8_t* wl = ra + 2048 + 512;
   const int E = r.E, k = a.k;
-  if (t == 0) missing = 0;
+  if (t == 0) any_missing = 0;
   __syncthreads();
   for (int e = t; e < E; e += NT) {
     unsigned long long w;
     unsigned n = 0;
     while (((w = __hip_atomic_load(r.flag + 2 + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) >> 32) != kLogitTag) {
-      if (++n > (1u << 22)) break;
+      if (++n > r.spin_limit) break;
       __builtin_amdgcn_s_sleep(1);
     }
-    if ((w >> 32) != kLogitTag) missing = 1;
+    const bool got = (w >> 32) == kLogitTag;
+    missing[e] = got ? 0 : 1;
+    if (!got) any_missing = 1;
     lg[e] = __builtin_bit_cast(float, (uint32_t)w);
   }
   __syncthreads();
-  if (missing) return false;
+  if (any_missing) {
+    for (int e = 0; e < E; ++e)
+      if (missing[e]) {  // block-uniform (LDS)
+        const float v = router_block_logit<NT>(a, e, lds);
+        if (t == 0) lg[e] = v;
+      }
+    if (t == 0) __hip_atomic_fetch_add(r.flag, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+  }
   if (t < 64)
     route_token(lg, E, k, r.renorm, r.routed, r.sigmoid, r.bias, r.groups_n, r.groups_top, wl, pidx, pgate, true);
   __syncthreads();
   int nv = 0;  // valid picks: a prefix (route_token puts the -1 entries last)
   for (int j = 0; j < k; ++j) nv += pidx[j] >= 0;
   if (blockIdx.x == 0) {
+    for (int e = t; e < E; e += NT) r.logits[e] = lg[e];
     if (t < k) {
       r.idx[t] = pidx[t];
       r.gates[t] = pgate[t];
@@ -462,7 +477,6 @@ __device__ bool route_block(const ProjArgs& a, uint8_t* ra, int32_t* s_off, int3
   }
   fused_dispatch(pidx, nv, E, s_off, s_used, s_n, s_perm);
   __syncthreads();
-  return true;
 }
 
 template <int FMT, int MT, bool GATED, int NB, int NT, int WPE, bool ROUTE>
@@ -476,15 +490,14 @@ __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) 
     const int b = blockIdx.x;
     uint8_t* ra = act_lds + fused_router_lds(a.route.d);  // the routing area, after the products
     if (threadIdx.x < 64) route_stage_tables(ra + 2048 + 512);
-    if (b < a.route.E) {  // router block: its expert's logit, published tagged
+    if (b < a.route.E && !a.route.no_publish) {  // router block: its expert's logit, published tagged
       const float v = router_block_logit<NT>(a, b, act_lds);
       if (threadIdx.x == 0) {
-        a.route.logits[b] = v;
         __hip_atomic_store(a.route.flag + 2 + b, ((unsigned long long)kLogitTag << 32) | __builtin_bit_cast(uint32_t, v),
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
-    if (!route_block<NT>(a, ra, s_off, s_used, &s_n, s_perm)) return;
+    route_block<NT>(a, act_lds, ra, s_off, s_used, &s_n, s_perm);
     __syncthreads();  // the routing work area (act_lds) is free for the activations
     Dispatch dp{s_n, s_used, s_off, s_perm};
     SegView v;
@@ -500,24 +513,12 @@ __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) 
 template <int FMT, int MT, bool GATED, int NB, int NT, int WPE, bool ROUTE = false>
 int launch_proj_cfg(const ProjArgs& a_in, size_t act_lds, hipStream_t st) {
   const void* fn = reinterpret_cast<const void*>(&proj_kernel<FMT, MT, GATED, NB, NT, WPE, ROUTE>);
-  static const bool attr_ok =
-      hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kProjLdsBytes) == hipSuccess;
-  if (!attr_ok) return EMBER_ERR_LAUNCH;
   const ProjArgs& a = a_in;
   const size_t lds = ROUTE ? std::max(act_lds, fused_router_lds(a.route.d) + fused_route_lds(a.route.E)) : act_lds;
-  // blocks per CU at this LDS size (cached per size; the launch is sized to one resident wave of blocks)
-  static size_t cached_lds = (size_t)-1;
-  static int cached_bpc = 1;
-  if (cached_lds != lds) {
-    int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, NT, lds) != hipSuccess) return EMBER_ERR_LAUNCH;
-    cached_bpc = std::max(n, 1);
-    cached_lds = lds;
-  }
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-    return EMBER_ERR_LAUNCH;
+  // blocks per CU at this LDS size (the launch is sized to one resident wave of blocks)
+  const int cached_bpc = blocks_per_cu(fn, NT, lds, kProjLdsBytes);
+  const int cus = device_cus();
+  if (cached_bpc <= 0 || cus <= 0) return EMBER_ERR_LAUNCH;
   static const int bpc_override = [] { const char* e = std::getenv("EMBER_PROJ_BPC"); return e ? atoi(e) : 0; }();
   const int bpc = bpc_override > 0 ? std::min(bpc_override, cached_bpc) : cached_bpc;
   const int segs = (a.used ? std::max(a.max_segments, 1) : 0) + (a.s_w0 ? 1 : 0);

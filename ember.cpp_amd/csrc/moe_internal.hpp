@@ -49,6 +49,11 @@ int launch_route_dispatch(const float* logits, int T, int E, int k, int renorm, 
                           const DispatchScratch& ds, hipStream_t st);
 
 bool type_quantizes_activations(int type);
+// Compute units of the current device (0 on error); cached per device.
+int device_cus();
+// Blocks per CU of kernel fn with `threads` threads and `lds` dynamic LDS bytes on the current device
+// (its dynamic-LDS limit raised to max_lds first); 0 on error. Cached per (kernel, device, LDS), thread-safe.
+int blocks_per_cu(const void* fn, int threads, size_t lds, size_t max_lds);
 int proj_max_row_bytes();  // LDS bytes one staged activation row of the decode kernel may take
 
 // One projection launch over expert segments: out[p][row] for rows [0, rows) of a [rows][K] matrix
@@ -83,12 +88,13 @@ struct ProjArgs {
   // host side only: when set, the launch records these events in its dispatch packet (kernel timing)
   hipEvent_t ev_start, ev_stop;
   // Routing fused into a one-token gate/up launch (route.flag non-null): blocks 0..E-1 each compute
-  // one expert's router logit and publish it in a tagged word of the flag area; every block collects
-  // them, computes the same picks and gates and builds the one-token dispatch; block 0 also writes the
-  // routing and dispatch (idx, gates, pos, offsets, used, n_used, perm) for the later launches. A
-  // later launch of the same call (clear_flag) zeroes the E + 2
-  // words, so stale words never carry a tag (a word of uninitialised scratch matches a 32-bit tag by
-  // chance with probability 2^-32).
+  // one expert's router logit and publish it in a tagged word of the flag area (words 2..E+1); every
+  // block collects them (a logit still missing after spin_limit polls it computes itself), computes the
+  // same picks and gates and builds the one-token dispatch; block 0 also writes the routing and
+  // dispatch (idx, gates, pos, offsets, used, n_used, perm) for the later launches. A later launch of
+  // the same call (clear_flag) zeroes the E logit words, so stale words never carry a tag (a word of
+  // uninitialised scratch matches a 32-bit tag by chance with probability 2^-32). Word 0 counts the
+  // blocks that computed a missing logit themselves.
   struct Route {
     unsigned long long* flag;  // E + 2 words
     const float* x;       // the token [d]
@@ -100,6 +106,8 @@ struct ProjArgs {
     float* gates;         // [k]
     int32_t* pos;         // [k]
     int32_t *offsets, *used, *n_used, *perm;  // the dispatch (the launch's read-only views alias these)
+    unsigned spin_limit;  // polls of a logit word before the block computes that logit itself
+    int no_publish;       // test hook: router blocks do not publish (every block computes every logit)
   } route;
   unsigned long long* clear_flag;  // non-null: block 0 of this launch zeroes clear_n words of the flag area
   int clear_n;

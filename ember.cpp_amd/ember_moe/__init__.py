@@ -58,6 +58,13 @@ class Layer(ctypes.Structure):
     ]
 
 
+class RoutingView(ctypes.Structure):
+    """ember_moe_routing_view (include/ember_moe.h): byte offsets of a call's routing in its scratch."""
+
+    _fields_ = [(n, ctypes.c_size_t) for n in
+                ("logits", "idx", "gates", "offsets", "perm", "pos", "used", "n_used", "fallbacks")]
+
+
 _lib = None
 _host = None
 
@@ -115,6 +122,8 @@ def lib() -> ctypes.CDLL:
         L.ember_moe_prefill_pack_bytes.restype = sz
         L.ember_moe_prefill_pack.argtypes = [ctypes.POINTER(Layer), vp, sz, vp]
         L.ember_moe_prefill_pack.restype = i
+        L.ember_moe_scratch_routing.argtypes = [ctypes.POINTER(Layer), i, ctypes.POINTER(RoutingView)]
+        L.ember_moe_scratch_routing.restype = i
         L.ember_moe_strerror.argtypes = [i]
         L.ember_moe_strerror.restype = ctypes.c_char_p
         L.ember_gguf_layer_bytes.argtypes = [ctypes.POINTER(GgufMoe)]
@@ -261,6 +270,27 @@ def moe_ffn(layer: Layer, x, T: int, out, scratch, scratch_nbytes: Optional[int]
     """Calls ember_moe_ffn; returns the status (0 on success)."""
     n = scratch_nbytes if scratch_nbytes is not None else (scratch.numel() * scratch.element_size() if scratch is not None else 0)
     return int(lib().ember_moe_ffn(ctypes.byref(layer), _ptr(x), T, _ptr(out), _ptr(scratch), n, _stream(stream)))
+
+
+def scratch_routing(layer: Layer, T: int, scratch) -> dict:
+    """The routing a completed ember_moe_ffn call left in `scratch` (a uint8 device tensor), copied to the
+    host: logits [T][E], idx / gates [T][k], offsets [E+1], perm / pos [T*k], used [n_used], fallbacks."""
+    v = RoutingView()
+    st = lib().ember_moe_scratch_routing(ctypes.byref(layer), T, ctypes.byref(v))
+    if st:
+        raise EmberError(st, "ember_moe_scratch_routing")
+    E, k = layer.E, layer.k
+    raw = scratch.cpu().numpy()
+
+    def arr(off, n, dt):
+        return raw[off:off + n * np.dtype(dt).itemsize].view(dt).copy()
+
+    n_used = int(arr(v.n_used, 1, np.int32)[0])
+    return dict(logits=arr(v.logits, T * E, np.float32).reshape(T, E),
+                idx=arr(v.idx, T * k, np.int32).reshape(T, k), gates=arr(v.gates, T * k, np.float32).reshape(T, k),
+                offsets=arr(v.offsets, E + 1, np.int32), perm=arr(v.perm, T * k, np.int32),
+                pos=arr(v.pos, T * k, np.int32), used=arr(v.used, max(min(n_used, E), 0), np.int32),
+                n_used=n_used, fallbacks=int(arr(v.fallbacks, 1, np.uint64)[0]))
 
 
 PHASES = ("router", "route", "dispatch", "gate_up", "down", "shared", "combine")

@@ -58,6 +58,24 @@ typedef struct ember_moe_layer {
  * cuda_kernels.h:678, in bytes). Returns 0 for an invalid descriptor. */
 size_t ember_moe_scratch_bytes(const ember_moe_layer* w, int T);
 
+/* Where ember_moe_ffn leaves its routing in the scratch buffer (byte offsets from its start), for
+ * callers and tests that inspect a call's routing after it completes (no reference counterpart; it
+ * plays the role of reading back moe_route_sel_kernel's outputs, cuda_kernels.cu:3565-3604):
+ *   logits    f32 [T][E]   router logits
+ *   idx       i32 [T][k]   picks, ascending expert ids (-1: none); gates f32 [T][k] their weights
+ *   offsets   i32 [E+1]    expert segment starts in the dispatch order; perm i32 [T*k] the slot t*k+j
+ *                          at each dispatch position; pos i32 [T*k] slot -> position (-1: no pick)
+ *   used      i32 [E]      experts with at least one slot, ascending; n_used i32 their count
+ *   fallbacks u64          one-token calls whose routing is fused into the expert launch: the number of
+ *                          blocks that stopped waiting for another block's router logit and computed it
+ *                          themselves (results are identical either way; a diagnostic that only grows,
+ *                          from whatever the buffer held, and is never reset by the library).
+ * The same layout holds for every call with this descriptor and T. */
+typedef struct ember_moe_routing_view {
+  size_t logits, idx, gates, offsets, perm, pos, used, n_used, fallbacks;
+} ember_moe_routing_view;
+int ember_moe_scratch_routing(const ember_moe_layer* w, int T, ember_moe_routing_view* view);
+
 /* Prefill weight packing (no counterpart in the reference, which dequantizes every stack to F32 at
  * load, weight_management.cpp:486-511). The prefill expert GEMM (T k / E > 96 tokens per expert) reads
  * its weights in 256-row x 64-column tiles; ggml rows give it 68-byte row slices 4 KiB-plus apart. A

@@ -44,14 +44,18 @@ def test_full_size_layer(gpu, name, T, sample):
     x = em.make_input(s, T, seed=1000 + T)
     print(f"full-size {name} T={T}", flush=True)
     xd = torch.from_numpy(x).cuda()
-    out, _ = dl.forward(xd)
-    lg = torch.empty((T, s.E), dtype=torch.float32, device="cuda")
-    assert em.router_logits(xd, T, s.d, s.E, dl.tensors["router"], lg) == 0
+    out, scratch = dl.forward(xd)
     torch.cuda.synchronize()
     y = out.cpu().numpy()
     assert np.all(np.isfinite(y))
-    # routing on every token: the device logits equal the oracle's bit for bit
-    assert same_bits(lg.cpu().numpy(), O.router_logits(x, hl.router))
+    # routing on every token, as this call computed it
+    r = em.scratch_routing(dl.desc, T, scratch)
+    lg = O.router_logits(x, hl.router)
+    assert same_bits(r["logits"], lg)
+    idx, gates = O.route(lg, s.k, renorm=s.renorm, bias=hl.bias)
+    assert np.array_equal(r["idx"], idx) and same_bits(r["gates"], gates)
+    offsets, perm = O.dispatch(idx, s.E)
+    assert np.array_equal(r["offsets"], offsets) and np.array_equal(r["perm"], perm)
     rows = np.sort(np.random.default_rng(T).choice(T, size=min(sample, T), replace=False))
     kw = {}
     if s.d_ff_shared:

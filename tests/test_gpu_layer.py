@@ -123,3 +123,22 @@ def test_t_zero_and_errors(gpu):
     assert em.moe_ffn(dl.desc, x, 4, out, scratch) == em.OK
     torch.cuda.synchronize()
     assert not torch.all(out == 7.0)
+
+
+@pytest.mark.parametrize("forced", ["gemv", None])
+@pytest.mark.parametrize("T", [2, 4, 6])
+@pytest.mark.parametrize("shape", ["c4-like", "mixtral-like-f16", "mixed-types"])
+def test_shared_expert_multi_token_gemv(gpu, monkeypatch, shape, T, forced):
+    """A shared expert riding in the multi-token decode launches (one more segment of the routed GEMV
+    launches when its types match the routed experts'; its own launches when they differ). EMBER_MOE_PATH
+    =gemv forces the GEMV for the routed experts; unforced, each layer takes its own path choice."""
+    if forced:
+        monkeypatch.setenv("EMBER_MOE_PATH", forced)
+    if shape == "c4-like":
+        spec = em.LayerSpec(d=2048, d_ff=1408, E=64, k=6, wtype=em.BF16, bias_std=2.0, d_ff_shared=2816, seed=21)
+    elif shape == "mixtral-like-f16":
+        spec = em.LayerSpec(d=1024, d_ff=3584, E=8, k=2, wtype=em.F16, d_ff_shared=1024, out_scale=1.5, seed=22)
+    else:  # BF16 routed experts with a Q8_0 shared expert
+        spec = em.LayerSpec(d=1024, d_ff=768, E=16, k=4, wtype=em.BF16, d_ff_shared=1536, shared_type=em.Q8_0,
+                            seed=23)
+    check(spec, T, seed=300 + T)
