@@ -530,6 +530,48 @@ int ember_moe_ffn(const ember_moe_layer* w, const float* x, int T, float* out, v
   return run_ffn(w, x, T, out, scratch, scratch_bytes, st, nullptr);
 }
 
+}  // extern "C"
+
+// ---- the allocation-free entry point: the library's own scratch in device memory
+// The buffer ember_moe_ffn_noalloc runs in. In host code `scratch` names a host-side stand-in, never
+// the device address: the address comes from hipGetSymbolAddress, once per device, and only that
+// pointer is handed to kernels. It is zero when the code object loads; the fused one-token routing's
+// logit words (its first bytes) are zeroed again by every call's last expert launch, as in a caller's
+// scratch.
+static __device__ __align__(256) uint8_t scratch[EMBER_MOE_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_noalloc_mu;
+void* g_noalloc_ptr[kMaxDevices];  // per device: the device address of `scratch`, or null before set-up
+
+// The device address of this device's copy of `scratch` (set up on the first call on the device).
+void* noalloc_scratch() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> g(g_noalloc_mu);
+  if (!g_noalloc_ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return nullptr;
+    g_noalloc_ptr[dev] = p;
+  }
+  return g_noalloc_ptr[dev];
+}
+}  // namespace
+
+extern "C" {
+
+int ember_moe_ffn_noalloc(const ember_moe_layer* w, const float* x, int T, float* out, hipStream_t st) {
+  int s = validate(w);
+  if (s) return s;
+  if (T < 0) return EMBER_ERR_SHAPE;
+  if (T == 0) return EMBER_OK;
+  if (layout(w, T).end > (size_t)EMBER_MOE_NOALLOC_SCRATCH_BYTES) return EMBER_ERR_SCRATCH;
+  void* p = noalloc_scratch();
+  if (!p) return EMBER_ERR_LAUNCH;
+  return run_ffn(w, x, T, out, p, (size_t)EMBER_MOE_NOALLOC_SCRATCH_BYTES, st, nullptr);
+}
+
 int ember_moe_ffn_timed(const ember_moe_layer* w, const float* x, int T, float* out, void* scratch,
                         size_t scratch_bytes, hipStream_t st, float* phase_ms) {
   if (!phase_ms) return EMBER_ERR_NULL;

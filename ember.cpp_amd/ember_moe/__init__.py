@@ -110,6 +110,8 @@ def lib() -> ctypes.CDLL:
         L.ember_moe_scratch_bytes.restype = sz
         L.ember_moe_ffn.argtypes = [ctypes.POINTER(Layer), vp, i, vp, vp, sz, vp]
         L.ember_moe_ffn.restype = i
+        L.ember_moe_ffn_noalloc.argtypes = [ctypes.POINTER(Layer), vp, i, vp, vp]
+        L.ember_moe_ffn_noalloc.restype = i
         L.ember_moe_ffn_timed.argtypes = [ctypes.POINTER(Layer), vp, i, vp, vp, sz, vp, ctypes.POINTER(ctypes.c_float)]
         L.ember_moe_ffn_timed.restype = i
         L.ember_moe_router_logits.argtypes = [vp, i, i, i, vp, vp, vp]
@@ -291,6 +293,14 @@ def scratch_routing(layer: Layer, T: int, scratch) -> dict:
                 offsets=arr(v.offsets, E + 1, np.int32), perm=arr(v.perm, T * k, np.int32),
                 pos=arr(v.pos, T * k, np.int32), used=arr(v.used, max(min(n_used, E), 0), np.int32),
                 n_used=n_used, fallbacks=int(arr(v.fallbacks, 1, np.uint64)[0]))
+
+
+NOALLOC_SCRATCH_BYTES = 32 << 20  # EMBER_MOE_NOALLOC_SCRATCH_BYTES
+
+
+def moe_ffn_noalloc(layer: Layer, x, T: int, out, stream=None) -> int:
+    """Calls ember_moe_ffn_noalloc (the library's own static scratch); returns the status."""
+    return int(lib().ember_moe_ffn_noalloc(ctypes.byref(layer), _ptr(x), T, _ptr(out), _stream(stream)))
 
 
 PHASES = ("router", "route", "dispatch", "gate_up", "down", "shared", "combine")

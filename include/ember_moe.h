@@ -95,6 +95,18 @@ int ember_moe_prefill_pack(const ember_moe_layer* w, void* pack, size_t pack_byt
 int ember_moe_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* scratch,
                   size_t scratch_bytes, hipStream_t stream);
 
+/* ember_moe_ffn without a caller scratch buffer, for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the
+ * reference (moe_ffn_cuda always takes a caller scratch). It runs exactly ember_moe_ffn's kernels, with
+ * identical results, in a library-owned static device buffer of EMBER_MOE_NOALLOC_SCRATCH_BYTES
+ * (32 MiB) that each GPU the library runs on holds until the process ends; the call allocates nothing
+ * (no hipMalloc / hipFree, no allocating library routine). Calls whose ember_moe_scratch_bytes(w, T)
+ * exceeds that size return EMBER_ERR_SCRATCH and launch nothing (decode batches and prefill of a few
+ * dozen tokens fit Mixtral-sized layers). Every call on one GPU shares that GPU's buffer: calls that
+ * overlap on one GPU (concurrent streams, threads) race and must be serialised by the caller. */
+#define EMBER_MOE_NOALLOC_SCRATCH_BYTES (32u << 20)
+int ember_moe_ffn_noalloc(const ember_moe_layer* w, const float* x, int T, float* out, hipStream_t stream);
+
 /* ember_moe_ffn with per-phase timing (the role of ember's PrefillOpTimer, model.cpp:1927-1975, which
  * brackets each op with CUDA events). Records HIP events between the launches on `stream`, waits for
  * the last one (this call synchronises the host; it is a profiling entry, not for graph capture) and
