@@ -171,10 +171,21 @@ def profiled_traffic(config, T):
     return None
 
 
-def cpu_baseline(hl, x_host, T_headline, max_seconds=20.0):
-    """The reference's CPU path (utils.cpp moe_ffn_f32_cpu over dequantized F32 stacks,
-    weight_management.cpp:802-877), decode T = 1 single-threaded as model.cpp:759 runs it, timed on a
-    bounded sample of tokens of the same layer."""
+def _host_info():
+    import multiprocessing
+
+    return {"nproc": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else multiprocessing.cpu_count(),
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS"), "host_cpu": _cpu_model()}
+
+
+def cpu_baseline(hl, spec, sweep_T, max_seconds=12.0, prefill_seconds=6.0):
+    """The reference's CPU MoE path on the GPU box's host, on F32 stacks dequantized from the same
+    encoded bytes (weight_management.cpp:802-877):
+      decode  moe_ffn_f32_cpu at T = 1, single-threaded, as model.cpp:759 runs it, over a bounded
+              sample of independent tokens;
+      prefill the same function under cpu_batch_processor.cpp:223-231's OpenMP static schedule over the
+              tokens of the batch, on every host core, for each sweep T > 8, timed on a bounded
+              prefix of the batch (tokens are independent, so tokens/s scales to the whole batch)."""
     from oracle import oracle as O
 
     s = hl.spec
@@ -188,21 +199,60 @@ def cpu_baseline(hl, x_host, T_headline, max_seconds=20.0):
     if s.d_ff_shared:
         sh = dict(d_ff_sh=s.d_ff_shared, Gs=hl.dequantized("gate_sh"), Us=hl.dequantized("up_sh"),
                   Ds=hl.dequantized("down_sh"))
-    out = np.empty((1, s.d), np.float32)
-    done, t_start = 0, time.time()
-    while done < x_host.shape[0] and (time.time() - t_start) < max_seconds:
-        xt = np.ascontiguousarray(x_host[done:done + 1])
+    info = _host_info()
+    cores = info["nproc"]
+
+    def run(x, nthreads):
+        out = np.empty_like(x)
         if use_ref:
-            O.ref().ref_moe_ffn_f32(xt.ctypes.data, 1, s.d, s.d_ff, s.E, s.k, R.ctypes.data, G.ctypes.data,
-                                    U.ctypes.data, D.ctypes.data, out.ctypes.data, int(s.renorm))
+            f = O.ref().ref_moe_ffn_f32 if nthreads == 1 else None
+            if f is not None:
+                f(x.ctypes.data, x.shape[0], s.d, s.d_ff, s.E, s.k, R.ctypes.data, G.ctypes.data, U.ctypes.data,
+                  D.ctypes.data, out.ctypes.data, int(s.renorm))
+            else:
+                O.ref().ref_moe_ffn_f32_omp(x.ctypes.data, x.shape[0], s.d, s.d_ff, s.E, s.k, R.ctypes.data,
+                                            G.ctypes.data, U.ctypes.data, D.ctypes.data, out.ctypes.data,
+                                            int(s.renorm), nthreads)
         else:
-            out[:] = O.moe_layer(xt, R, G, U, D, s.d_ff, s.E, s.k, renorm=s.renorm, bias=hl.bias, nthreads=1, **sh)
+            out[:] = O.moe_layer(x, R, G, U, D, s.d_ff, s.E, s.k, renorm=s.renorm, bias=hl.bias, nthreads=nthreads,
+                                 **sh)
+        return out
+
+    x1 = em_input(spec, 1024)
+    done, t_start = 0, time.time()
+    while done < x1.shape[0] and (time.time() - t_start) < max_seconds:
+        run(np.ascontiguousarray(x1[done:done + 1]), 1)
         done += 1
     el = time.time() - t_start
-    return {"value": done / el, "unit": "tokens/s", "cores": 1,
-            "kind": "reference" if use_ref else "port",
-            "sample": f"{done} decode tokens (T=1 calls) of the same layer on F32 stacks dequantized from the "
-                      f"same encoded bytes, single thread, {el:.1f}s"}
+    res = {"value": done / el, "unit": "tokens/s", "cores": 1, "kind": "reference" if use_ref else "port",
+           "sample": f"{done} decode tokens (T=1 calls) of the same layer on F32 stacks dequantized from the "
+                     f"same encoded bytes, single thread, {el:.1f}s", **info}
+    prefill = []
+    for T in sweep_T:
+        if T <= 8:
+            continue
+        x = em_input(spec, T)
+        # a first chunk of one token per core sizes the timed prefix to about prefill_seconds
+        n = min(T, cores)
+        t_s = time.time()
+        run(np.ascontiguousarray(x[:n]), cores)
+        per_tok = (time.time() - t_s) / n
+        n = int(min(T, max(cores, cores * round(prefill_seconds / max(per_tok * cores, 1e-6)))))
+        t_s = time.time()
+        run(np.ascontiguousarray(x[:n]), cores)
+        el = time.time() - t_s
+        prefill.append({"T": T, "value": n / el, "unit": "tokens/s", "cores": cores,
+                        "sample": f"the first {n} of the T={T} batch's tokens, OpenMP static over tokens on "
+                                  f"{cores} threads, {el:.1f}s"})
+        log(f"[bench] cpu prefill T={T}: {n / el:.1f} tokens/s ({n} tokens, {el:.1f}s, {cores} threads)")
+    res["prefill"] = prefill
+    return res
+
+
+def em_input(spec, T):
+    import ember_moe as em
+
+    return em.make_input(spec, T)
 
 
 def main():
@@ -311,8 +361,11 @@ def main():
     }
     if not args.no_cpu:
         try:
-            line["cpu_baseline"] = cpu_baseline(hl, em.make_input(spec, 1024), args.tokens, max_seconds=12.0)
-            line["cpu_baseline"]["host_cpu"] = _cpu_model()
+            line["cpu_baseline"] = cpu_baseline(hl, spec, sweep_T)
+            for p in line["cpu_baseline"]["prefill"]:
+                for r in line["sweep"]:
+                    if r["T"] == p["T"]:
+                        r["cpu_tokens_per_s"] = p["value"]
         except Exception as exc:
             line["cpu_baseline"] = {"value": None, "error": str(exc)}
     print(json.dumps(line), flush=True)

@@ -323,12 +323,24 @@ int ember_gguf_moe_layer(const ember_gguf* g, int layer, ember_gguf_moe* out) {
   out->renorm = 1;
   out->groups_n = out->groups_top = 1;
   out->out_scale = 1.0f;
-  ember_gguf_tensor t;
   if (a == "llama" || a == "mistral" || a == "qwen3moe") {
     // Mixtral's layout and qwen3moe: renorm softmax gates, no shared expert (graph_ir.cpp:681-699)
   } else if (a == "qwen2moe") {
     out->renorm = 0;  // llama.cpp b6000's qwen2moe graph ignores norm_topk_prob (graph_ir.cpp:693-699)
-    if (find(B + "ffn_gate_inp_shexp.weight", &t) == EMBER_OK) return EMBER_ERR_SHAPE;  // gated shared expert
+    // the shared expert joins the FFN only when ffn_gate_inp_shexp gates it (graph_ir.cpp:700-706):
+    // f = f + sigmoid(ffn_gate_inp_shexp · h2) * shared(h2)
+    if (find(B + "ffn_gate_inp_shexp.weight", &out->shared_gate) == EMBER_OK) {
+      const ember_gguf_tensor& g = out->shared_gate;
+      if (g.ne[0] != d || g.ne[1] != 1 || g.ne[2] != 1 || g.ne[3] != 1) return EMBER_ERR_SHAPE;
+      if (find(B + "ffn_gate_shexp.weight", &out->gate_shared) || find(B + "ffn_up_shexp.weight", &out->up_shared) ||
+          find(B + "ffn_down_shexp.weight", &out->down_shared))
+        return EMBER_ERR_SHAPE;
+      const int64_t dfs = out->gate_shared.ne[1];
+      if (dfs <= 0 || !same(out->gate_shared, d, dfs, 1) || !same(out->up_shared, d, dfs, 1) ||
+          !same(out->down_shared, dfs, d, 1))
+        return EMBER_ERR_SHAPE;
+      out->d_ff_shared = (int)dfs;
+    }
   } else if (a == "deepseek2") {
     double gating = num("expert_gating_func", 1.0);
     if (gating == 0.0) gating = 1.0;

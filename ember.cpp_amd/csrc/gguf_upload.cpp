@@ -33,6 +33,7 @@ size_t ember_gguf_layer_bytes(const ember_gguf_moe* m) {
   if (present(m->bias)) n += up((size_t)m->E * sizeof(float));
   n += up(m->gate.bytes) + up(m->up.bytes) + up(m->down.bytes);
   if (m->d_ff_shared > 0) n += up(m->gate_shared.bytes) + up(m->up_shared.bytes) + up(m->down_shared.bytes);
+  if (m->d_ff_shared > 0 && present(m->shared_gate)) n += up((size_t)m->d * sizeof(float));
   return n;
 }
 
@@ -49,6 +50,8 @@ int ember_gguf_upload_layer(const ember_gguf_moe* m, void* dev, size_t dev_bytes
                              !expert_type_ok(m->gate_shared.type) || !expert_type_ok(m->up_shared.type) ||
                              !expert_type_ok(m->down_shared.type)))
     return EMBER_ERR_TYPE;
+  const bool sgate = m->d_ff_shared > 0 && present(m->shared_gate);
+  if (sgate && !router_type_ok(m->shared_gate.type)) return EMBER_ERR_TYPE;
   // the descriptor first, so that its own validation (block widths, alignment) runs before any copy
   ember_moe_layer l{};
   l.d = m->d;
@@ -85,6 +88,8 @@ int ember_gguf_upload_layer(const ember_gguf_moe* m, void* dev, size_t dev_bytes
     l.up_shared_type = m->up_shared.type;
     l.down_shared_type = m->down_shared.type;
   }
+  float* sg = sgate ? static_cast<float*>(place((size_t)m->d * sizeof(float))) : nullptr;
+  l.shared_gate = sg;
   l.router = router;
   l.selection_bias = bias;
   l.gate = gate;
@@ -113,6 +118,18 @@ int ember_gguf_upload_layer(const ember_gguf_moe* m, void* dev, size_t dev_bytes
   if (e == hipSuccess && gs) e = hipMemcpyAsync(gs, m->gate_shared.data, m->gate_shared.bytes, hipMemcpyHostToDevice, stream);
   if (e == hipSuccess && us) e = hipMemcpyAsync(us, m->up_shared.data, m->up_shared.bytes, hipMemcpyHostToDevice, stream);
   if (e == hipSuccess && ds) e = hipMemcpyAsync(ds, m->down_shared.data, m->down_shared.bytes, hipMemcpyHostToDevice, stream);
+  // qwen2moe's shared-expert gate row, F32 on the device like the router (widened exactly)
+  std::vector<float> gf;
+  if (e == hipSuccess && sg) {
+    const void* src = m->shared_gate.data;
+    if (m->shared_gate.type != EMBER_TYPE_F32) {
+      gf.resize((size_t)m->d);
+      if (ember_dequantize(m->shared_gate.type, m->shared_gate.data, (int64_t)gf.size(), gf.data()) != EMBER_OK)
+        return EMBER_ERR_TYPE;
+      src = gf.data();
+    }
+    e = hipMemcpyAsync(sg, src, (size_t)m->d * sizeof(float), hipMemcpyHostToDevice, stream);
+  }
   // the host sources (the mapped file, the dequantized router) must outlive the copies
   if (e == hipSuccess) e = hipStreamSynchronize(stream);
   if (e != hipSuccess) return EMBER_ERR_LAUNCH;

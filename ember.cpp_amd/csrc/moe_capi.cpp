@@ -119,6 +119,10 @@ int validate(const ember_moe_layer* w) {
     if (w->gate_shared_type != w->up_shared_type) return EMBER_ERR_TYPE;
     if (w->d_ff_shared % 4) return EMBER_ERR_SHAPE;
   }
+  if (w->shared_gate) {
+    if (w->d_ff_shared <= 0) return EMBER_ERR_SHAPE;
+    if (reinterpret_cast<uintptr_t>(w->shared_gate) % 16) return EMBER_ERR_ALIGN;
+  }
   if (w->prefill_pack) {
     if (!packable(w)) return EMBER_ERR_TYPE;
     if (reinterpret_cast<uintptr_t>(w->prefill_pack) % 256) return EMBER_ERR_ALIGN;
@@ -145,7 +149,7 @@ RouteLayout route_layout(int T, int E, int k, size_t base) {
 
 struct Layout {
   size_t flag;  // the fused routing's flag words (ProjArgs::Route), at a fixed place: offset 0
-  size_t logits, idx, gates, offsets, perm, h, y, hs, ys;
+  size_t logits, idx, gates, offsets, perm, h, y, hs, ys, sg;
   size_t x16, h16, hs16, tiles, n_tiles;  // MFMA paths
   int mode, mode_shared;                  // PathMode of the routed experts and of the shared expert
   RouteLayout r;
@@ -167,6 +171,7 @@ Layout layout(const ember_moe_layer* w, int T) {
   l.y = o; o = align_up(o + slots * w->d * 4 * kMaxKSplit);
   l.hs = o; o = align_up(o + (size_t)T * w->d_ff_shared * 4);
   l.ys = o; o = align_up(o + (w->d_ff_shared > 0 ? (size_t)T * w->d * 4 : 0));
+  l.sg = o; o = align_up(o + (w->shared_gate ? (size_t)T * 4 : 0));
   l.mode = path_mode(w->gate_type, w->d, w->down_type, w->d_ff, (double)T * w->k / w->E, w->E);
   l.mode_shared = w->d_ff_shared > 0
                       ? path_mode(w->gate_shared_type, w->d, w->down_shared_type, w->d_ff_shared, (double)T, 1)
@@ -517,9 +522,12 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     b.s_out = ys;
     if ((s = launch_projection(b, st))) return s;
   }
+  // qwen2moe's shared-expert gate logit per token: a one-row router (the same FP64 fixed-order dot)
+  float* sg = w->shared_gate ? at<float>(scratch, l.sg) : nullptr;
+  if (sg && (s = launch_router_logits(x, T, d, 1, w->shared_gate, sg, st))) return s;
   mark(ev, 6, st);
-  s = launch_combine(y, ksplit, (int64_t)T * k * d, gates, ds.pos, ys, w->out_scale == 0.0f ? 1.0f : w->out_scale, T,
-                     k, d, out, st);
+  s = launch_combine(y, ksplit, (int64_t)T * k * d, gates, ds.pos, ys, sg, w->out_scale == 0.0f ? 1.0f : w->out_scale,
+                     T, k, d, out, st);
   mark(ev, 7, st);
   return s;
 }

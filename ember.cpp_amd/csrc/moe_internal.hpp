@@ -181,7 +181,7 @@ int gemm_skinny_ksplit(int type, int max_mtiles, int N, int K);
 int gemm_ksplit(int type, int T, int k, int E, int N, int K);
 
 int launch_combine(const float* y, int nparts, int64_t part_stride, const float* gates, const int32_t* pos,
-                   const float* y_shared, float scale, int T,
+                   const float* y_shared, const float* shared_gate_logit, float scale, int T,
                    int k, int d, float* out, hipStream_t st);
 
 }  // namespace ember_moe

@@ -55,6 +55,7 @@ class Layer(ctypes.Structure):
         ("up_shared", ctypes.c_void_p), ("up_shared_type", ctypes.c_int),
         ("down_shared", ctypes.c_void_p), ("down_shared_type", ctypes.c_int),
         ("prefill_pack", ctypes.c_void_p),
+        ("shared_gate", ctypes.c_void_p),
     ]
 
 
@@ -86,7 +87,7 @@ class GgufMoe(ctypes.Structure):
                 ("d_ff_shared", ctypes.c_int),
                 ("router", GgufTensor), ("gate", GgufTensor), ("up", GgufTensor), ("down", GgufTensor),
                 ("bias", GgufTensor), ("gate_shared", GgufTensor), ("up_shared", GgufTensor),
-                ("down_shared", GgufTensor)]
+                ("down_shared", GgufTensor), ("shared_gate", GgufTensor)]
 
 
 def lib_path() -> str:
@@ -352,13 +353,15 @@ class LayerSpec:
     out_scale: float = 1.0
     d_ff_shared: int = 0
     shared_type: Optional[int] = None
+    shared_gated: bool = False     # qwen2moe: the shared expert scaled by sigmoid(shared_gate . x)
     weight_std: float = 0.02
     router_std: Optional[float] = None  # default 1/sqrt(d)
     seed: int = 0
 
 
 # generator streams for each tensor of a layer
-_STREAM = {"router": 1, "gate": 2, "up": 3, "down": 4, "bias": 5, "gate_sh": 6, "up_sh": 7, "down_sh": 8, "x": 100}
+_STREAM = {"router": 1, "gate": 2, "up": 3, "down": 4, "bias": 5, "gate_sh": 6, "up_sh": 7, "down_sh": 8,
+           "shared_gate": 9, "x": 100}
 
 
 @dataclass
@@ -374,6 +377,7 @@ class HostLayer:
     gate_sh: Optional[np.ndarray] = None
     up_sh: Optional[np.ndarray] = None
     down_sh: Optional[np.ndarray] = None
+    shared_gate: Optional[np.ndarray] = None  # f32 [d] (qwen2moe's ffn_gate_inp_shexp)
 
     def dequantized(self, name: str) -> np.ndarray:
         """The F32 stack the reference would hold after dequantize-at-load (weight_management.cpp:802-877)."""
@@ -407,6 +411,8 @@ def make_host_layer(spec: LayerSpec) -> HostLayer:
         hl.gate_sh = stack("gate_sh", s.d_ff_shared * s.d, st)
         hl.up_sh = stack("up_sh", s.d_ff_shared * s.d, st)
         hl.down_sh = stack("down_sh", s.d * s.d_ff_shared, st)
+        if s.shared_gated:
+            hl.shared_gate = normal(s.d, s.seed, _STREAM["shared_gate"], 0.0, 1.0 / np.sqrt(s.d))
     return hl
 
 
@@ -432,7 +438,7 @@ class DeviceLayer:
         def up(a):
             return torch.from_numpy(np.ascontiguousarray(a)).to(device)
 
-        for name in ("router", "gate", "up", "down", "bias", "gate_sh", "up_sh", "down_sh"):
+        for name in ("router", "gate", "up", "down", "bias", "gate_sh", "up_sh", "down_sh", "shared_gate"):
             a = getattr(hl, name)
             if a is not None:
                 dl.tensors[name] = up(a)
@@ -453,6 +459,7 @@ class DeviceLayer:
             L.gate_shared, L.gate_shared_type = _ptr(t["gate_sh"]), st
             L.up_shared, L.up_shared_type = _ptr(t["up_sh"]), st
             L.down_shared, L.down_shared_type = _ptr(t["down_sh"]), st
+            L.shared_gate = _ptr(t.get("shared_gate"))
         return dl
 
     def forward(self, x, out=None, scratch=None, stream=None):

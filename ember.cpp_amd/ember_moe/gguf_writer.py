@@ -88,7 +88,8 @@ def write_gguf(path: str, meta: dict, tensors: Sequence[tuple], alignment: int =
 def moe_layer_tensors(hl, layer: int, router_type: int = 0) -> list:
     """GGUF tensors of one ember_moe.HostLayer as llama.cpp names and lays them out: router
     ffn_gate_inp [E][d] (ne {d, E}), ffn_{gate,up}_exps ne {d, d_ff, E}, ffn_down_exps ne {d_ff, d, E},
-    and for a DeepSeek-style layer exp_probs_b.bias and ffn_{gate,up,down}_shexp."""
+    and for a DeepSeek-style layer exp_probs_b.bias and ffn_{gate,up,down}_shexp (qwen2moe's gated shared
+    expert adds ffn_gate_inp_shexp)."""
     from . import F32, quantize
 
     s = hl.spec
@@ -105,6 +106,8 @@ def moe_layer_tensors(hl, layer: int, router_type: int = 0) -> list:
         out += [(B + "ffn_gate_shexp.weight", st, (s.d, s.d_ff_shared), hl.gate_sh),
                 (B + "ffn_up_shexp.weight", st, (s.d, s.d_ff_shared), hl.up_sh),
                 (B + "ffn_down_shexp.weight", st, (s.d_ff_shared, s.d), hl.down_sh)]
+        if hl.shared_gate is not None:
+            out.append((B + "ffn_gate_inp_shexp.weight", F32, (s.d,), hl.shared_gate))
     return out
 
 

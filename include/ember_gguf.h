@@ -55,8 +55,9 @@ int ember_gguf_n_layers(const ember_gguf* g); /* {arch}.block_count, or -1 */
 
 /* Mixture-of-experts layer `layer` of the file, as the reference's IR builder reads it:
  *   llama / mistral (Mixtral's layout): softmax, renorm (graph_ir.cpp:681-690);
- *   qwen3moe: softmax, renorm; qwen2moe: softmax, raw gates, and a file whose shared expert is gated
- *     by ffn_gate_inp_shexp is not supported (EMBER_ERR_SHAPE) (graph_ir.cpp:694-705);
+ *   qwen3moe: softmax, renorm; qwen2moe: softmax, raw gates, and, when the file has
+ *     ffn_gate_inp_shexp, the shared expert ffn_{gate,up,down}_shexp scaled per token by
+ *     sigmoid(ffn_gate_inp_shexp · h) (graph_ir.cpp:694-705);
  *   deepseek2: expert_gating_func (1 softmax, 2 sigmoid), expert_weights_norm (renorm), expert_weights_scale,
  *     exp_probs_b.bias as the selection bias, expert_group_count / expert_group_used_count, and the
  *     ungated shared expert ffn_{gate,up,down}_shexp (graph_ir.cpp:832-851, 911-928).
@@ -75,6 +76,7 @@ typedef struct ember_gguf_moe {
   ember_gguf_tensor router, gate, up, down;
   ember_gguf_tensor bias;                               /* name NULL: none */
   ember_gguf_tensor gate_shared, up_shared, down_shared; /* name NULL: none */
+  ember_gguf_tensor shared_gate;                        /* qwen2moe ffn_gate_inp_shexp ne {d}; name NULL: none */
 } ember_gguf_moe;
 int ember_gguf_moe_layer(const ember_gguf* g, int layer, ember_gguf_moe* out);
 

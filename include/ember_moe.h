@@ -52,6 +52,10 @@ typedef struct ember_moe_layer {
   /* Optional (NULL: none): the routed Q8_0 stacks repacked for the prefill MFMA path by
    * ember_moe_prefill_pack. Appended last, so descriptors that zero-initialise keep working. */
   const void* prefill_pack;
+  /* Optional (NULL: none; requires d_ff_shared > 0): qwen2moe's shared-expert gate ffn_gate_inp_shexp,
+   * f32 [d] on the device. The shared expert's output row of token t is scaled by
+   * sigmoid(shared_gate · x_t) before it is added (graph_ir.cpp:694-705). Appended last. */
+  const float* shared_gate;
 } ember_moe_layer;
 
 /* Scratch bytes ember_moe_ffn needs for T tokens of this layer (moe_ffn_scratch_floats' role,

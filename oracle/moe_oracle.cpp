@@ -322,12 +322,14 @@ void oracle_dispatch(const int32_t* idx, int T, int k, int E, int32_t* offsets, 
 // moe_ffn op (graph_ir.cpp:2704-2709): router, routing (as oracle_route), experts (utils.cpp:735-747),
 // then — IR deepseek2 graph (graph_ir.cpp:919-928) — f = (f * scale) + 0 when scale != 1 and, with a
 // shared expert of width d_ff_sh, f = f + sf, sf = down_sh · ((g * (1/(1+expf(-g)))) * u) with g, u, sf
-// the FP64-dot rows of matmul_f32_f32_batch_cpu (utils.cpp:867-909) and silu_cpu (utils.cpp:838-844).
+// the FP64-dot rows of matmul_f32_f32_batch_cpu (utils.cpp:867-909) and silu_cpu (utils.cpp:838-844);
+// with Wsg (qwen2moe's ffn_gate_inp_shexp, graph_ir.cpp:694-705) sf is first scaled by sigmoid(Wsg · x).
 // nthreads <= 0 leaves OpenMP's default.
-void oracle_moe_layer(const float* x, int T, int d, int d_ff, int E, int k, int renorm, int sigmoid,
-                      const float* bias, int groups_n, int groups_top, float scale, const float* router,
-                      const float* G, const float* U, const float* D, int d_ff_sh, const float* Gs,
-                      const float* Us, const float* Ds, float* out, int nthreads) {
+void oracle_moe_layer_gated(const float* x, int T, int d, int d_ff, int E, int k, int renorm, int sigmoid,
+                            const float* bias, int groups_n, int groups_top, float scale, const float* router,
+                            const float* G, const float* U, const float* D, int d_ff_sh, const float* Gs,
+                            const float* Us, const float* Ds, const float* Wsg, float* sgate_out, float* out,
+                            int nthreads) {
 #pragma omp parallel for schedule(static) num_threads(nthreads > 0 ? nthreads : omp_get_max_threads())
   for (int t = 0; t < T; ++t) {
     const float* xt = x + (size_t)t * d;
@@ -349,9 +351,30 @@ void oracle_moe_layer(const float* x, int T, int d, int d_ff, int E, int k, int 
         const float sg = g * (1.0f / (1.0f + std::exp(-g)));
         hs[i] = sg * u;
       }
-      for (int o = 0; o < d; ++o) ot[o] = ot[o] + (float)dot64(Ds + (size_t)o * d_ff_sh, hs.data(), d_ff_sh);
+      // qwen2moe (graph_ir.cpp:704-705): sgate = linear(h2, ffn_gate_inp_shexp), a one-row FP64 dot
+      // (utils.cpp:867-909); sigmoid 1 / (1 + expf(-s)) (graph_ir_ops.cpp:22); sf * sgate per token
+      // (mul_col, graph_ir_ops.cpp:61); then f + sf
+      float c = 1.0f;
+      if (Wsg) {
+        const float s = (float)dot64(Wsg, xt, d);
+        if (sgate_out) sgate_out[t] = s;
+        c = 1.0f / (1.0f + std::exp(-s));
+      }
+      for (int o = 0; o < d; ++o) {
+        float sf = (float)dot64(Ds + (size_t)o * d_ff_sh, hs.data(), d_ff_sh);
+        if (Wsg) sf = sf * c;
+        ot[o] = ot[o] + sf;
+      }
     }
   }
+}
+
+void oracle_moe_layer(const float* x, int T, int d, int d_ff, int E, int k, int renorm, int sigmoid,
+                      const float* bias, int groups_n, int groups_top, float scale, const float* router,
+                      const float* G, const float* U, const float* D, int d_ff_sh, const float* Gs,
+                      const float* Us, const float* Ds, float* out, int nthreads) {
+  oracle_moe_layer_gated(x, T, d, d_ff, E, k, renorm, sigmoid, bias, groups_n, groups_top, scale, router, G, U, D,
+                         d_ff_sh, Gs, Us, Ds, nullptr, nullptr, out, nthreads);
 }
 
 }  // extern "C"

@@ -46,6 +46,8 @@ def ora() -> ctypes.CDLL:
         L.oracle_route.restype = i
         L.oracle_dispatch.argtypes = [vp, i, i, i, vp, vp]
         L.oracle_moe_layer.argtypes = [vp, i, i, i, i, i, i, i, vp, i, i, f, vp, vp, vp, vp, i, vp, vp, vp, vp, i]
+        L.oracle_moe_layer_gated.argtypes = [vp, i, i, i, i, i, i, i, vp, i, i, f, vp, vp, vp, vp, i, vp, vp, vp, vp,
+                                             vp, vp, i]
         _ora = L
     return _ora
 
@@ -68,9 +70,12 @@ def ref() -> ctypes.CDLL:
         L.ref_dequant_q8_0.argtypes = [vp, i64, vp]
         L.ref_dequant_q4_k.argtypes = [vp, i64, vp]
         L.ref_moe_ffn_f32.argtypes = [vp, i, i, i, i, i, vp, vp, vp, vp, vp, i]
+        L.ref_moe_ffn_f32_omp.argtypes = [vp, i, i, i, i, i, vp, vp, vp, vp, vp, i, i]
         L.ref_moe_ffn_routed_f32.argtypes = [vp, i, i, i, i, i, vp, vp, vp, vp, vp, i, i, vp, i, i]
         L.ref_matmul_f32_batch.argtypes = [vp, vp, vp, i, i, i]
         L.ref_silu.argtypes = [vp, vp, i64]
+        L.ref_sigmoid.argtypes = [vp, vp, i64]
+        L.ref_mul_col.argtypes = [vp, vp, vp, i, i]
         _ref = L
     return _ref
 
@@ -124,15 +129,17 @@ def dispatch(idx: np.ndarray, E: int):
 
 
 def moe_layer(x, router, G, U, D, d_ff, E, k, renorm=True, sigmoid=False, bias=None, groups_n=1, groups_top=1,
-              scale=1.0, d_ff_sh=0, Gs=None, Us=None, Ds=None, nthreads=0) -> np.ndarray:
+              scale=1.0, d_ff_sh=0, Gs=None, Us=None, Ds=None, Wsg=None, sgate_out=None, nthreads=0) -> np.ndarray:
     """The whole layer on F32 stacks (moe_ffn_f32_cpu / moe_ffn_routed_f32_cpu + the IR's scale and
-    shared expert), token-parallel over `nthreads` OpenMP threads (0: OpenMP's default)."""
+    shared expert; Wsg [d]: qwen2moe's shared-expert gate ffn_gate_inp_shexp), token-parallel over
+    `nthreads` OpenMP threads (0: OpenMP's default). sgate_out [T], if given, receives the gate logits."""
     arrs = [np.ascontiguousarray(a, np.float32) if a is not None else None
-            for a in (x, router, G, U, D, bias, Gs, Us, Ds)]
-    x, router, G, U, D, bias, Gs, Us, Ds = arrs
+            for a in (x, router, G, U, D, bias, Gs, Us, Ds, Wsg)]
+    x, router, G, U, D, bias, Gs, Us, Ds, Wsg = arrs
     T, d = x.shape
     out = np.empty((T, d), np.float32)
-    ora().oracle_moe_layer(x.ctypes.data, T, d, d_ff, E, k, int(renorm), int(sigmoid), _vp(bias), groups_n, groups_top,
-                           float(scale), router.ctypes.data, G.ctypes.data, U.ctypes.data, D.ctypes.data, d_ff_sh,
-                           _vp(Gs), _vp(Us), _vp(Ds), out.ctypes.data, nthreads)
+    ora().oracle_moe_layer_gated(x.ctypes.data, T, d, d_ff, E, k, int(renorm), int(sigmoid), _vp(bias), groups_n,
+                                 groups_top, float(scale), router.ctypes.data, G.ctypes.data, U.ctypes.data,
+                                 D.ctypes.data, d_ff_sh, _vp(Gs), _vp(Us), _vp(Ds), _vp(Wsg), _vp(sgate_out),
+                                 out.ctypes.data, nthreads)
     return out

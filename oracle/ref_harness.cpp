@@ -1,10 +1,13 @@
 // ORACLE — TEST INFRASTRUCTURE ONLY. A C-ABI harness around the reference's own CPU MoE sources
-// (utils.cpp, quantization.cpp, logger.cpp under /root/reference, compiled in place by oracle/Makefile
+// (utils.cpp, quantization.cpp, logger.cpp, graph_ir_ops.cpp under /root/reference, compiled in place by oracle/Makefile
 // into oracle/_ref/libref_moe.so). It is used to pin oracle/moe_oracle.cpp and to write golden vectors;
 // nothing from the reference is copied into this repository.
+#include <omp.h>
+
 #include <cstdint>
 #include <vector>
 #include "cpu_dot.h"
+#include "graph_ir_ops.h"
 #include "quantization.h"
 #include "utils.h"
 
@@ -34,6 +37,15 @@ void ref_moe_ffn_f32(const float* x, int T, int d, int d_ff, int E, int k, const
     moe_ffn_f32_cpu(x + (size_t)t * d, d, d_ff, E, k, R, G, U, D, out + (size_t)t * d, renorm != 0);
 }
 
+// The reference's prefill driver over the same function: an OpenMP static schedule over tokens
+// (cpu_batch_processor.cpp:223-231), on nthreads threads (<= 0: OpenMP's default).
+void ref_moe_ffn_f32_omp(const float* x, int T, int d, int d_ff, int E, int k, const float* R, const float* G,
+                         const float* U, const float* D, float* out, int renorm, int nthreads) {
+#pragma omp parallel for schedule(static) num_threads(nthreads > 0 ? nthreads : omp_get_max_threads())
+  for (int t = 0; t < T; ++t)
+    moe_ffn_f32_cpu(x + (size_t)t * d, d, d_ff, E, k, R, G, U, D, out + (size_t)t * d, renorm != 0);
+}
+
 // utils.cpp:758 moe_ffn_routed_f32_cpu, token by token.
 void ref_moe_ffn_routed_f32(const float* x, int T, int d, int d_ff, int E, int k, const float* R, const float* G,
                             const float* U, const float* D, float* out, int renorm, int sigmoid, const float* bias,
@@ -54,5 +66,10 @@ void ref_silu(const float* x, float* y, int64_t n) {
   silu_cpu(xv, yv);
   for (int64_t i = 0; i < n; ++i) y[i] = yv[i];
 }
+
+// graph_ir_ops.cpp:22 sigmoid and :61 mul_col (the IR ops of qwen2moe's shared-expert gate,
+// graph_ir.cpp:704-705).
+void ref_sigmoid(const float* x, float* y, int64_t n) { ember_ir::cpu::sigmoid(x, y, (size_t)n); }
+void ref_mul_col(const float* x, const float* c, float* y, int T, int w) { ember_ir::cpu::mul_col(x, c, y, T, w); }
 
 }  // extern "C"

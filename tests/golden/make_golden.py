@@ -146,6 +146,45 @@ def shared_cases():
     return cases
 
 
+def gated_shared_cases():
+    """qwen2moe's FFN in the IR (graph_ir.cpp:694-705): f = moe_ffn(h2) with raw gates; sf = linear(down_sh,
+    silu(linear(gate_sh, h2)) * linear(up_sh, h2)); sgate = sigmoid(linear(ffn_gate_inp_shexp, h2));
+    sf = mul_col(sf, sgate); f = f + sf — composed from the reference's own moe_ffn_f32_cpu,
+    matmul_f32_f32_batch_cpu, silu_cpu, and graph_ir_ops.cpp's sigmoid and mul_col."""
+    rng = np.random.default_rng(17)
+    d, d_ff, E, k, dsh, T = 32, 48, 16, 4, 64, 7
+    G = (rng.standard_normal((E, d_ff, d)) * 0.2).astype(np.float32)
+    U = (rng.standard_normal((E, d_ff, d)) * 0.2).astype(np.float32)
+    D = (rng.standard_normal((E, d, d_ff)) * 0.2).astype(np.float32)
+    R = (rng.standard_normal((E, d)) / np.sqrt(d)).astype(np.float32)
+    Gs = (rng.standard_normal((dsh, d)) * 0.2).astype(np.float32)
+    Us = (rng.standard_normal((dsh, d)) * 0.2).astype(np.float32)
+    Ds = (rng.standard_normal((d, dsh)) * 0.2).astype(np.float32)
+    x = rng.standard_normal((T, d)).astype(np.float32)
+    cases = {}
+    for wscale in (0.3, 3.0):  # sigmoid near its middle, and saturating
+        Wsg = (rng.standard_normal(d) * wscale / np.sqrt(d)).astype(np.float32)
+        f = ref_layer(x, R, G, U, D, d_ff, E, k, 0)
+        sg = np.empty((T, dsh), np.float32); su = np.empty((T, dsh), np.float32); sf = np.empty((T, d), np.float32)
+        O.ref().ref_matmul_f32_batch(Gs.ctypes.data, x.ctypes.data, sg.ctypes.data, T, dsh, d)
+        O.ref().ref_matmul_f32_batch(Us.ctypes.data, x.ctypes.data, su.ctypes.data, T, dsh, d)
+        sgs = np.empty_like(sg)
+        O.ref().ref_silu(sg.ctypes.data, sgs.ctypes.data, sg.size)
+        sgu = (sgs * su).astype(np.float32)
+        O.ref().ref_matmul_f32_batch(Ds.ctypes.data, sgu.ctypes.data, sf.ctypes.data, T, d, dsh)
+        gl = np.empty((T, 1), np.float32)
+        O.ref().ref_matmul_f32_batch(Wsg.ctypes.data, x.ctypes.data, gl.ctypes.data, T, 1, d)
+        gate = np.empty_like(gl)
+        O.ref().ref_sigmoid(gl.ctypes.data, gate.ctypes.data, gl.size)
+        sfg = np.empty_like(sf)
+        O.ref().ref_mul_col(sf.ctypes.data, gate.ctypes.data, sfg.ctypes.data, T, d)
+        y = (f + sfg).astype(np.float32)
+        cases[f"gated_w{wscale}"] = dict(x=x, R=R, G=G, U=U, D=D, Gs=Gs, Us=Us, Ds=Ds, Wsg=Wsg, d_ff=d_ff, E=E, k=k,
+                                         dsh=dsh, sgate_bits=gl.reshape(T).view(np.uint32),
+                                         out_bits=y.view(np.uint32))
+    return cases
+
+
 def dequant_kats():
     """fp16 -> f32 for all 65536 codes; Q8_0 and Q4_K blocks with random payloads (including
     negative, subnormal, Inf/NaN fp16 scales) through the reference's block dequantizers."""
@@ -170,7 +209,7 @@ def dequant_kats():
                 q4_out_bits=q4_out.view(np.uint32))
 
 
-def main():
+def main(only=None):
     if not O.ref_available():
         O.build(ref=True)
     assert O.ref_available(), "oracle/_ref/libref_moe.so could not be built (is /root/reference present?)"
@@ -193,14 +232,16 @@ def main():
         np.savez_compressed(os.path.join(HERE, name), **flat)
         print(name, len(cases), "cases")
 
-    save("c1_layer.npz", c1_cases())
-    save("routing_edges.npz", routing_edge_cases())
-    save("routed_router.npz", routed_cases())
-    save("shared_expert.npz", shared_cases())
-    kats = dequant_kats()
-    np.savez_compressed(os.path.join(HERE, "dequant_kat.npz"), **kats)
-    print("dequant_kat.npz")
+    sets = {"c1_layer.npz": c1_cases, "routing_edges.npz": routing_edge_cases, "routed_router.npz": routed_cases,
+            "shared_expert.npz": shared_cases, "gated_shared.npz": gated_shared_cases}
+    for name, fn in sets.items():
+        if only is None or name in only:
+            save(name, fn())
+    if only is None or "dequant_kat.npz" in only:
+        kats = dequant_kats()
+        np.savez_compressed(os.path.join(HERE, "dequant_kat.npz"), **kats)
+        print("dequant_kat.npz")
 
 
 if __name__ == "__main__":
-    main()
+    main(set(sys.argv[1:]) or None)

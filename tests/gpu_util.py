@@ -32,7 +32,7 @@ def run_oracle(hl: em.HostLayer, x: np.ndarray, nthreads: int = 0):
                   Ds=hl.dequantized("down_sh"))
     return O.moe_layer(x, hl.router, G, U, D, s.d_ff, s.E, s.k, renorm=s.renorm,
                        sigmoid=s.scoring == em.SCORE_SIGMOID, bias=hl.bias, groups_n=s.groups_n,
-                       groups_top=s.groups_top, scale=s.out_scale, nthreads=nthreads, **kw)
+                       groups_top=s.groups_top, scale=s.out_scale, Wsg=hl.shared_gate, nthreads=nthreads, **kw)
 
 
 def same_bits(a, b) -> bool:

@@ -79,12 +79,31 @@ def test_qwen_and_mistral_gates(tmp_path, arch, renorm):
         assert g.moe_layer(0).renorm == renorm
 
 
+def test_qwen2moe_gated_shared_expert(tmp_path):
+    """graph_ir.cpp:700-706: qwen2moe's shared expert counts only when ffn_gate_inp_shexp gates it."""
+    hl = _layer(d_ff_shared=128, shared_gated=True)
+    assert hl.shared_gate is not None
+    t = gw.moe_layer_tensors(hl, 0)
+    p = _write(tmp_path, "q2.gguf", gw.moe_meta("qwen2moe", hl, 1), t)
+    with em.Gguf(p) as g:
+        m = g.moe_layer(0)
+        assert (m.renorm, m.d_ff_shared) == (0, 128)
+        assert m.shared_gate.name.decode() == "blk.0.ffn_gate_inp_shexp.weight"
+        assert np.array_equal(g.tensor_bytes(m.shared_gate).view(np.float32), hl.shared_gate)
+    # the same shared expert without its gate: the reference's graph leaves it out
+    ungated = [x for x in t if "gate_inp_shexp" not in x[0]]
+    p = _write(tmp_path, "q2u.gguf", gw.moe_meta("qwen2moe", hl, 1), ungated)
+    with em.Gguf(p) as g:
+        m = g.moe_layer(0)
+        assert m.d_ff_shared == 0 and not m.shared_gate.name
+
+
 def test_unsupported_layers(tmp_path):
     hl = _layer()
     t = gw.moe_layer_tensors(hl, 0)
-    gated = t + [("blk.0.ffn_gate_inp_shexp.weight", em.F32, (64,), np.zeros(64, np.float32))]
+    gate_only = t + [("blk.0.ffn_gate_inp_shexp.weight", em.F32, (64,), np.zeros(64, np.float32))]
     cases = {
-        "qwen2moe gated shared expert": (gw.moe_meta("qwen2moe", hl, 1), gated),
+        "qwen2moe shared-expert gate without the shared expert": (gw.moe_meta("qwen2moe", hl, 1), gate_only),
         "unknown architecture": (gw.moe_meta("gpt2", hl, 1), t),
         "expert_count disagrees": (gw.moe_meta("llama", hl, 1, {"llama.expert_count": 5}), t),
         "expert_used_count > E": (gw.moe_meta("llama", hl, 1, {"llama.expert_used_count": 9}), t),

@@ -84,3 +84,18 @@ def test_upload_rejects_small_buffer_and_unsupported_type(gpu, tmp_path):
         with pytest.raises(em.EmberError) as e:
             em.gguf_upload_layer(m, dev)
         assert e.value.status == em.ERR_TYPE
+
+
+@pytest.mark.parametrize("T", [1, 12])
+def test_qwen2moe_gated_shared_from_gguf(gpu, tmp_path, T):
+    spec = em.LayerSpec(d=512, d_ff=256, E=16, k=4, wtype=em.Q8_0, renorm=False, d_ff_shared=512, shared_gated=True,
+                        seed=8)
+    hl = em.make_host_layer(spec)
+    p = str(tmp_path / "q2.gguf")
+    gw.write_gguf(p, gw.moe_meta("qwen2moe", hl, 1), gw.moe_layer_tensors(hl, 0))
+    x = em.make_input(spec, T)
+    print(f"gguf qwen2moe gated shared T={T}", flush=True)
+    y, L = _run_from_gguf(p, 0, x)
+    assert (L.renorm, L.d_ff_shared) == (0, 512) and L.shared_gate
+    assert same_bits(y, run_gpu(hl, x))
+    assert rel_l2(y, run_oracle(hl, x)) < 2e-3

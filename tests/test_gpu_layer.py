@@ -142,3 +142,13 @@ def test_shared_expert_multi_token_gemv(gpu, monkeypatch, shape, T, forced):
         spec = em.LayerSpec(d=1024, d_ff=768, E=16, k=4, wtype=em.BF16, d_ff_shared=1536, shared_type=em.Q8_0,
                             seed=23)
     check(spec, T, seed=300 + T)
+
+
+@pytest.mark.parametrize("wtype,T", [(em.BF16, 1), (em.BF16, 3), (em.BF16, 40), (em.BF16, 300), (em.Q8_0, 1),
+                                     (em.Q8_0, 70), (em.F32, 5)])
+def test_qwen2moe_gated_shared_expert(gpu, wtype, T):
+    """qwen2moe (graph_ir.cpp:694-705): raw gates; the shared expert's row scaled by
+    sigmoid(ffn_gate_inp_shexp . x) per token, then added. One token: the shared expert rides in the
+    routed decode launches; many: its own MFMA launches."""
+    check(em.LayerSpec(d=512, d_ff=256, E=16, k=4, wtype=wtype, renorm=False, d_ff_shared=1024, shared_gated=True,
+                       seed=41), T)

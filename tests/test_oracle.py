@@ -80,6 +80,24 @@ def test_golden_shared_expert_bit_exact():
         assert same_bits(y, f32(c["out_bits"])), name
 
 
+def test_golden_gated_shared_expert_bit_exact():
+    """qwen2moe's sigmoid-gated shared expert (graph_ir.cpp:694-705) against the reference's own ops."""
+    cases = load_cases("gated_shared.npz")
+    assert len(cases) == 2
+    for name, c in cases.items():
+        T = c["x"].shape[0]
+        sg = np.empty(T, np.float32)
+        y = O.moe_layer(c["x"], c["R"], c["G"], c["U"], c["D"], int(c["d_ff"]), int(c["E"]), int(c["k"]),
+                        renorm=False, d_ff_sh=int(c["dsh"]), Gs=c["Gs"], Us=c["Us"], Ds=c["Ds"], Wsg=c["Wsg"],
+                        sgate_out=sg)
+        assert same_bits(sg, f32(c["sgate_bits"])), name
+        assert same_bits(y, f32(c["out_bits"])), name
+        # the gate matters: without it the output differs
+        y0 = O.moe_layer(c["x"], c["R"], c["G"], c["U"], c["D"], int(c["d_ff"]), int(c["E"]), int(c["k"]),
+                         renorm=False, d_ff_sh=int(c["dsh"]), Gs=c["Gs"], Us=c["Us"], Ds=c["Ds"])
+        assert not same_bits(y0, y)
+
+
 def test_golden_dequant_kats():
     z = np.load(f"{__import__('golden_util').GOLDEN}/dequant_kat.npz")
     fp16 = np.array([O.ora().oracle_fp16_to_fp32(h) for h in range(65536)], np.float32)
