@@ -56,6 +56,31 @@ def ref_available() -> bool:
     return os.path.exists(os.path.join(HERE, "_ref", "libref_moe.so"))
 
 
+_ref_gguf = None
+
+
+def ref_gguf_available() -> bool:
+    return os.path.exists(os.path.join(HERE, "_ref", "libref_gguf.so"))
+
+
+def ref_gguf_dump(path: str):
+    """The reference's load_gguf_meta on `path` (oracle/_ref/libref_gguf.so): (0, text) on success,
+    (-1, exception message) when the reference rejects the file."""
+    global _ref_gguf
+    if _ref_gguf is None:
+        L = ctypes.CDLL(os.path.join(HERE, "_ref", "libref_gguf.so"))
+        L.ref_gguf_dump.argtypes = [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_size_t]
+        L.ref_gguf_dump.restype = ctypes.c_int
+        _ref_gguf = L
+    cap = 1 << 16
+    while True:
+        buf = ctypes.create_string_buffer(cap)
+        st = _ref_gguf.ref_gguf_dump(os.fsencode(path), buf, cap)
+        if st != -2:
+            return st, buf.value.decode(errors="replace")
+        cap *= 4
+
+
 def ref() -> ctypes.CDLL:
     global _ref
     if _ref is None:
