@@ -313,7 +313,7 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
   static const bool fuse_ok = [] { const char* v = std::getenv("EMBER_FUSE_ROUTE"); return !(v && atoi(v) == 0); }();
   // (the router blocks are one per expert and must fit the device's CUs: fewer CUs than experts take the
   // unfused launches)
-  const bool fuse_route = fuse_ok && l.mode == kGemv && T == 1 && fused_route_fits(d, E, k) && E <= device_cus();
+  const bool fuse_route = fuse_ok && l.mode == kGemv && T == 1 && fused_route_fits(w->gate_type, d, E, k) && E <= device_cus();
   auto* flag = at<unsigned long long>(scratch, l.flag);
   mark(ev, 0, st);
   if (!fuse_route && (s = launch_router_logits(x, T, d, E, w->router, logits, st))) return s;
@@ -326,6 +326,7 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
 
   const bool shared = w->d_ff_shared > 0;
   const bool shared_mfma = shared && l.mode_shared != kGemv;
+  const float out_scale = w->out_scale == 0.0f ? 1.0f : w->out_scale;
   // the shared expert joins the routed decode launches when its type matches (one more segment)
   const bool shared_fused = shared && !shared_mfma && l.mode == kGemv && w->gate_shared_type == w->gate_type &&
                             w->down_shared_type == w->down_type;
@@ -334,6 +335,14 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     if ((s = launch_to_f16(x, (int64_t)T * d, x16, st))) return s;
   float* ys = shared ? at<float>(scratch, l.ys) : nullptr;
   float* hs = at<float>(scratch, l.hs);
+  // one token on the decode path: the down launch also forms the output rows (combine fused in) when the
+  // shared expert, if any, rides in the routed launches
+  static const bool down1_ok = [] { const char* v = std::getenv("EMBER_MOE_DOWN1"); return !(v && atoi(v) == 0); }();
+  const bool down1 = down1_ok && l.mode == kGemv && T == 1 && (!shared || shared_fused) &&
+                     down1_fits(w->down_type, d, d_ff, k, shared_fused ? w->d_ff_shared : 0);
+  // qwen2moe's shared-expert gate logit per token: a one-row router (the same FP64 fixed-order dot)
+  float* sg = w->shared_gate ? at<float>(scratch, l.sg) : nullptr;
+  if (sg && (s = launch_router_logits(x, T, d, 1, w->shared_gate, sg, st))) return s;
 
   if (l.mode != kGemv) {
     const bool skinny = l.mode == kSkinny;
@@ -447,6 +456,39 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     }
     if ((s = launch_projection(a, st))) return s;
     mark(ev, 4, st);
+    if (down1) {
+      // one token: the down projection with the combine fused in (no y rows, no combine launch)
+      Down1Args b{};
+      b.type = w->down_type;
+      b.w = w->down;
+      b.expert_stride = row_bytes(w->down_type, d_ff) * d;
+      b.d = d;
+      b.K = d_ff;
+      b.k = k;
+      b.h = h;
+      b.pos = ds.pos;
+      b.idx = idx;
+      b.gates = gates;
+      if (shared_fused) {
+        b.s_w = w->down_shared;
+        b.s_K = w->d_ff_shared;
+        b.s_h = hs;
+      }
+      b.sg_logit = sg;
+      b.scale = out_scale;
+      b.out = out;
+      b.clear_flag = fuse_route ? flag + 2 : nullptr;
+      b.clear_n = E;
+      if (kev) {
+        b.ev_start = kev[2];
+        b.ev_stop = kev[3];
+      }
+      if ((s = launch_down1(b, st))) return s;
+      mark(ev, 5, st);
+      mark(ev, 6, st);
+      mark(ev, 7, st);
+      return EMBER_OK;
+    }
     a.route = ProjArgs::Route{};
     a.clear_flag = fuse_route ? flag + 2 : nullptr;  // the down launch resets the logit words for the next call
     a.clear_n = E;
@@ -522,12 +564,8 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     b.s_out = ys;
     if ((s = launch_projection(b, st))) return s;
   }
-  // qwen2moe's shared-expert gate logit per token: a one-row router (the same FP64 fixed-order dot)
-  float* sg = w->shared_gate ? at<float>(scratch, l.sg) : nullptr;
-  if (sg && (s = launch_router_logits(x, T, d, 1, w->shared_gate, sg, st))) return s;
   mark(ev, 6, st);
-  s = launch_combine(y, ksplit, (int64_t)T * k * d, gates, ds.pos, ys, sg, w->out_scale == 0.0f ? 1.0f : w->out_scale,
-                     T, k, d, out, st);
+  s = launch_combine(y, ksplit, (int64_t)T * k * d, gates, ds.pos, ys, sg, out_scale, T, k, d, out, st);
   mark(ev, 7, st);
   return s;
 }

@@ -30,6 +30,21 @@
 namespace ember_moe {
 using namespace ember_math;
 
+// Timeline probe for profiling builds (-DEMBER_PROBE): thread 0 of each block stamps the 100 MHz
+// real-time counter into probe[(launch slot * grid + block) * 8 + point]. Compiled out otherwise.
+#ifdef EMBER_PROBE
+__constant__ unsigned long long* g_probe;
+#define EMBER_STAMP(slot, pt)                                                                        \
+  do {                                                                                              \
+    if (g_probe && threadIdx.x == 0)                                                                \
+      g_probe[((size_t)(slot) * 4096 + blockIdx.x) * 8 + (pt)] = __builtin_amdgcn_s_memrealtime(); \
+  } while (0)
+#else
+#define EMBER_STAMP(slot, pt) \
+  do {                        \
+  } while (0)
+#endif
+
 
 constexpr int kProjLdsBytes = 80 * 1024;     // staged activation rows per block (two blocks per CU)
 
@@ -169,11 +184,15 @@ __device__ inline bool seg_view(const ProjArgs& a, const Dispatch& dp, int b, in
 // register buffers ahead of the dots. MT tokens per pass over the weights; their activation rows are
 // staged in LDS (quantized on the way for Q8_0 / Q4_K).
 // The body of proj_kernel for one segment view.
+// prestaged (one-token launches only): the activation row is already in LDS there, staged at the start
+// of the launch, so the pass skips its staging.
 template <int FMT, int MT, bool GATED, int NB, int NT>
-__device__ inline void proj_body(const ProjArgs& a, const Dispatch& dp, const SegView& v) {
+__device__ inline void proj_body(const ProjArgs& a, const Dispatch& dp, const SegView& v,
+                                 const uint8_t* prestaged = nullptr) {
   using F = Fmt<FMT>;
   constexpr int G2 = GATED ? 2 : 1;
-  extern __shared__ __align__(16) uint8_t act_lds[];
+  extern __shared__ __align__(16) uint8_t act_lds_base[];
+  const uint8_t* act_lds = prestaged ? prestaged : act_lds_base;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = NT / 64;
   const int K = v.K;
   const int C = (K + F::CE - 1) / F::CE;
@@ -218,17 +237,20 @@ __device__ inline void proj_body(const ProjArgs& a, const Dispatch& dp, const Se
       load_step(j / G2, j % G2, buf[j]);
     };
     if (nloads > 0) ring_for<NB - 1>(pre);  // wave-uniform: a wave without rows loads nothing
-    __syncthreads();  // the previous pass no longer reads the staged rows
-    if (threadIdx.x < nvalid) {
-      const int p = v.p0 + m0 + threadIdx.x;
-      rows_idx[threadIdx.x] = v.by_perm ? dp.perm[p] / a.k : p;
+    if (!prestaged) {
+      __syncthreads();  // the previous pass no longer reads the staged rows
+      if (threadIdx.x < nvalid) {
+        const int p = v.p0 + m0 + threadIdx.x;
+        rows_idx[threadIdx.x] = v.by_perm ? dp.perm[p] / a.k : p;
+      }
+      __syncthreads();
+      if constexpr (F::QX)
+        stage_rows_quant<F::PLANES>(v.in, K, rows_idx, nvalid, act_lds_base, row_lds);
+      else
+        stage_rows_f32<F::NGL>(v.in, K, rows_idx, nvalid, act_lds_base, row_lds);
+      __syncthreads();
     }
-    __syncthreads();
-    if constexpr (F::QX)
-      stage_rows_quant<F::PLANES>(v.in, K, rows_idx, nvalid, act_lds, row_lds);
-    else
-      stage_rows_f32<F::NGL>(v.in, K, rows_idx, nvalid, act_lds, row_lds);
-    __syncthreads();
+    EMBER_STAMP(GATED ? 0 : 1, 5);
 
     float acc[G2][MT];
 #pragma unroll
@@ -281,6 +303,7 @@ __device__ inline void proj_body(const ProjArgs& a, const Dispatch& dp, const Se
       const int q = q0 + j;
       load_step((q + NB - 1) / G2, (j + NB - 1) % G2, buf[(j + NB - 1) % NB]);
       dot(q, buf[j % NB], acc[j % G2]);
+      if (q == 0) EMBER_STAMP(GATED ? 0 : 1, 6);
       if (j % G2 == G2 - 1) finish(q / G2);
     };
 #pragma unroll 1
@@ -416,7 +439,20 @@ __device__ inline void fused_dispatch(const int* picks, int nv, int E, int32_t* 
 // the waiting block itself with the same code the router block runs, so the picks never depend on the
 // other blocks being resident; each block that does so adds one to the flag area's word 0 (a
 // diagnostic count for the host, never cleared by the library).
+// The give-up path of route_block: it only runs when a router block is not resident.
 template <int NT>
+__device__ inline void fill_missing_logits(const ProjArgs& a, uint8_t* lds, const uint8_t* missing,
+                                                               float* lg) {
+  for (int e = 0; e < a.route.E; ++e)
+    if (missing[e]) {  // block-uniform (LDS)
+      const float v = router_block_logit<NT>(a, e, lds);
+      if (threadIdx.x == 0) lg[e] = v;
+    }
+  if (threadIdx.x == 0) __hip_atomic_fetch_add(a.route.flag, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+}
+
+template <int NT, bool ROUTED>
 __device__ void route_block(const ProjArgs& a, uint8_t* lds, uint8_t* ra, int32_t* s_off, int32_t* s_used,
                             int32_t* s_n, int32_t* s_perm) {
   __shared__ uint8_t missing[kMaxRouteE];
@@ -443,17 +479,11 @@ __device__ void route_block(const ProjArgs& a, uint8_t* lds, uint8_t* ra, int32_
     lg[e] = __builtin_bit_cast(float, (uint32_t)w);
   }
   __syncthreads();
-  if (any_missing) {
-    for (int e = 0; e < E; ++e)
-      if (missing[e]) {  // block-uniform (LDS)
-        const float v = router_block_logit<NT>(a, e, lds);
-        if (t == 0) lg[e] = v;
-      }
-    if (t == 0) __hip_atomic_fetch_add(r.flag, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-  }
+  EMBER_STAMP(0, 2);
+  if (any_missing) fill_missing_logits<NT>(a, lds, missing, lg);
   if (t < 64)
-    route_token(lg, E, k, r.renorm, r.routed, r.sigmoid, r.bias, r.groups_n, r.groups_top, wl, pidx, pgate, true);
+    route_token<ROUTED>(lg, E, k, r.renorm, r.routed, r.sigmoid, r.bias, r.groups_n, r.groups_top, wl, pidx, pgate,
+                        true);
   __syncthreads();
   int nv = 0;  // valid picks: a prefix (route_token puts the -1 entries last)
   for (int j = 0; j < k; ++j) nv += pidx[j] >= 0;
@@ -479,42 +509,65 @@ __device__ void route_block(const ProjArgs& a, uint8_t* lds, uint8_t* ra, int32_
   __syncthreads();
 }
 
-template <int FMT, int MT, bool GATED, int NB, int NT, int WPE, bool ROUTE>
+// ROUTE: 0 none; 1 the fused one-token routing with a softmax router; 2 with the DeepSeek-style options
+template <int FMT, int MT, bool GATED, int NB, int NT, int WPE, int ROUTE>
 __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) proj_kernel(ProjArgs a) {
   if (a.clear_flag && blockIdx.x == 0)
     for (int i = threadIdx.x; i < a.clear_n; i += NT)
       __hip_atomic_store(a.clear_flag + i, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  if constexpr (ROUTE) {
+  if constexpr (ROUTE != 0) {
     extern __shared__ __align__(16) uint8_t act_lds[];
     __shared__ int32_t s_off[kMaxRouteE + 1], s_used[kFusedMaxK], s_perm[kFusedMaxK], s_n;
+    __shared__ int zero_row;
     const int b = blockIdx.x;
     uint8_t* ra = act_lds + fused_router_lds(a.route.d);  // the routing area, after the products
+    // the token's activation row, staged once at the start (it does not depend on the routing), after
+    // the routing area: the expert rows' dots read it there, for the routed and the shared segments
+    uint8_t* xs = ra + fused_route_lds(a.route.E);
+    EMBER_STAMP(0, 0);
+    if (threadIdx.x == 0) zero_row = 0;
     if (threadIdx.x < 64) route_stage_tables(ra + 2048 + 512);
     if (b < a.route.E && !a.route.no_publish) {  // router block: its expert's logit, published tagged
       const float v = router_block_logit<NT>(a, b, act_lds);
+      EMBER_STAMP(0, 1);
       if (threadIdx.x == 0) {
         __hip_atomic_store(a.route.flag + 2 + b, ((unsigned long long)kLogitTag << 32) | __builtin_bit_cast(uint32_t, v),
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
-    route_block<NT>(a, act_lds, ra, s_off, s_used, &s_n, s_perm);
+    __syncthreads();
+    {  // then the activation row (router blocks after their logit, which is on the routing's critical path)
+      using F = Fmt<FMT>;
+      if constexpr (F::QX)
+        stage_rows_quant<F::PLANES>(a.route.x, a.route.d, &zero_row, 1, xs, act_lds_bytes(true, a.route.d));
+      else
+        stage_rows_f32<F::NGL>(a.route.x, a.route.d, &zero_row, 1, xs, act_lds_bytes(false, a.route.d));
+    }
+    route_block<NT, ROUTE == 2>(a, act_lds, ra, s_off, s_used, &s_n, s_perm);
+    EMBER_STAMP(0, 3);
     __syncthreads();  // the routing work area (act_lds) is free for the activations
     Dispatch dp{s_n, s_used, s_off, s_perm};
     SegView v;
-    if (seg_view<GATED, MT>(a, dp, blockIdx.x, gridDim.x, v)) proj_body<FMT, MT, GATED, NB, NT>(a, dp, v);
+    const bool act = seg_view<GATED, MT>(a, dp, blockIdx.x, gridDim.x, v);
+    EMBER_STAMP(0, 4);
+    if (act) proj_body<FMT, MT, GATED, NB, NT>(a, dp, v, xs);
+    EMBER_STAMP(0, 7);
   } else {
     Dispatch dp{a.used ? *a.n_used : 0, a.used, a.offsets, a.perm};
     SegView v;
     const bool active = seg_view<GATED, MT>(a, dp, blockIdx.x, gridDim.x, v);
+    EMBER_STAMP(GATED ? 0 : 1, 0);
     if (active) proj_body<FMT, MT, GATED, NB, NT>(a, dp, v);
+    EMBER_STAMP(GATED ? 0 : 1, 7);
   }
 }
 
-template <int FMT, int MT, bool GATED, int NB, int NT, int WPE, bool ROUTE = false>
+template <int FMT, int MT, bool GATED, int NB, int NT, int WPE, int ROUTE = 0>
 int launch_proj_cfg(const ProjArgs& a_in, size_t act_lds, hipStream_t st) {
   const void* fn = reinterpret_cast<const void*>(&proj_kernel<FMT, MT, GATED, NB, NT, WPE, ROUTE>);
   const ProjArgs& a = a_in;
-  const size_t lds = ROUTE ? std::max(act_lds, fused_router_lds(a.route.d) + fused_route_lds(a.route.E)) : act_lds;
+  const size_t lds =
+      ROUTE ? fused_router_lds(a.route.d) + fused_route_lds(a.route.E) + act_lds_bytes(Fmt<FMT>::QX, a.route.d) : act_lds;
   // blocks per CU at this LDS size (the launch is sized to one resident wave of blocks)
   const int cached_bpc = blocks_per_cu(fn, NT, lds, kProjLdsBytes);
   const int cus = device_cus();
@@ -558,9 +611,12 @@ int launch_proj_fmt(const ProjArgs& a, hipStream_t st) {
   while (MT > 1 && MT * row_lds > kProjLdsBytes) MT >>= 1;
   const size_t lds = (size_t)MT * row_lds;
   if (a.route.flag) {  // routing fused into a one-token gate/up launch
-    if (!GATED || a.T != 1 || !fused_route_fits(a.route.d, a.route.E, a.k))
+    if (!GATED || a.T != 1 || !fused_route_fits(a.type, a.route.d, a.route.E, a.k))
       return EMBER_ERR_SHAPE;
-    if constexpr (GATED) return launch_proj_cfg<FMT, 1, GATED, 2, 512, 4, true>(a, (size_t)row_lds, st);
+    if constexpr (GATED) {
+      if (a.route.routed) return launch_proj_cfg<FMT, 1, GATED, 2, 512, 4, 2>(a, (size_t)row_lds, st);
+      return launch_proj_cfg<FMT, 1, GATED, 2, 512, 4, 1>(a, (size_t)row_lds, st);
+    }
   }
   if (MT == 1) return launch_proj_mt<FMT, 1, GATED>(a, lds, st);
   if (MT == 2) return launch_proj_mt<FMT, 2, GATED>(a, lds, st);
@@ -583,12 +639,273 @@ int launch_projection(const ProjArgs& a, hipStream_t st) {
   return a.gated ? launch_proj_gated<true>(a, st) : launch_proj_gated<false>(a, st);
 }
 
+// 1 / (1 + expf(-s)) in binary32 with glibc's expf (graph_ir_ops.cpp:22 evaluates it on the host)
+__device__ inline float shared_gate_sigmoid(float s) { return 1.0f / (1.0f + expf_glibc(-s)); }
+
+// ---- one-token down projection with the combine fused in
+// At T = 1 the token's picks all produce the same output rows: out[o] = sum over picks j ascending of
+// gate_j * (W_down[e_j][o] . h_j), then * scale, then + the shared expert's row (times its gate). Block
+// b owns a set of output rows ("slots") for every pick, so each row's sum is formed where its dots are,
+// and neither a y buffer nor a combine launch is needed. Each dot is computed exactly as proj_body
+// computes it (same lane partition of the row, same chunk order, same shuffle reduction, same
+// activation quantization) and the sum in combine_kernel's order, so the output bits equal those of
+// the down launch followed by the combine launch.
+//
+// Row ownership follows proj_body's interleave for the routed matrices (the grid's waves read adjacent
+// rows at any time): with RPS rows per wave step, wave w of block b owns rows (b*nw + w)*RPS + i*W*RPS
+// + sub, W = all waves of the grid; slot (i*nw + w)*RPS + sub of the block's row list holds that row.
+// The shared expert's rows (another row length, so another lane partition) are the same rows, walked
+// through the slot list.
+
+// Walks npicks matrices (wbase[j]: rows of K elements, rb bytes apart) over the block's slots; the dot
+// of slot s's row with activation row j (act + j * row_lds) goes to obuf[s]: obuf = obuf + coef[j] * dot,
+// or (shared) obuf = obuf + dot * (*sgc) / obuf + dot.
+// before_loop() runs (on every thread of the block) after the first weight loads are issued and before
+// the first dot: the activation staging goes there, so that the weights travel while it runs.
+template <int FMT, int NB, int NT, class Before>
+__device__ __attribute__((always_inline)) inline void down1_walk(const uint8_t* w0, const int* exps, int64_t estride,
+                                                                 int npicks, int64_t rb, int K, const uint8_t* act,
+                                                                 int row_lds, const int* rowlist, int nslots,
+                                                                 float* obuf, const float* coef, bool shared,
+                                                                 const float* sgc, int rows_total,
+                                                                 Before&& before_loop) {
+  using F = Fmt<FMT>;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = NT / 64;
+  const int C = (K + F::CE - 1) / F::CE;
+  int Lg = 0;
+  while ((1 << Lg) < C && Lg < 6) ++Lg;
+  const int L = 1 << Lg, RPS = 64 >> Lg;
+  const int sub = lane >> Lg, rl = lane & (L - 1);
+  const int NC = (C + L - 1) / L;
+  // slot groups of this wave: for the routed walk (rows_total > 0) the groups holding rows, a prefix
+  // (proj_body's count); for the shared walk every group of the slot list (its holes load row 0 and
+  // store nothing)
+  int ngroups;
+  if (rows_total > 0) {
+    const int gt = (rows_total + RPS - 1) / RPS, wg = blockIdx.x * nwaves + wave, Wall = gridDim.x * nwaves;
+    ngroups = wg < gt ? (gt - wg + Wall - 1) / Wall : 0;
+  } else {
+    const int ngt = (nslots + RPS - 1) / RPS;
+    ngroups = wave < ngt ? (ngt - wave + nwaves - 1) / nwaves : 0;
+  }
+  const int nsteps = ngroups * NC;
+  const int nloads = npicks > 0 ? nsteps * npicks : 0;  // load q: pick q / nsteps, step q % nsteps
+  auto slot_of = [&](int st) { return ((st / NC) * nwaves + wave) * RPS + sub; };
+  // the routed walk's rows follow arithmetically from the slot (no LDS lookup on the load path)
+  const int wg = blockIdx.x * nwaves + wave, Wall = gridDim.x * nwaves;
+  auto row_of = [&](int st) {
+    return rows_total > 0 ? min((wg + (st / NC) * Wall) * RPS + sub, rows_total - 1)
+                          : max(rowlist[min(slot_of(st), nslots - 1)], 0);
+  };
+  auto load_q = [&](int q, uint32_t (&buf)[F::NW]) {
+    const int j = min(q / nsteps, npicks - 1), st = q - (q / nsteps) * nsteps;
+    const int e = __builtin_amdgcn_readfirstlane(exps[j]);  // LDS, a wave-uniform index
+    const int c = min(rl + (st % NC) * L, C - 1);
+    F::load(w0 + (int64_t)e * estride + (int64_t)row_of(st) * rb, c, K, buf);
+  };
+  uint32_t buf[NB][F::NW];
+  if (nloads > 0) ring_for<NB - 1>([&](auto J) { load_q(decltype(J)::value, buf[decltype(J)::value]); });
+  before_loop();
+  if (nloads == 0) return;
+  float acc = 0.0f;
+#pragma unroll 1
+  for (int q0 = 0; q0 < nloads; q0 += NB) {
+    ring_for<NB>([&](auto J) {
+      constexpr int jj = decltype(J)::value;
+      const int q = q0 + jj;
+      load_q(q + NB - 1, buf[(jj + NB - 1) % NB]);
+      const int j = min(q / nsteps, npicks - 1), st = q - (q / nsteps) * nsteps;
+      const int sl = slot_of(st);
+      const int c = rl + (st % NC) * L;
+      const bool ok = q < nloads && c < C && sl < nslots;
+      float tk[1] = {0.0f};
+      F::template dot_tokens<1>(buf[jj % NB], act + (size_t)j * row_lds, row_lds, min(c, C - 1), K, 1, tk);
+      acc += ok ? tk[0] : 0.0f;
+      if (q == 0 && !shared) EMBER_STAMP(1, 6);
+      if (q < nloads && st % NC == NC - 1) {  // the row is complete for pick j
+        float v = acc;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1)
+          if (off < L) v += __shfl_xor(v, off, 64);
+        if (rl == 0 && sl < nslots && rowlist[sl] >= 0) {
+          float& o = obuf[sl];
+          if (shared)
+            o = o + (sgc ? v * *sgc : v);  // the shared expert's row (qwen2moe: times its gate)
+          else
+            o = o + coef[j] * v;  // combine_kernel: acc = acc + gate * y
+        }
+        acc = 0.0f;
+      }
+    });
+  }
+}
+
+template <int FMT, int NB, int NT, int WPE>
+__global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) down1_kernel(Down1Args a) {
+  using F = Fmt<FMT>;
+  constexpr int NW = NT / 64;
+  extern __shared__ __align__(16) uint8_t act_lds[];
+  __shared__ float obuf[kDown1Slots];
+  __shared__ int rowlist[kDown1Slots];
+  __shared__ float gate_s[kDown1MaxPicks], sgc_s;
+  __shared__ int pos_s[kDown1MaxPicks], exp_s[kDown1MaxPicks], np_s, zero_row;
+  if (a.clear_flag && blockIdx.x == 0)
+    for (int i = threadIdx.x; i < a.clear_n; i += NT)
+      __hip_atomic_store(a.clear_flag + i, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const int t = threadIdx.x;
+  EMBER_STAMP(1, 0);
+  if (t < 64) {  // the valid picks in ascending order (the combine's order): one round of loads, compacted
+    int p = -1, e = 0;
+    float g = 0.0f;
+    if (t < a.k) {
+      p = a.pos[t];
+      e = a.idx[t];
+      g = a.gates[t];
+    }
+    const unsigned long long m = __ballot(p >= 0);
+    if (p >= 0) {
+      const int j = __popcll(m & ((1ull << t) - 1));
+      pos_s[j] = p;
+      exp_s[j] = e;
+      gate_s[j] = g;
+    }
+    if (t == 0) {
+      np_s = __popcll(m);
+      sgc_s = a.sg_logit ? shared_gate_sigmoid(*a.sg_logit) : 1.0f;
+      zero_row = 0;
+    }
+  }
+  // the block's rows: proj_body's interleave for the routed row length (see above)
+  {
+    const int C = (a.K + F::CE - 1) / F::CE;
+    int Lg = 0;
+    while ((1 << Lg) < C && Lg < 6) ++Lg;
+    const int RPS = 64 >> Lg;
+    const int Wall = gridDim.x * NW;
+    for (int sl = t; sl < a.nslots; sl += NT) {
+      const int grp = sl / RPS, sub = sl - grp * RPS;
+      const int i = grp / NW, w = grp - i * NW;
+      const int r = ((blockIdx.x * NW + w) + i * Wall) * RPS + sub;
+      rowlist[sl] = r < a.d ? r : -1;
+      obuf[sl] = 0.0f;
+    }
+  }
+  __syncthreads();
+  const int np = np_s;
+  const int row_lds = act_lds_bytes(F::QX, a.K);
+  const int srow_lds = a.s_w ? act_lds_bytes(F::QX, a.s_K) : 0;
+  // the first down rows are requested before every pick's h row (then the shared expert's) is staged
+  auto stage = [&] {
+    if (np > 0) {
+      if constexpr (F::QX)
+        stage_rows_quant<F::PLANES>(a.h, a.K, pos_s, np, act_lds, row_lds);
+      else
+        stage_rows_f32<F::NGL>(a.h, a.K, pos_s, np, act_lds, row_lds);
+    }
+    if (a.s_w) {
+      if constexpr (F::QX)
+        stage_rows_quant<F::PLANES>(a.s_h, a.s_K, &zero_row, 1, act_lds + (size_t)np * row_lds, srow_lds);
+      else
+        stage_rows_f32<F::NGL>(a.s_h, a.s_K, &zero_row, 1, act_lds + (size_t)np * row_lds, srow_lds);
+    }
+    __syncthreads();
+    EMBER_STAMP(1, 5);
+  };
+  down1_walk<FMT, NB, NT>(static_cast<const uint8_t*>(a.w), exp_s, a.expert_stride, np, F::row_bytes(a.K), a.K, act_lds,
+                          row_lds, rowlist, a.nslots, obuf, gate_s, false, nullptr, a.d, stage);
+  __syncthreads();
+  // the rest of combine_kernel's sequence on this block's rows: (acc * scale) + 0, then the shared row
+  if (a.scale != 1.0f)
+    for (int sl = t; sl < a.nslots; sl += NT) obuf[sl] = obuf[sl] * a.scale + 0.0f;
+  if (a.s_w) {
+    __syncthreads();
+    down1_walk<FMT, NB, NT>(static_cast<const uint8_t*>(a.s_w), exp_s, 0, 1, F::row_bytes(a.s_K), a.s_K,
+                            act_lds + (size_t)np * row_lds, srow_lds, rowlist, a.nslots, obuf, nullptr, true,
+                            a.sg_logit ? &sgc_s : nullptr, 0, [] {});
+  }
+  __syncthreads();
+  for (int sl = t; sl < a.nslots; sl += NT)
+    if (rowlist[sl] >= 0) a.out[rowlist[sl]] = obuf[sl];
+  EMBER_STAMP(1, 7);
+}
+
+template <int FMT, int NT>
+int launch_down1_cfg(const Down1Args& a_in, hipStream_t st) {
+  using F = Fmt<FMT>;
+  constexpr int NB = 2, WPE = 4;
+  const void* fn = reinterpret_cast<const void*>(&down1_kernel<FMT, NB, NT, WPE>);
+  const int row_lds = act_lds_bytes(F::QX, a_in.K);
+  const size_t lds = (size_t)a_in.k * row_lds + (a_in.s_w ? act_lds_bytes(F::QX, a_in.s_K) : 0);
+  if (a_in.k > kDown1MaxPicks || lds > (size_t)kProjLdsBytes) return EMBER_ERR_SHAPE;
+  const int bpc = blocks_per_cu(fn, NT, lds, kProjLdsBytes), cus = device_cus();
+  if (bpc <= 0 || cus <= 0) return EMBER_ERR_LAUNCH;
+  const int G = cus * bpc;
+  const int C = (a_in.K + F::CE - 1) / F::CE;
+  int Lg = 0;
+  while ((1 << Lg) < C && Lg < 6) ++Lg;
+  const int RPS = 64 >> Lg, NW = NT / 64;
+  const int gt = (a_in.d + RPS - 1) / RPS, Wall = G * NW;
+  Down1Args a = a_in;
+  a.nslots = (gt + Wall - 1) / Wall * NW * RPS;  // every wave's groups, in slots
+  if (a.nslots > kDown1Slots) return EMBER_ERR_SHAPE;
+  if (a.ev_start)
+    hipExtLaunchKernelGGL(down1_kernel<FMT, NB, NT, WPE>, dim3(G), dim3(NT), lds, st, a.ev_start, a.ev_stop, 0, a);
+  else
+    down1_kernel<FMT, NB, NT, WPE><<<G, NT, lds, st>>>(a);
+  return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
+}
+
+template <int FMT>
+int launch_down1_fmt(const Down1Args& a, hipStream_t st) {
+  static const int nt = [] { const char* v = std::getenv("EMBER_DOWN1_NT"); return v ? atoi(v) : 1024; }();
+  return nt == 1024 ? launch_down1_cfg<FMT, 1024>(a, st) : launch_down1_cfg<FMT, 512>(a, st);
+}
+
+bool down1_fits(int type, int d, int K, int k, int s_K) {
+  if (k > kDown1MaxPicks) return false;
+  const bool qx = type_quantizes_activations(type);
+  const size_t lds = (size_t)k * act_lds_bytes(qx, K) + (s_K > 0 ? act_lds_bytes(qx, s_K) : 0);
+  if (lds > (size_t)kProjLdsBytes) return false;
+  const int CE = type == EMBER_TYPE_F32 ? 16 : type == EMBER_TYPE_F16 || type == EMBER_TYPE_BF16 ? 32 : 64;
+  const int C = (K + CE - 1) / CE;
+  int Lg = 0;
+  while ((1 << Lg) < C && Lg < 6) ++Lg;
+  const int RPS = 64 >> Lg;
+  // at least one block per CU of eight waves: the slot bound for the smallest grid
+  const int cus = device_cus();
+  if (cus <= 0) return false;
+  const int Wall = cus * 8, gt = (d + RPS - 1) / RPS;
+  return (gt + Wall - 1) / Wall * 8 * RPS <= kDown1Slots;
+}
+
+int launch_down1(const Down1Args& a, hipStream_t st) {
+  switch (a.type) {
+    case EMBER_TYPE_F32: return launch_down1_fmt<EMBER_TYPE_F32>(a, st);
+    case EMBER_TYPE_F16: return launch_down1_fmt<EMBER_TYPE_F16>(a, st);
+    case EMBER_TYPE_BF16: return launch_down1_fmt<EMBER_TYPE_BF16>(a, st);
+    case EMBER_TYPE_Q8_0: return launch_down1_fmt<EMBER_TYPE_Q8_0>(a, st);
+    case EMBER_TYPE_Q4_K: return launch_down1_fmt<EMBER_TYPE_Q4_K>(a, st);
+    default: return EMBER_ERR_TYPE;
+  }
+}
+
 int proj_max_row_bytes() { return kProjLdsBytes; }
+
+#ifdef EMBER_PROBE
+}  // namespace ember_moe
+extern "C" int ember_moe_probe_set(void* buf) {
+  unsigned long long* p = static_cast<unsigned long long*>(buf);
+  return hipMemcpyToSymbol(HIP_SYMBOL(ember_moe::g_probe), &p, sizeof(p)) == hipSuccess ? 0 : -1;
+}
+namespace ember_moe {
+#endif
 
 // The router blocks (0..E-1) must be resident together with block 0, which waits for them while they
 // wait for it: at least one block per CU is resident (MI355X: 256 CUs), so E <= 255 (ids fit a byte).
-bool fused_route_fits(int d, int E, int k) {
-  return E <= 255 && k <= kFusedMaxK && d >= 8 && d <= 16 * 512 && fused_router_lds(d) + fused_route_lds(E) <= (size_t)kProjLdsBytes;
+bool fused_route_fits(int type, int d, int E, int k) {
+  return E <= 255 && k <= kFusedMaxK && d >= 8 && d <= 16 * 512 &&
+         fused_router_lds(d) + fused_route_lds(E) + act_lds_bytes(type_quantizes_activations(type), d) <=
+             (size_t)kProjLdsBytes;
 }
 
 bool type_quantizes_activations(int type) { return type == EMBER_TYPE_Q8_0 || type == EMBER_TYPE_Q4_K; }
@@ -599,9 +916,6 @@ bool type_quantizes_activations(int type) { return type == EMBER_TYPE_Q8_0 || ty
 // sigmoid(s) = 1 / (1 + expf(-s)) of the gate logit s (graph_ir.cpp:704-705; graph_ir_ops.cpp:22, 61).
 // A y row given as nparts K-split partial sums is their sum in ascending part order. One thread per
 // output element.
-// 1 / (1 + expf(-s)) in binary32 with glibc's expf (graph_ir_ops.cpp:22 evaluates it on the host)
-__device__ inline float shared_gate_sigmoid(float s) { return 1.0f / (1.0f + expf_glibc(-s)); }
-
 __device__ inline float y_at(const float* __restrict__ y, int nparts, int64_t part_stride, size_t i) {
   float v = y[i];
   for (int s = 1; s < nparts; ++s) v = v + y[s * part_stride + i];

@@ -113,11 +113,38 @@ struct ProjArgs {
   int clear_n;
 };
 // the fused routing's shape limits (the router blocks' and block 0's LDS)
-bool fused_route_fits(int d, int E, int k);
+bool fused_route_fits(int type, int d, int E, int k);
 constexpr unsigned long long kRouteReady = 0x5e11a7ed0ddba11full;
 constexpr int kMaxRouteE = 256;  // experts a fused routing block handles (E <= 255)
 
 int launch_projection(const ProjArgs& a, hipStream_t st);
+
+// One-token down projection with the combine fused in (decode, T = 1): out[o] over the token's picks
+// (pos / idx / gates of its k slots) and the optional shared expert, in combine_kernel's order.
+constexpr int kDown1MaxPicks = 8;
+constexpr int kDown1Slots = 512;  // output rows one block owns, at most
+struct Down1Args {
+  int type;
+  const void* w;           // down stack base [E][d][K]
+  int64_t expert_stride;
+  int d, K, k;
+  const float* h;          // [npos][K] dispatch order
+  const int32_t* pos;      // [k] slot -> dispatch position (-1: none)
+  const int32_t* idx;      // [k]
+  const float* gates;      // [k]
+  const void* s_w;         // shared expert's down [d][s_K], or null
+  int s_K;
+  const float* s_h;        // [s_K]
+  const float* sg_logit;   // qwen2moe shared-expert gate logit, or null
+  float scale;
+  float* out;              // [d]
+  int nslots;              // set by the launcher
+  unsigned long long* clear_flag;
+  int clear_n;
+  hipEvent_t ev_start, ev_stop;
+};
+bool down1_fits(int type, int d, int K, int k, int s_K);
+int launch_down1(const Down1Args& a, hipStream_t st);
 
 // Grouped MFMA GEMM (prefill). Tiles come from `tiles` (pairs expert, first token; *n_tiles valid)
 // over expert segments of the dispatch order, or, when tiles is null, cover T rows of one matrix.

@@ -352,7 +352,10 @@ __device__ inline void route_stage_tables(unsigned char* wl) {
   if (lane < 32) tab128[256 + lane] = ember_math::kExp2Tab32[lane];
 }
 
-// tables_ready: the exp tables are already in wl (route_stage_tables ran earlier on this wave)
+// tables_ready: the exp tables are already in wl (route_stage_tables ran earlier on this wave).
+// ROUTED = false compiles the DeepSeek-style paths out (callers then pass routed = 0): a launch that
+// inlines route_token keeps only the code its router needs.
+template <bool ROUTED = true>
 __device__ __attribute__((always_inline)) inline void route_token(const float* __restrict__ r, int E, int k, int renorm, int routed, int sigmoid,
                             const float* __restrict__ bias, int groups_n, int groups_top, unsigned char* wl,
                             int32_t* __restrict__ idx_t, float* __restrict__ gate_t, bool tables_ready = false) {
@@ -388,14 +391,16 @@ __device__ __attribute__((always_inline)) inline void route_token(const float* _
   }
   has_nan = __any(has_nan);
   wave_sync_lds();
-  if (routed && !has_nan && groups_n <= 64 &&
-      route_routed_wave(row, E, k, renorm, sigmoid, bias, groups_n, groups_top, s, cbuf, cand, picks, idx_t, gate_t,
-                        tab32))
-    return;
+  if constexpr (ROUTED) {
+    if (routed && !has_nan && groups_n <= 64 &&
+        route_routed_wave(row, E, k, renorm, sigmoid, bias, groups_n, groups_top, s, cbuf, cand, picks, idx_t, gate_t,
+                          tab32))
+      return;
+  }
   if (routed || has_nan) {
     wave_sync_lds();
     if (lane == 0) {
-      if (routed)
+      if (ROUTED && routed)
         route_routed_serial(row, E, k, renorm, sigmoid, bias, groups_n, groups_top, s, cbuf, cand, taken, picks, idx_t,
                             gate_t);
       else
