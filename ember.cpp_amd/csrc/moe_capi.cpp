@@ -283,7 +283,7 @@ inline void mark(hipEvent_t* ev, int i, hipStream_t st) {
 }
 
 int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* scratch, size_t scratch_bytes,
-            hipStream_t st, hipEvent_t* ev, hipEvent_t* kev = nullptr, bool* kev_used = nullptr) {
+            hipStream_t st, hipEvent_t* ev, hipEvent_t* kev = nullptr, int* kev_used = nullptr) {
   int s = validate(w);
   if (s) return s;
   if (T < 0) return EMBER_ERR_SHAPE;
@@ -335,11 +335,13 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     if ((s = launch_to_f16(x, (int64_t)T * d, x16, st))) return s;
   float* ys = shared ? at<float>(scratch, l.ys) : nullptr;
   float* hs = at<float>(scratch, l.hs);
-  // one token on the decode path: the down launch also forms the output rows (combine fused in) when the
-  // shared expert, if any, rides in the routed launches
+  // one token on the decode path: the down launch also forms the output rows (combine fused in)
   static const bool down1_ok = [] { const char* v = std::getenv("EMBER_MOE_DOWN1"); return !(v && atoi(v) == 0); }();
-  const bool down1 = down1_ok && l.mode == kGemv && T == 1 && (!shared || shared_fused) &&
-                     down1_fits(w->down_type, d, d_ff, k, shared_fused ? w->d_ff_shared : 0);
+  // (measured on MI355X: C1-shaped layer 22.6 -> 20.4 us, Mixtral-shaped even; with many picks or a
+  // shared expert its row partition leaves blocks idle: Qwen-shaped top-8 32 -> 40 us, DeepSeek-shaped
+  // top-6 + shared 50 -> 54 us, so those keep the down launch + combine)
+  const bool down1 = down1_ok && l.mode == kGemv && T == 1 && k <= 2 && !shared &&
+                     down1_fits(w->down_type, d, d_ff, k, 0);
   // qwen2moe's shared-expert gate logit per token: a one-row router (the same FP64 fixed-order dot)
   float* sg = w->shared_gate ? at<float>(scratch, l.sg) : nullptr;
   if (sg && (s = launch_router_logits(x, T, d, 1, w->shared_gate, sg, st))) return s;
@@ -423,7 +425,7 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     if (kev) {  // per-dispatch timing events of the two expert launches (ember_moe_ffn_timed)
       a.ev_start = kev[0];
       a.ev_stop = kev[1];
-      *kev_used = true;
+      *kev_used = 3;
     }
     if (fuse_route) {
       ProjArgs::Route& r = a.route;
@@ -454,8 +456,6 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
       r.no_publish = test_nopub ? 1 : 0;
       r.spin_limit = test_nopub ? 4u : 4096u;
     }
-    if ((s = launch_projection(a, st))) return s;
-    mark(ev, 4, st);
     if (down1) {
       // one token: the down projection with the combine fused in (no y rows, no combine launch)
       Down1Args b{};
@@ -479,9 +479,12 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
       b.out = out;
       b.clear_flag = fuse_route ? flag + 2 : nullptr;
       b.clear_n = E;
+      if ((s = launch_projection(a, st))) return s;
+      mark(ev, 4, st);
       if (kev) {
         b.ev_start = kev[2];
         b.ev_stop = kev[3];
+        *kev_used = 3;
       }
       if ((s = launch_down1(b, st))) return s;
       mark(ev, 5, st);
@@ -489,6 +492,8 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
       mark(ev, 7, st);
       return EMBER_OK;
     }
+    if ((s = launch_projection(a, st))) return s;
+    mark(ev, 4, st);
     a.route = ProjArgs::Route{};
     a.clear_flag = fuse_route ? flag + 2 : nullptr;  // the down launch resets the logit words for the next call
     a.clear_n = E;
@@ -627,15 +632,15 @@ int ember_moe_ffn_timed(const ember_moe_layer* w, const float* x, int T, float* 
   // The dispatch events are recorded only by the decode path's expert launches; then they replace the
   // event-to-event spans of those two phases (unrecorded events are never queried: a failed query
   // would stay behind as HIP's last error).
-  bool kev_used = false;
+  int kev_used = 0;  // bit 0: the gate/up dispatch events were recorded; bit 1: the down dispatch events
   int s = run_ffn(w, x, T, out, scratch, scratch_bytes, st, ev, ev + 8, &kev_used);
   if (s == EMBER_OK && T > 0) {
     if (hipEventSynchronize(ev[7]) != hipSuccess) s = EMBER_ERR_LAUNCH;
     for (int i = 0; i < EMBER_MOE_NPHASES && s == EMBER_OK; ++i)
       if (hipEventElapsedTime(&phase_ms[i], ev[i], ev[i + 1]) != hipSuccess) s = EMBER_ERR_LAUNCH;
-    if (s == EMBER_OK && kev_used &&
-        (hipEventElapsedTime(&phase_ms[3], ev[8], ev[9]) != hipSuccess ||
-         hipEventElapsedTime(&phase_ms[4], ev[10], ev[11]) != hipSuccess))
+    if (s == EMBER_OK && (kev_used & 1) && hipEventElapsedTime(&phase_ms[3], ev[8], ev[9]) != hipSuccess)
+      s = EMBER_ERR_LAUNCH;
+    if (s == EMBER_OK && (kev_used & 2) && hipEventElapsedTime(&phase_ms[4], ev[10], ev[11]) != hipSuccess)
       s = EMBER_ERR_LAUNCH;
   }
   for (int i = 0; i < 12; ++i) hipEventDestroy(ev[i]);

@@ -184,15 +184,15 @@ __device__ inline bool seg_view(const ProjArgs& a, const Dispatch& dp, int b, in
 // register buffers ahead of the dots. MT tokens per pass over the weights; their activation rows are
 // staged in LDS (quantized on the way for Q8_0 / Q4_K).
 // The body of proj_kernel for one segment view.
-// prestaged (one-token launches only): the activation row is already in LDS there, staged at the start
-// of the launch, so the pass skips its staging.
-template <int FMT, int MT, bool GATED, int NB, int NT>
-__device__ inline void proj_body(const ProjArgs& a, const Dispatch& dp, const SegView& v,
-                                 const uint8_t* prestaged = nullptr) {
+// PRESTAGED (one-token launches only): the activation row is already at the start of the dynamic LDS,
+// staged at the start of the launch, so the pass skips its staging.
+// COHERENT_OUT: the outputs are device-coherent stores (no L2 write-back needed before another XCD
+// reads them in the same launch: the one-launch layer's h rows).
+template <int FMT, int MT, bool GATED, int NB, int NT, bool COHERENT_OUT = false, bool PRESTAGED = false>
+__device__ inline void proj_body(const ProjArgs& a, const Dispatch& dp, const SegView& v) {
   using F = Fmt<FMT>;
   constexpr int G2 = GATED ? 2 : 1;
-  extern __shared__ __align__(16) uint8_t act_lds_base[];
-  const uint8_t* act_lds = prestaged ? prestaged : act_lds_base;
+  extern __shared__ __align__(16) uint8_t act_lds[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = NT / 64;
   const int K = v.K;
   const int C = (K + F::CE - 1) / F::CE;
@@ -237,7 +237,7 @@ __device__ inline void proj_body(const ProjArgs& a, const Dispatch& dp, const Se
       load_step(j / G2, j % G2, buf[j]);
     };
     if (nloads > 0) ring_for<NB - 1>(pre);  // wave-uniform: a wave without rows loads nothing
-    if (!prestaged) {
+    if constexpr (!PRESTAGED) {
       __syncthreads();  // the previous pass no longer reads the staged rows
       if (threadIdx.x < nvalid) {
         const int p = v.p0 + m0 + threadIdx.x;
@@ -245,9 +245,9 @@ __device__ inline void proj_body(const ProjArgs& a, const Dispatch& dp, const Se
       }
       __syncthreads();
       if constexpr (F::QX)
-        stage_rows_quant<F::PLANES>(v.in, K, rows_idx, nvalid, act_lds_base, row_lds);
+        stage_rows_quant<F::PLANES>(v.in, K, rows_idx, nvalid, act_lds, row_lds);
       else
-        stage_rows_f32<F::NGL>(v.in, K, rows_idx, nvalid, act_lds_base, row_lds);
+        stage_rows_f32<F::NGL>(v.in, K, rows_idx, nvalid, act_lds, row_lds);
       __syncthreads();
     }
     EMBER_STAMP(GATED ? 0 : 1, 5);
@@ -287,7 +287,14 @@ __device__ inline void proj_body(const ProjArgs& a, const Dispatch& dp, const Se
 #pragma unroll
         for (int m = 0; m < MT; ++m)
           if (m < nvalid)
-            v.out[(size_t)(v.p0 + m0 + m) * v.rows + r] = GATED ? swiglu(acc[0][m], acc[G2 - 1][m]) : acc[0][m];
+          {
+            const float o = GATED ? swiglu(acc[0][m], acc[G2 - 1][m]) : acc[0][m];
+            float* dst = v.out + (size_t)(v.p0 + m0 + m) * v.rows + r;
+            if constexpr (COHERENT_OUT)
+              __hip_atomic_store(dst, o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            else
+              *dst = o;
+          }
       }
 #pragma unroll
       for (int g = 0; g < G2; ++g)
@@ -321,6 +328,10 @@ constexpr uint32_t kLogitTag = 0x10617ed5u;
 // (logits, picks, gates, one routing wave's work area)
 __host__ __device__ inline size_t fused_router_lds(int d) { return (size_t)8 * d + 8 * 8 * 6 + 256; }
 __host__ __device__ inline size_t fused_route_lds(int E) { return 2048 + 512 + route_wave_lds(E); }
+// the staged activation row of a one-token launch (16-byte multiple)
+__host__ __device__ inline size_t fused_x_lds(int type, int d) {
+  return ((size_t)act_lds_bytes(type == EMBER_TYPE_Q8_0 || type == EMBER_TYPE_Q4_K, d) + 15) & ~(size_t)15;
+}
 
 // Router block e (blocks 0..E-1): the logit of expert e as the reference computes it (cpu_dot.h:
 // eight FP64 chains over i = 8q + c, combined ((c0+c1)+(c2+c3))+((c4+c5)+(c6+c7)), plus the tail).
@@ -439,17 +450,32 @@ __device__ inline void fused_dispatch(const int* picks, int nv, int E, int32_t* 
 // the waiting block itself with the same code the router block runs, so the picks never depend on the
 // other blocks being resident; each block that does so adds one to the flag area's word 0 (a
 // diagnostic count for the host, never cleared by the library).
-// The give-up path of route_block: it only runs when a router block is not resident.
+// The give-up path's logit: the same arithmetic as router_block_logit (every product exact in f64,
+// eight chains in order, the same combination), written for few registers rather than speed (it only
+// runs when a router block is not resident), so that it costs the launch no registers.
 template <int NT>
-__device__ inline void fill_missing_logits(const ProjArgs& a, uint8_t* lds, const uint8_t* missing,
-                                                               float* lg) {
-  for (int e = 0; e < a.route.E; ++e)
-    if (missing[e]) {  // block-uniform (LDS)
-      const float v = router_block_logit<NT>(a, e, lds);
-      if (threadIdx.x == 0) lg[e] = v;
-    }
-  if (threadIdx.x == 0) __hip_atomic_fetch_add(a.route.flag, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ float router_logit_slow(const ProjArgs& a, int e, uint8_t* lds) {
+  const ProjArgs::Route& r = a.route;
+  const int t = threadIdx.x, d = r.d, n8 = d - d % 8, nq = n8 / 8;
+  double* pd = reinterpret_cast<double*>(lds);
+  const float* row = r.router + (size_t)e * d;
   __syncthreads();
+  for (int i = t; i < n8; i += NT) pd[(i & 7) * nq + (i >> 3)] = (double)row[i] * (double)r.x[i];
+  __syncthreads();
+  double acc = 0.0;
+  if (t < 8)
+    for (int q = 0; q < nq; ++q) acc = acc + pd[t * nq + q];
+  double c[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) c[j] = __shfl(acc, j, 64);
+  float v = 0.0f;
+  if (t == 0) {
+    double tail = 0.0;
+    for (int i = n8; i < d; ++i) tail = __builtin_fma((double)row[i], (double)r.x[i], tail);
+    v = (float)((((c[0] + c[1]) + (c[2] + c[3])) + ((c[4] + c[5]) + (c[6] + c[7]))) + tail);
+  }
+  __syncthreads();
+  return v;
 }
 
 template <int NT, bool ROUTED>
@@ -480,7 +506,15 @@ __device__ void route_block(const ProjArgs& a, uint8_t* lds, uint8_t* ra, int32_
   }
   __syncthreads();
   EMBER_STAMP(0, 2);
-  if (any_missing) fill_missing_logits<NT>(a, lds, missing, lg);
+  if (any_missing) {  // block-uniform
+    for (int e = 0; e < E; ++e)
+      if (missing[e]) {
+        const float v = router_logit_slow<NT>(a, e, lds);
+        if (t == 0) lg[e] = v;
+      }
+    if (t == 0) __hip_atomic_fetch_add(r.flag, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+  }
   if (t < 64)
     route_token<ROUTED>(lg, E, k, r.renorm, r.routed, r.sigmoid, r.bias, r.groups_n, r.groups_top, wl, pidx, pgate,
                         true);
@@ -520,15 +554,17 @@ __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) 
     __shared__ int32_t s_off[kMaxRouteE + 1], s_used[kFusedMaxK], s_perm[kFusedMaxK], s_n;
     __shared__ int zero_row;
     const int b = blockIdx.x;
-    uint8_t* ra = act_lds + fused_router_lds(a.route.d);  // the routing area, after the products
-    // the token's activation row, staged once at the start (it does not depend on the routing), after
-    // the routing area: the expert rows' dots read it there, for the routed and the shared segments
-    uint8_t* xs = ra + fused_route_lds(a.route.E);
+    // the token's activation row, staged once at the start (it does not depend on the routing) at the
+    // start of the dynamic LDS, where the expert rows' dots read it (routed and shared segments); the
+    // router products and the routing area follow it
+    uint8_t* xs = act_lds;
+    uint8_t* prod = act_lds + fused_x_lds(FMT, a.route.d);
+    uint8_t* ra = prod + fused_router_lds(a.route.d);
     EMBER_STAMP(0, 0);
     if (threadIdx.x == 0) zero_row = 0;
     if (threadIdx.x < 64) route_stage_tables(ra + 2048 + 512);
     if (b < a.route.E && !a.route.no_publish) {  // router block: its expert's logit, published tagged
-      const float v = router_block_logit<NT>(a, b, act_lds);
+      const float v = router_block_logit<NT>(a, b, prod);
       EMBER_STAMP(0, 1);
       if (threadIdx.x == 0) {
         __hip_atomic_store(a.route.flag + 2 + b, ((unsigned long long)kLogitTag << 32) | __builtin_bit_cast(uint32_t, v),
@@ -543,14 +579,14 @@ __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) 
       else
         stage_rows_f32<F::NGL>(a.route.x, a.route.d, &zero_row, 1, xs, act_lds_bytes(false, a.route.d));
     }
-    route_block<NT, ROUTE == 2>(a, act_lds, ra, s_off, s_used, &s_n, s_perm);
+    route_block<NT, ROUTE == 2>(a, prod, ra, s_off, s_used, &s_n, s_perm);
     EMBER_STAMP(0, 3);
-    __syncthreads();  // the routing work area (act_lds) is free for the activations
+    __syncthreads();
     Dispatch dp{s_n, s_used, s_off, s_perm};
     SegView v;
     const bool act = seg_view<GATED, MT>(a, dp, blockIdx.x, gridDim.x, v);
     EMBER_STAMP(0, 4);
-    if (act) proj_body<FMT, MT, GATED, NB, NT>(a, dp, v, xs);
+    if (act) proj_body<FMT, MT, GATED, NB, NT, false, true>(a, dp, v);
     EMBER_STAMP(0, 7);
   } else {
     Dispatch dp{a.used ? *a.n_used : 0, a.used, a.offsets, a.perm};
@@ -567,7 +603,7 @@ int launch_proj_cfg(const ProjArgs& a_in, size_t act_lds, hipStream_t st) {
   const void* fn = reinterpret_cast<const void*>(&proj_kernel<FMT, MT, GATED, NB, NT, WPE, ROUTE>);
   const ProjArgs& a = a_in;
   const size_t lds =
-      ROUTE ? fused_router_lds(a.route.d) + fused_route_lds(a.route.E) + act_lds_bytes(Fmt<FMT>::QX, a.route.d) : act_lds;
+      ROUTE ? fused_x_lds(FMT, a.route.d) + fused_router_lds(a.route.d) + fused_route_lds(a.route.E) : act_lds;
   // blocks per CU at this LDS size (the launch is sized to one resident wave of blocks)
   const int cached_bpc = blocks_per_cu(fn, NT, lds, kProjLdsBytes);
   const int cus = device_cus();
@@ -904,8 +940,7 @@ namespace ember_moe {
 // wait for it: at least one block per CU is resident (MI355X: 256 CUs), so E <= 255 (ids fit a byte).
 bool fused_route_fits(int type, int d, int E, int k) {
   return E <= 255 && k <= kFusedMaxK && d >= 8 && d <= 16 * 512 &&
-         fused_router_lds(d) + fused_route_lds(E) + act_lds_bytes(type_quantizes_activations(type), d) <=
-             (size_t)kProjLdsBytes;
+         fused_x_lds(type, d) + fused_router_lds(d) + fused_route_lds(E) <= (size_t)kProjLdsBytes;
 }
 
 bool type_quantizes_activations(int type) { return type == EMBER_TYPE_Q8_0 || type == EMBER_TYPE_Q4_K; }

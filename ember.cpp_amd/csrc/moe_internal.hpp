@@ -146,6 +146,7 @@ struct Down1Args {
 bool down1_fits(int type, int d, int K, int k, int s_K);
 int launch_down1(const Down1Args& a, hipStream_t st);
 
+
 // Grouped MFMA GEMM (prefill). Tiles come from `tiles` (pairs expert, first token; *n_tiles valid)
 // over expert segments of the dispatch order, or, when tiles is null, cover T rows of one matrix.
 struct GemmArgs {

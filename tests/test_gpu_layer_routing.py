@@ -148,3 +148,4 @@ def test_fused_routing_fallback(gpu, monkeypatch):
     # and the next normal call is unaffected (the stale words were cleared)
     y2, r2 = _run(dl, x)
     assert r2["fallbacks"] == 0 and same_bits(y2, y0)
+
