@@ -53,8 +53,14 @@ int path_mode(int type_in, int K_in, int type_out, int K_out, double avg_m, int 
     return kGemv;
   }
   if (avg_m <= 96.0) return kSkinny;
+  // BF16 stacks run bf16 MFMA with split activations, which only the 64-token-tile kernel implements
+  if (type_in == EMBER_TYPE_BF16 && type_out == EMBER_TYPE_BF16) return kSkinny;
   return kGemm;
 }
+
+// BF16 gate/up and down: the MFMA paths run bf16 MFMA on the weights' own bits with split (hi + lo)
+// bf16 activations (GemmArgs::split_bf16); other stacks run fp16 MFMA on row-scaled fp16 activations.
+bool split_bf16(int type_in, int type_out) { return type_in == EMBER_TYPE_BF16 && type_out == EMBER_TYPE_BF16; }
 
 size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
 
@@ -150,7 +156,7 @@ RouteLayout route_layout(int T, int E, int k, size_t base) {
 struct Layout {
   size_t flag;  // the fused routing's flag words (ProjArgs::Route), at a fixed place: offset 0
   size_t logits, idx, gates, offsets, perm, h, y, hs, ys, sg;
-  size_t x16, h16, hs16, tiles, n_tiles;  // MFMA paths
+  size_t x16, xexp, xb, h16, hexp, hs16, hsexp, tiles, n_tiles;  // MFMA paths
   int mode, mode_shared;                  // PathMode of the routed experts and of the shared expert
   RouteLayout r;
   size_t end;
@@ -186,9 +192,16 @@ Layout layout(const ember_moe_layer* w, int T) {
                        : l.mode == kSkinny ? (size_t)gemm_skinny_max_tiles(T, w->k, w->E)
                                            : 0;
   const bool mfma = l.mode != kGemv, mfma_sh = w->d_ff_shared > 0 && l.mode_shared != kGemv;
-  l.x16 = o; o = align_up(o + (mfma || mfma_sh ? (size_t)T * w->d * 2 : 0));
-  l.h16 = o; o = align_up(o + (mfma ? slots * w->d_ff * 2 : 0));
-  l.hs16 = o; o = align_up(o + (mfma_sh ? (size_t)T * w->d_ff_shared * 2 : 0));
+  const bool sp = split_bf16(w->gate_type, w->down_type);
+  const bool sp_sh = w->d_ff_shared > 0 && split_bf16(w->gate_shared_type, w->down_shared_type);
+  const bool need16 = (mfma && !sp) || (mfma_sh && !sp_sh), needb = (mfma && sp) || (mfma_sh && sp_sh);
+  l.x16 = o; o = align_up(o + (need16 ? (size_t)T * w->d * 2 : 0));
+  l.xexp = o; o = align_up(o + (need16 ? (size_t)T * 4 : 0));
+  l.xb = o; o = align_up(o + (needb ? (size_t)T * w->d * 4 : 0));
+  l.h16 = o; o = align_up(o + (mfma ? slots * w->d_ff * (sp ? 4 : 2) : 0));
+  l.hexp = o; o = align_up(o + (mfma && !sp ? slots * 4 : 0));
+  l.hs16 = o; o = align_up(o + (mfma_sh ? (size_t)T * w->d_ff_shared * (sp_sh ? 4 : 2) : 0));
+  l.hsexp = o; o = align_up(o + (mfma_sh && !sp_sh ? (size_t)T * 4 : 0));
   l.tiles = o; o = align_up(o + tiles * 8);
   l.n_tiles = o; o = align_up(o + 4);
   l.end = o;
@@ -330,9 +343,16 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
   // the shared expert joins the routed decode launches when its type matches (one more segment)
   const bool shared_fused = shared && !shared_mfma && l.mode == kGemv && w->gate_shared_type == w->gate_type &&
                             w->down_shared_type == w->down_type;
+  // the activations of the MFMA paths: row-scaled fp16 (x16, xexp) and / or split bf16 planes (xb)
+  const bool sp = split_bf16(w->gate_type, w->down_type);
+  const bool sp_sh = shared && split_bf16(w->gate_shared_type, w->down_shared_type);
   _Float16* x16 = at<_Float16>(scratch, l.x16);
-  if (l.mode != kGemv || shared_mfma)
-    if ((s = launch_to_f16(x, (int64_t)T * d, x16, st))) return s;
+  int32_t* xexp = at<int32_t>(scratch, l.xexp);
+  uint16_t* xb = at<uint16_t>(scratch, l.xb);
+  if ((l.mode != kGemv && !sp) || (shared_mfma && !sp_sh))
+    if ((s = launch_to_f16_rows(x, T, d, x16, xexp, st))) return s;
+  if ((l.mode != kGemv && sp) || (shared_mfma && sp_sh))
+    if ((s = launch_to_bf16x2(x, (int64_t)T * d, xb, (int64_t)T * d, st))) return s;
   float* ys = shared ? at<float>(scratch, l.ys) : nullptr;
   float* hs = at<float>(scratch, l.hs);
   // one token on the decode path: the down launch also forms the output rows (combine fused in)
@@ -355,8 +375,14 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     int32_t* n_tiles = at<int32_t>(scratch, l.n_tiles);
     if ((s = launch_build_tiles(offsets, E, skinny, tiles, n_tiles, st))) return s;
     _Float16* h16 = at<_Float16>(scratch, l.h16);
+    int32_t* hexp = at<int32_t>(scratch, l.hexp);
     GemmArgs g{};
-    g.A = x16;
+    g.A = sp ? reinterpret_cast<const _Float16*>(xb) : x16;
+    g.a_exp = sp ? nullptr : xexp;
+    g.h_exp = sp ? nullptr : hexp;
+    g.split_bf16 = sp;
+    g.a_plane = (int64_t)T * d;
+    g.h_plane = (int64_t)T * k * d_ff;
     g.perm = perm;
     g.k = k;
     g.T = T;
@@ -380,6 +406,9 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     mark(ev, 4, st);
     g.A = h16;
     g.perm = nullptr;
+    g.a_exp = sp ? nullptr : hexp;
+    g.h_exp = nullptr;
+    g.a_plane = (int64_t)T * k * d_ff;
     g.W0 = w->down;
     g.W1 = nullptr;
     g.type = w->down_type;
@@ -524,8 +553,14 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
   }
   if (shared_mfma) {
     _Float16* hs16 = at<_Float16>(scratch, l.hs16);
+    int32_t* hsexp = at<int32_t>(scratch, l.hsexp);
     GemmArgs g{};
-    g.A = x16;
+    g.A = sp_sh ? reinterpret_cast<const _Float16*>(xb) : x16;
+    g.a_exp = sp_sh ? nullptr : xexp;
+    g.h_exp = sp_sh ? nullptr : hsexp;
+    g.split_bf16 = sp_sh;
+    g.a_plane = (int64_t)T * d;
+    g.h_plane = (int64_t)T * w->d_ff_shared;
     g.T = T;
     g.W0 = w->gate_shared;
     g.W1 = w->up_shared;
@@ -538,6 +573,9 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     const int mt = skinny ? gemm_skinny_max_tiles(T, 1, 0) : gemm_max_tiles(T, 1, 0);
     if ((s = skinny ? launch_gemm_skinny(g, true, mt, st) : launch_gemm(g, true, mt, st))) return s;
     g.A = hs16;
+    g.a_exp = sp_sh ? nullptr : hsexp;
+    g.h_exp = nullptr;
+    g.a_plane = (int64_t)T * w->d_ff_shared;
     g.W0 = w->down_shared;
     g.W1 = nullptr;
     g.type = w->down_shared_type;

@@ -207,6 +207,36 @@ struct Deq<EMBER_TYPE_BF16> : DeqHalf<EMBER_TYPE_BF16> {};
 // The GEMM path carries ~4e-4 relative error from fp16 operands, so SwiGLU uses the hardware exp here.
 __device__ inline float swiglu_g(float g, float u) { return g * __frcp_rn(1.0f + __expf(-g)) * u; }
 
+// ---- epilogue stores shared by the MFMA kernels (GemmArgs::a_exp / h_exp / split_bf16)
+// the range exponent of the A row behind output row p (0: unscaled)
+__device__ inline int row_exp(const GemmArgs& g, int p) {
+  return g.a_exp ? g.a_exp[g.perm ? g.perm[p] / g.k : p] : 0;
+}
+__device__ inline uint16_t bf16_rne(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // NaN stays NaN
+  return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+__device__ inline float bf16_f32(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
+// h[p][n] = SwiGLU of the unscaled gate and up dots, stored in the A format of the down projection
+__device__ inline void store_h(const GemmArgs& g, size_t o, int p, int e, float ga, float ua, bool first_col) {
+  const float hv = swiglu_g(__builtin_ldexpf(ga, e), __builtin_ldexpf(ua, e));
+  if (g.split_bf16) {
+    uint16_t* hb = reinterpret_cast<uint16_t*>(g.out_h);
+    const uint16_t hi = bf16_rne(hv);
+    hb[o] = hi;
+    hb[g.h_plane + o] = bf16_rne(hv - bf16_f32(hi));
+  } else {
+    g.out_h[o] = (_Float16)__builtin_ldexpf(hv, -2 * e);
+    if (first_col && g.h_exp) g.h_exp[p] = 2 * e;
+  }
+}
+__device__ inline float unscale_y(float acc, int e) { return __builtin_ldexpf(acc, e); }
+// the tile's row exponents, looked up once into LDS (rows of the tile: positions p0 .. p0 + rows)
+__device__ inline void load_row_exps(const GemmArgs& g, int p0, int rows, int* s_rexp) {
+  for (int r = threadIdx.x; r < rows; r += blockDim.x) s_rexp[r] = row_exp(g, p0 + r);
+}
+
 // Blocks are laid out XCD-aware: the hardware hands block b to XCD b % 8, and block b works on
 // m-tile (b % 8) + 8 * ((b / 8) / NT) and n-tile (b / 8) % NT, so the blocks resident on one XCD at a
 // time share one m-tile of activations (read into that XCD's L2 once) while consecutive m-tiles of an
@@ -327,6 +357,8 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs g, int NT) 
     }
   };
 
+  __shared__ int s_rexp[GBM];
+  load_row_exps(g, p0, rows, s_rexp);
   fetch(0);
   stage_in(0, 0);
   __syncthreads();
@@ -351,10 +383,11 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs g, int NT) 
           const int m = wm * 64 + 32 * i + 8 * ii + 4 * (lane >> 5) + jj;
           if (m >= rows) continue;
           const size_t o = (size_t)(p0 + m) * N + n;
+          const int ex = s_rexp[m];
           if constexpr (GATED) {
-            g.out_h[o] = (_Float16)swiglu_g(acc[0][i][jn][4 * ii + jj], acc[1][i][jn][4 * ii + jj]);
+            store_h(g, o, p0 + m, ex, acc[0][i][jn][4 * ii + jj], acc[1][i][jn][4 * ii + jj], n == n0);
           } else {
-            g.out_y[o] = acc[0][i][jn][4 * ii + jj];
+            g.out_y[o] = unscale_y(acc[0][i][jn][4 * ii + jj], ex);
           }
         }
     }
@@ -592,6 +625,8 @@ __global__ void __launch_bounds__(kDmaThreads) gemm_dma_q8_kernel(GemmArgs g, in
       }
     }
   };
+  __shared__ int s_rexp[GBM];
+  load_row_exps(g, p0, rows, s_rexp);
   switch (msub) {  // wave-uniform
     case 4: k_loop(std::integral_constant<int, 4>{}); break;
     case 3: k_loop(std::integral_constant<int, 3>{}); break;
@@ -600,6 +635,7 @@ __global__ void __launch_bounds__(kDmaThreads) gemm_dma_q8_kernel(GemmArgs g, in
     default: k_loop(std::integral_constant<int, 0>{}); break;
   }
   wait_vmcnt<0>();  // no DMA may still target LDS when the block exits
+  __syncthreads();  // the row exponents are visible
 
   // ---- epilogue: lane holds column (lane & 31) of each 32x32 subtile, rows 8*ii + 4*(lane>>5) + jj
 #pragma unroll
@@ -615,10 +651,11 @@ __global__ void __launch_bounds__(kDmaThreads) gemm_dma_q8_kernel(GemmArgs g, in
           const int m = wm * 128 + 32 * i + 8 * ii + 4 * (lane >> 5) + jj;
           if (m >= rows) continue;
           const size_t o = (size_t)(p0 + m) * N + n;
+          const int ex = s_rexp[m];
           if constexpr (GATED) {
-            g.out_h[o] = (_Float16)swiglu_g(acc[i][0][4 * ii + jj], acc[i][1][4 * ii + jj]);
+            store_h(g, o, p0 + m, ex, acc[i][0][4 * ii + jj], acc[i][1][4 * ii + jj], n == n0);
           } else {
-            g.out_y[ks * g.part_stride + o] = acc[i][jn][4 * ii + jj];
+            g.out_y[ks * g.part_stride + o] = unscale_y(acc[i][jn][4 * ii + jj], ex);
           }
         }
     }
@@ -777,6 +814,8 @@ __global__ void __launch_bounds__(kD64Threads) gemm_dma64_q8_kernel(GemmArgs g, 
     mfmas(f1);
   };
 
+  __shared__ int s_rexp[kD64BM];
+  load_row_exps(g, p0, rows, s_rexp);
   constexpr int kPerTile = kD64InstA + kD64InstB;
   static_assert(kD64Stages == 5, "the wait below keeps three tiles in flight beyond the current one");
 #pragma unroll
@@ -791,6 +830,7 @@ __global__ void __launch_bounds__(kD64Threads) gemm_dma64_q8_kernel(GemmArgs g, 
     compute(kt);
   }
   wait_vmcnt<0>();
+  __syncthreads();  // the row exponents are visible
 
 #pragma unroll
   for (int i = 0; i < 2; ++i)
@@ -805,10 +845,11 @@ __global__ void __launch_bounds__(kD64Threads) gemm_dma64_q8_kernel(GemmArgs g, 
           const int m = 32 * i + 8 * ii + 4 * (lane >> 5) + jj;
           if (m >= rows) continue;
           const size_t o = (size_t)(p0 + m) * N + n;
+          const int ex = s_rexp[m];
           if constexpr (GATED) {
-            g.out_h[o] = (_Float16)swiglu_g(acc[i][0][4 * ii + jj], acc[i][1][4 * ii + jj]);
+            store_h(g, o, p0 + m, ex, acc[i][0][4 * ii + jj], acc[i][1][4 * ii + jj], n == n0);
           } else {
-            g.out_y[ks * g.part_stride + o] = acc[i][jn][4 * ii + jj];
+            g.out_y[ks * g.part_stride + o] = unscale_y(acc[i][jn][4 * ii + jj], ex);
           }
         }
     }
@@ -822,13 +863,19 @@ __global__ void __launch_bounds__(kD64Threads) gemm_dma64_q8_kernel(GemmArgs g, 
 // operand uses the same K order). Weights never touch LDS; activations are staged in LDS, two stages.
 constexpr int SBM = 64;
 
-template <int FMT, bool GATED>
+// SPLIT (BF16 weights): A holds bf16 hi and lo planes and each product is two bf16 MFMAs, hi * w + lo * w,
+// with the weights' bf16 bits as they are (GemmArgs::split_bf16).
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+template <int FMT, bool GATED, bool SPLIT = false>
 __global__ void __launch_bounds__(256) gemm_skinny_kernel(GemmArgs g, int NT) {
   using D = Deq<FMT>;
+  static_assert(!SPLIT || FMT == EMBER_TYPE_BF16, "the split path is for bf16 weights");
   constexpr int G = GATED ? 2 : 1;
   constexpr int WN = GATED ? 1 : 2;     // 32-row subtiles per matrix per wave
   constexpr int BN = GATED ? 128 : 256; // output columns per block
-  __shared__ __align__(16) _Float16 As[2][SBM][LDK];
+  constexpr int NP = SPLIT ? 2 : 1;     // A planes
+  __shared__ __align__(16) _Float16 As[2][NP][SBM][LDK];
 
   const int mt = blockIdx.x % g.max_mt, nt = blockIdx.x / g.max_mt;
   int e = 0, p0 = 0, rows = 0;
@@ -847,7 +894,8 @@ __global__ void __launch_bounds__(256) gemm_skinny_kernel(GemmArgs g, int NT) {
   const int K = g.K, N = g.N, nk = K / GBK;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int h = lane >> 5, nl = lane & 31;
-  const int ncol0 = nt * BN + wave * (GATED ? 32 : 64);  // first output column of this wave
+  const int n0 = nt * BN;
+  const int ncol0 = n0 + wave * (GATED ? 32 : 64);  // first output column of this wave
 
   // A loads: thread -> token row tid / 4, 16-element quarter (tid & 3) of the K tile
   const int a_r = tid >> 2, a_q = tid & 3;
@@ -868,12 +916,15 @@ __global__ void __launch_bounds__(256) gemm_skinny_kernel(GemmArgs g, int NT) {
                           : nullptr;
     }
 
-  u32x4 a_reg[2];
+  u32x4 a_reg[NP][2];
   uint32_t b_raw[G][WN][D::NWH];
   auto fetch = [&](int kt) {
 #pragma unroll
-    for (int v = 0; v < 2; ++v)
-      a_reg[v] = a_src ? *reinterpret_cast<const u32x4*>(a_src + (size_t)kt * GBK + 8 * v) : u32x4{0, 0, 0, 0};
+    for (int pl = 0; pl < NP; ++pl)
+#pragma unroll
+      for (int v = 0; v < 2; ++v)
+        a_reg[pl][v] = a_src ? *reinterpret_cast<const u32x4*>(a_src + pl * g.a_plane + (size_t)kt * GBK + 8 * v)
+                             : u32x4{0, 0, 0, 0};
 #pragma unroll
     for (int q = 0; q < G; ++q)
 #pragma unroll
@@ -886,6 +937,12 @@ __global__ void __launch_bounds__(256) gemm_skinny_kernel(GemmArgs g, int NT) {
         }
       }
   };
+  auto stage_a = [&](int st) {
+#pragma unroll
+    for (int pl = 0; pl < NP; ++pl)
+#pragma unroll
+      for (int v = 0; v < 2; ++v) *reinterpret_cast<u32x4*>(&As[st][pl][a_r][16 * a_q + 8 * v]) = a_reg[pl][v];
+  };
 
   floatx16 acc[G][2][WN];
 #pragma unroll
@@ -897,40 +954,55 @@ __global__ void __launch_bounds__(256) gemm_skinny_kernel(GemmArgs g, int NT) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[q][i][j][r] = 0.0f;
 
+  __shared__ int s_rexp[SBM];
+  load_row_exps(g, p0, rows, s_rexp);
   fetch(0);
-#pragma unroll
-  for (int v = 0; v < 2; ++v) *reinterpret_cast<u32x4*>(&As[0][a_r][16 * a_q + 8 * v]) = a_reg[v];
+  stage_a(0);
   __syncthreads();
   for (int kt = 0; kt < nk; ++kt) {
     const int st = kt & 1;
     // decode this tile's weights (registers loaded in the previous iteration) before the loads of
-    // the next tile overwrite them
+    // the next tile overwrite them (the split path multiplies the bf16 bits as they are)
     uint32_t bq[G][WN][16];
 #pragma unroll
     for (int q = 0; q < G; ++q)
 #pragma unroll
-      for (int j = 0; j < WN; ++j) D::decode_half(b_raw[q][j], kt, h, bq[q][j]);
+      for (int j = 0; j < WN; ++j) {
+        if constexpr (SPLIT) {
+#pragma unroll
+          for (int w = 0; w < 16; ++w) bq[q][j][w] = b_raw[q][j][w];
+        } else {
+          D::decode_half(b_raw[q][j], kt, h, bq[q][j]);
+        }
+      }
     if (kt + 1 < nk) fetch(kt + 1);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      half8 af[2];
+      u32x4 af[NP][2];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) af[i] = *reinterpret_cast<const half8*>(&As[st][32 * i + nl][32 * h + 8 * s]);
+      for (int pl = 0; pl < NP; ++pl)
+#pragma unroll
+        for (int i = 0; i < 2; ++i) af[pl][i] = *reinterpret_cast<const u32x4*>(&As[st][pl][32 * i + nl][32 * h + 8 * s]);
 #pragma unroll
       for (int q = 0; q < G; ++q)
 #pragma unroll
         for (int j = 0; j < WN; ++j) {
-          const half8 bf = __builtin_bit_cast(half8, u32x4{bq[q][j][4 * s], bq[q][j][4 * s + 1], bq[q][j][4 * s + 2],
-                                                          bq[q][j][4 * s + 3]});
+          const u32x4 bw{bq[q][j][4 * s], bq[q][j][4 * s + 1], bq[q][j][4 * s + 2], bq[q][j][4 * s + 3]};
 #pragma unroll
-          for (int i = 0; i < 2; ++i)
-            acc[q][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf, acc[q][i][j], 0, 0, 0);
+          for (int i = 0; i < 2; ++i) {
+            if constexpr (SPLIT) {
+              acc[q][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, af[0][i]),
+                                                                      __builtin_bit_cast(bf16x8, bw), acc[q][i][j], 0, 0, 0);
+              acc[q][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, af[1][i]),
+                                                                      __builtin_bit_cast(bf16x8, bw), acc[q][i][j], 0, 0, 0);
+            } else {
+              acc[q][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, af[0][i]),
+                                                                     __builtin_bit_cast(half8, bw), acc[q][i][j], 0, 0, 0);
+            }
+          }
         }
     }
-    if (kt + 1 < nk) {
-#pragma unroll
-      for (int v = 0; v < 2; ++v) *reinterpret_cast<u32x4*>(&As[st ^ 1][a_r][16 * a_q + 8 * v]) = a_reg[v];
-    }
+    if (kt + 1 < nk) stage_a(st ^ 1);
     __syncthreads();
   }
 
@@ -947,10 +1019,11 @@ __global__ void __launch_bounds__(256) gemm_skinny_kernel(GemmArgs g, int NT) {
           const int m = 32 * i + 8 * ii + 4 * h + jj;
           if (m >= rows) continue;
           const size_t o = (size_t)(p0 + m) * N + n;
+          const int ex = s_rexp[m];
           if constexpr (GATED) {
-            g.out_h[o] = (_Float16)swiglu_g(acc[0][i][j][4 * ii + jj], acc[1][i][j][4 * ii + jj]);
+            store_h(g, o, p0 + m, ex, acc[0][i][j][4 * ii + jj], acc[1][i][j][4 * ii + jj], n == n0);
           } else {
-            g.out_y[o] = acc[0][i][j][4 * ii + jj];
+            g.out_y[o] = unscale_y(acc[0][i][j][4 * ii + jj], ex);
           }
         }
     }
@@ -996,6 +1069,7 @@ int launch_gemm_fmt(const GemmArgs& g, int max_mtiles, hipStream_t st) {
       gemm_dma_q8_kernel<GATED, false><<<blocks * (unsigned)gk.ksplit, kDmaThreads, kDmaLds, st>>>(gk, NT);
     return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
   }
+  if (g.split_bf16) return EMBER_ERR_TYPE;  // the split path runs in the 64-token-tile kernel only
   gemm_kernel<FMT, GATED><<<blocks, kGemmThreads, kGemmLds, st>>>(g, NT);
   return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
 }
@@ -1037,6 +1111,12 @@ int launch_skinny_fmt(GemmArgs g, int max_mtiles, hipStream_t st) {
       gemm_dma64_q8_kernel<GATED, false><<<blocks, kD64Threads, kD64Lds, st>>>(g, NT);
     return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
   }
+  if constexpr (FMT == EMBER_TYPE_BF16) {
+    if (g.split_bf16) {
+      gemm_skinny_kernel<FMT, GATED, true><<<(unsigned)(max_mtiles * NT), 256, 0, st>>>(g, NT);
+      return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
+    }
+  }
   gemm_skinny_kernel<FMT, GATED><<<(unsigned)(max_mtiles * NT), 256, 0, st>>>(g, NT);
   return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
 }
@@ -1076,22 +1156,46 @@ int gemm_skinny_ksplit(int type, int max_mtiles, int N, int K) {
   return ks;
 }
 
-// x (f32) -> fp16, RNE, elementwise.
-__global__ void __launch_bounds__(256) to_f16_kernel(const float* __restrict__ x, int64_t n, _Float16* __restrict__ y) {
-  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
-  if (i + 3 < n) {
-    const float4 v = *reinterpret_cast<const float4*>(x + i);
-    const half2_t a = {(_Float16)v.x, (_Float16)v.y}, b = {(_Float16)v.z, (_Float16)v.w};
-    *reinterpret_cast<uint2*>(y + i) = make_uint2(u32(a), u32(b));
-  } else {
-    for (int64_t j = i; j < n; ++j) y[j] = (_Float16)x[j];
-  }
+// x [rows][K] -> fp16 rows scaled by 2^-e, e chosen per row so that its largest magnitude m lands in
+// [0.5, 1) (frexp's exponent; 0 for an all-zero or non-finite row). One block per row.
+__global__ void __launch_bounds__(256) to_f16_rows_kernel(const float* __restrict__ x, int K, _Float16* __restrict__ y,
+                                                          int32_t* __restrict__ row_exp) {
+  __shared__ float red[4];
+  const float* xr = x + (size_t)blockIdx.x * K;
+  float m = 0.0f;
+  for (int i = threadIdx.x; i < K; i += 256) m = fmaxf(m, fabsf(xr[i]));
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  int e = 0;
+  if (m > 0.0f && m <= 3.4028235e38f) (void)__builtin_frexpf(m, &e);
+  if (threadIdx.x == 0) row_exp[blockIdx.x] = e;
+  _Float16* yr = y + (size_t)blockIdx.x * K;
+  for (int i = threadIdx.x; i < K; i += 256) yr[i] = (_Float16)__builtin_ldexpf(xr[i], -e);
 }
 
-int launch_to_f16(const float* x, int64_t n, _Float16* y, hipStream_t st) {
+int launch_to_f16_rows(const float* x, int rows, int K, _Float16* y, int32_t* row_exp, hipStream_t st) {
+  if (rows <= 0) return EMBER_OK;
+  to_f16_rows_kernel<<<(unsigned)rows, 256, 0, st>>>(x, K, y, row_exp);
+  return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
+}
+
+// x -> bf16 hi = RNE(x) and lo = RNE(x - hi) planes (x - hi is exact in f32).
+__global__ void __launch_bounds__(256) to_bf16x2_kernel(const float* __restrict__ x, int64_t n, uint16_t* __restrict__ y,
+                                                        int64_t plane) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float v = x[i];
+  const uint16_t hi = bf16_rne(v);
+  y[i] = hi;
+  y[plane + i] = bf16_rne(v - bf16_f32(hi));
+}
+
+int launch_to_bf16x2(const float* x, int64_t n, uint16_t* y, int64_t plane, hipStream_t st) {
   if (n <= 0) return EMBER_OK;
-  const int64_t threads = (n + 3) / 4;
-  to_f16_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, st>>>(x, n, y);
+  to_bf16x2_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(x, n, y, plane);
   return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
 }
 

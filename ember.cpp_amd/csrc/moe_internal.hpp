@@ -168,6 +168,18 @@ struct GemmArgs {
   int ksplit;              // plain projections: K split over this many blocks, partial sums to
   int64_t part_stride;     // out_y + s * part_stride (floats), summed in order by the combine
   const uint8_t* Wp;       // non-null: this projection's tiles in the prefill pack (Q8_0, 256-token tiles)
+  // Activation range (fp16 operands): A row r holds its values times 2^-a_exp[r] (a_exp indexed as the A
+  // rows are: tokens for gate/up, dispatch positions for down; null: unscaled). The gated epilogue
+  // undoes the scale before SwiGLU and writes h times 2^-h_exp[p] with h_exp[p] = 2 a_exp (h grows as
+  // the product of two projections of x); the plain epilogue multiplies by 2^a_exp. Powers of two:
+  // exact.
+  const int32_t* a_exp;
+  int32_t* h_exp;
+  // BF16 weights: bf16 MFMA with A as two bf16 planes, hi = bf16(v) and lo = bf16(v - hi), lo at
+  // A + a_plane elements (the products hi * w + lo * w in fp32); the gated epilogue writes h the same
+  // way (lo at out_h + h_plane). No range scaling: bf16 has f32's exponent range.
+  bool split_bf16;
+  int64_t a_plane, h_plane;
 };
 // Prefill pack (ember_moe_prefill_pack): Q8_0 tiles of 256 weight rows x 64 columns, 68-byte rows,
 // one tile contiguous; the gate/up section [E][ceil(d_ff / 128)][d / 64] (each tile: the 128 gate rows
@@ -196,7 +208,11 @@ int launch_prefill_pack(const void* W0, const void* W1, int64_t expert_stride, i
 bool gemm_supported(int type, int K);
 int gemm_max_tiles(int T, int k, int E);
 int launch_gemm(const GemmArgs& g, bool gated, int max_mtiles, hipStream_t st);
-int launch_to_f16(const float* x, int64_t n, _Float16* y, hipStream_t st);
+// x [rows][K] f32 -> fp16 rows scaled by 2^-e (e per row: the row's largest magnitude lands in
+// [0.5, 1)), e -> row_exp[row] (GemmArgs::a_exp).
+int launch_to_f16_rows(const float* x, int rows, int K, _Float16* y, int32_t* row_exp, hipStream_t st);
+// x (f32, n elements) -> bf16 hi plane y[0..n) and lo plane y[plane..plane+n) (GemmArgs::split_bf16).
+int launch_to_bf16x2(const float* x, int64_t n, uint16_t* y, int64_t plane, hipStream_t st);
 int launch_build_tiles(const int32_t* offsets, int E, bool skinny, int32_t* tiles, int32_t* n_tiles, hipStream_t st);
 // Skinny variant for segments of a few dozen tokens (64-token tiles).
 int launch_gemm_skinny(const GemmArgs& g, bool gated, int max_mtiles, hipStream_t st);
