@@ -264,6 +264,7 @@ def main():
     ap.add_argument("--tokens", type=int, default=None, help="headline token count (default: the config's first)")
     ap.add_argument("--sweep", type=str, default=None, help="comma-separated token counts (default: the config's)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-c5", action="store_true", help="skip the end-to-end config 5 run the default c2 run adds")
     ap.add_argument("--no-pack", action="store_true",
                     help="run prefill on the ggml rows instead of the prefill pack (all-Q8_0 layers)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -359,6 +360,13 @@ def main():
         "layer_hbm_frac": h["layer_hbm_frac"],
         "sweep": [results[T] for T in sweep_T],
     }
+    if args.config == "c2" and not args.no_c5:
+        # BASELINE config 5 (the 32-layer Mixtral-architecture model, Q4_K experts) end to end, in the same
+        # run: its own line's figures, nested here so the default run records them too
+        try:
+            line["c5"] = run_e2e(log_prefix="[bench c5]")
+        except Exception as exc:
+            line["c5"] = {"value": None, "error": str(exc)}
     if not args.no_cpu:
         try:
             line["cpu_baseline"] = cpu_baseline(hl, spec, sweep_T)
@@ -371,37 +379,30 @@ def main():
     print(json.dumps(line), flush=True)
 
 
-def bench_e2e(args, prompt_len=512, n_new=256):
+def run_e2e(prompt_len=512, n_new=256, log_prefix="[bench]"):
     """a random-init Mixtral-8x7B-architecture model (32 layers, Q4_K experts) through
     ember_moe/mixtral.py: seeded uniform-random prompt ids, prefill, then greedy decode steps at batch 1
-    replayed from one captured HIP graph. One JSON line; value = (prompt + generated tokens) / seconds."""
+    replayed from one captured HIP graph. Returns the figures; value = (prompt + generated tokens) / s."""
     import torch
     from ember_moe import mixtral
 
     spec = mixtral.MixtralSpec()
-    model = mixtral.Mixtral(spec, max_ctx=prompt_len + n_new, log=log)
+    model = mixtral.Mixtral(spec, max_ctx=prompt_len + n_new, log=lambda *a: log(log_prefix, *a))
     prompt = torch.from_numpy(np.random.default_rng(0).integers(0, spec.vocab, prompt_len)).cuda()
     model.generate(prompt[:16], 4)  # warm-up: kernels, the decode graph's code paths
     first, toks, t_pre, t_dec = model.generate(prompt, n_new)
     total = t_pre + t_dec
     # the same decode steps without the MoE FFN calls: the difference is the FFN's time per token
     _, _, _, t_dec_nomoe = model.generate(prompt, n_new, skip_moe=True)
-    line = {
+    out = {
         "metric": "end-to-end tokens/s (c5)",
         "value": (prompt_len + n_new) / total,
         "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": 1,
-        "warmup": 1,
-        "ms_per_step": total * 1e3,
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "q4_k experts through ember_moe_ffn; attention, norms, head bf16/fp32 PyTorch",
-        "data": "synthetic (random-init weights, seeded uniform-random prompt ids)",
         "config": {"workload": f"config 5: Mixtral-8x7B architecture, {spec.n_layers} layers, prefill {prompt_len} + "
                                f"{n_new} greedy decode steps, batch 1", "expert_gb": model.expert_bytes / 1e9,
                    "decode": "one HIP graph per step"},
+        "dtype": "q4_k experts through ember_moe_ffn; attention, norms, head bf16/fp32 PyTorch",
+        "data": "synthetic (random-init weights, seeded uniform-random prompt ids)",
         "prefill_tokens_per_s": prompt_len / t_pre,
         "decode_tokens_per_s": n_new / t_dec,
         "prefill_s": t_pre,
@@ -411,6 +412,18 @@ def bench_e2e(args, prompt_len=512, n_new=256):
         "decode_moe_share": (t_dec - t_dec_nomoe) / t_dec,
         "first_tokens": [int(first[0])] + [int(t) for t in toks[:8].cpu()],
     }
+    del model
+    torch.cuda.empty_cache()
+    return out
+
+
+def bench_e2e(args):
+    """bench.py --config c5: the end-to-end run alone, as its own JSON line."""
+    r = run_e2e()
+    line = {"metric": r["metric"], "value": r["value"], "unit": r["unit"], "n_gpus": 1, "steps": 1, "warmup": 1,
+            "ms_per_step": (r["prefill_s"] + r["decode_s"]) * 1e3, "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": r["dtype"], "data": r["data"], "config": r["config"]}
+    line.update({k: v for k, v in r.items() if k not in line and k != "metric"})
     print(json.dumps(line), flush=True)
 
 

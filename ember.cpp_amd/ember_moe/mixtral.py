@@ -97,6 +97,9 @@ class Mixtral:
         self.kcache = torch.zeros(s.n_layers, s.n_kv, max_ctx, s.head_dim, device=device, dtype=torch.bfloat16)
         self.vcache = torch.zeros_like(self.kcache)
         self.scratch = None
+        # optional hook probe(layer, h, f, scratch, layer_descriptor) after every eager MoE FFN call (the
+        # per-layer parity check of the end-to-end test reads the call's inputs, output and routing)
+        self.probe = None
 
     # ---- pieces
     def _rms(self, x):
@@ -128,6 +131,8 @@ class Mixtral:
         st = moe_ffn(self.layers[l], h, T, f, self.scratch)
         if st:
             raise EmberError(st, "ember_moe_ffn")
+        if self.probe is not None:
+            self.probe(l, h, f, self.scratch, self.layers[l])
         return f
 
     def _ensure_scratch(self, T):
