@@ -23,7 +23,7 @@ constexpr int kMaxK = 64;   // picks live in a 64-entry LDS array per wave
 // Expert-product kernels by tokens per expert (M): the int16-dot GEMV while M is at most a few tokens,
 // the skinny MFMA GEMM (64-token tiles) for up to ~100, the 256-token-tile MFMA GEMM beyond.
 enum PathMode { kGemv = 0, kSkinny = 1, kGemm = 2 };
-int path_mode(int type_in, int K_in, int type_out, int K_out, double avg_m, int E) {
+int path_mode(int type_in, int K_in, int type_out, int K_out, double avg_m, int E, bool packed = false) {
   if (!gemm_supported(type_in, K_in) || !gemm_supported(type_out, K_out)) return kGemv;
   // tuning override: gemv | skinny | gemm (read per call, so a test can select each kernel)
   const int forced = [] {
@@ -39,6 +39,8 @@ int path_mode(int type_in, int K_in, int type_out, int K_out, double avg_m, int 
   // vs 387 us with the prefill pack, 447 vs 483 without; T = 256: 498 vs 612)
   const bool q8 = type_in == EMBER_TYPE_Q8_0 && type_out == EMBER_TYPE_Q8_0;
   if (q8) return avg_m <= 1.5 ? kGemv : kGemm;
+  // packed Q4_K (the same DMA tile kernels): its GEMV holds up to 2 tokens per expert
+  if (packed && type_in == EMBER_TYPE_Q4_K && type_out == EMBER_TYPE_Q4_K) return avg_m <= 2.0 ? kGemv : kGemm;
   // BF16 / F16: by the expected tokens per expert HIT, T*k / (E (1 - (1 - 1/E)^(T*k))), since the GEMV's
   // cost follows the token passes over the hit experts and the MFMA tiles' the hit experts' weights; the
   // GEMV wins up to ~1.5 (C4-shaped routed experts: T = 8 183 vs 184 us, T = 12 254 vs 202; Qwen-shaped
@@ -93,9 +95,11 @@ bool is_routed(const ember_moe_layer* w) {
 }
 
 // The prefill pack covers layers whose routed stacks are all Q8_0 with whole 64-column tiles.
+// the prefill pack serves layers whose three routed stacks are all Q8_0 or all Q4_K
 bool packable(const ember_moe_layer* w) {
-  return w->gate_type == EMBER_TYPE_Q8_0 && w->up_type == EMBER_TYPE_Q8_0 && w->down_type == EMBER_TYPE_Q8_0 &&
-         w->d % 64 == 0 && w->d_ff % 64 == 0;
+  const int t = w->gate_type;
+  return (t == EMBER_TYPE_Q8_0 || t == EMBER_TYPE_Q4_K) && w->up_type == t && w->down_type == t && w->d % 64 == 0 &&
+         w->d_ff % 64 == 0;
 }
 
 int validate(const ember_moe_layer* w) {
@@ -178,7 +182,7 @@ Layout layout(const ember_moe_layer* w, int T) {
   l.hs = o; o = align_up(o + (size_t)T * w->d_ff_shared * 4);
   l.ys = o; o = align_up(o + (w->d_ff_shared > 0 ? (size_t)T * w->d * 4 : 0));
   l.sg = o; o = align_up(o + (w->shared_gate ? (size_t)T * 4 : 0));
-  l.mode = path_mode(w->gate_type, w->d, w->down_type, w->d_ff, (double)T * w->k / w->E, w->E);
+  l.mode = path_mode(w->gate_type, w->d, w->down_type, w->d_ff, (double)T * w->k / w->E, w->E, w->prefill_pack != nullptr);
   l.mode_shared = w->d_ff_shared > 0
                       ? path_mode(w->gate_shared_type, w->d, w->down_shared_type, w->d_ff_shared, (double)T, 1)
                       : kGemv;
@@ -397,8 +401,8 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     g.n_tiles = n_tiles;
     g.offsets = offsets;
     g.out_h = h16;
-    // the prefill pack serves the Q8_0 tile kernels (256- and 64-token tiles alike)
-    const PackLayout pl = pack_layout(d, d_ff, E);
+    // the prefill pack serves the DMA tile kernels (256- and 64-token tiles alike)
+    const PackLayout pl = pack_layout(d, d_ff, E, w->gate_type);
     const uint8_t* pack = static_cast<const uint8_t*>(w->prefill_pack);
     g.Wp = pack ? pack + pl.gu : nullptr;
     const int mt = skinny ? gemm_skinny_max_tiles(T, k, E) : gemm_max_tiles(T, k, E);
@@ -419,7 +423,8 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     g.out_h = nullptr;
     g.out_y = y;
     g.Wp = pack ? pack + pl.dn : nullptr;
-    g.ksplit = ksplit = skinny ? gemm_skinny_ksplit(g.type, mt, d, d_ff) : gemm_ksplit(g.type, T, k, E, d, d_ff);
+    g.ksplit = ksplit = skinny ? gemm_skinny_ksplit(g.type, pack != nullptr, mt, d, d_ff)
+                               : gemm_ksplit(g.type, pack != nullptr, T, k, E, d, d_ff);
     g.part_stride = (int64_t)T * k * d;
     if ((s = gemm(g, false, mt))) return s;
     mark(ev, 5, st);
@@ -705,7 +710,7 @@ int ember_moe_scratch_routing(const ember_moe_layer* w, int T, ember_moe_routing
 
 size_t ember_moe_prefill_pack_bytes(const ember_moe_layer* w) {
   if (validate(w) != EMBER_OK || !packable(w)) return 0;
-  return (size_t)pack_layout(w->d, w->d_ff, w->E).end;
+  return (size_t)pack_layout(w->d, w->d_ff, w->E, w->gate_type).end;
 }
 
 int ember_moe_prefill_pack(const ember_moe_layer* w, void* pack, size_t pack_bytes, hipStream_t st) {
@@ -714,12 +719,13 @@ int ember_moe_prefill_pack(const ember_moe_layer* w, void* pack, size_t pack_byt
   if (!packable(w)) return EMBER_ERR_TYPE;
   if (!pack) return EMBER_ERR_NULL;
   if (reinterpret_cast<uintptr_t>(pack) % 256) return EMBER_ERR_ALIGN;
-  const PackLayout pl = pack_layout(w->d, w->d_ff, w->E);
+  const int t = w->gate_type;
+  const PackLayout pl = pack_layout(w->d, w->d_ff, w->E, t);
   if (pack_bytes < (size_t)pl.end) return EMBER_ERR_SCRATCH;
   uint8_t* p = static_cast<uint8_t*>(pack);
-  const int64_t rb_gu = row_bytes(w->gate_type, w->d), rb_dn = row_bytes(w->down_type, w->d_ff);
-  if ((s = launch_prefill_pack(w->gate, w->up, rb_gu * w->d_ff, rb_gu, w->E, w->d_ff, w->d, p + pl.gu, st))) return s;
-  return launch_prefill_pack(w->down, nullptr, rb_dn * w->d, rb_dn, w->E, w->d, w->d_ff, p + pl.dn, st);
+  const int64_t rb_gu = row_bytes(t, w->d), rb_dn = row_bytes(t, w->d_ff);
+  if ((s = launch_prefill_pack(t, w->gate, w->up, rb_gu * w->d_ff, rb_gu, w->E, w->d_ff, w->d, p + pl.gu, st))) return s;
+  return launch_prefill_pack(t, w->down, nullptr, rb_dn * w->d, rb_dn, w->E, w->d, w->d_ff, p + pl.dn, st);
 }
 
 int ember_moe_router_logits(const float* x, int T, int d, int E, const float* router, float* logits, hipStream_t st) {

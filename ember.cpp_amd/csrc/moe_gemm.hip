@@ -412,8 +412,6 @@ constexpr int kDmaB = 256 * kDmaRowB;            // weight bytes per stage (20 K
 constexpr int kDmaStage = kDmaA + kDmaB;
 constexpr size_t kDmaLds = (size_t)kDmaStages * kDmaStage;
 constexpr int kDmaInstA = kDmaA / 1024 / 8;      // 16-byte DMA instructions per wave per tile: activations (4)
-constexpr int kDmaInstB = (kDmaB / 1024 + 7) / 8; // ... weights (3, the last shared)
-constexpr int kDmaInst = kDmaInstA + kDmaInstB;
 
 __device__ inline void lds_dma16(const void* g, uint8_t* lds) {
   __builtin_amdgcn_global_load_lds(g, (lds_void_t*)lds, 16, 0, 0);
@@ -425,14 +423,76 @@ __device__ inline void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// PACKED: the weight tiles come from the prefill pack (GemmArgs::Wp): one tile is 17 KiB contiguous,
-// loaded as 17 whole-kilobyte DMA instructions and laid out in LDS as 68-byte rows (17 dwords: the 32
-// rows a B fragment read touches fall on distinct banks).
-template <bool GATED, bool PACKED>
+// Weight tile formats of the DMA kernels (template parameter WF):
+//   kWfQ8Rows  Q8_0 row slices read from the ggml rows (80 LDS bytes per row, as above);
+//   kWfQ8Pack  prefill-pack Q8_0 tiles: 17 KiB contiguous, loaded as 17 whole-kilobyte DMA instructions
+//              into 68-byte LDS rows (17 dwords: the 32 rows a B fragment read touches fall on distinct
+//              banks);
+//   kWfQ4Pack  prefill-pack Q4_K tiles: 10 KiB, 40-byte rows {a0, m0, a1, m1, 32 nibble bytes} (10 dwords,
+//              again 32 distinct banks).
+enum { kWfQ8Rows = 0, kWfQ8Pack = 1, kWfQ4Pack = 2 };
+template <int WF>
+struct DmaW {
+  static constexpr int kRowB = WF == kWfQ8Rows ? kDmaRowB : WF == kWfQ8Pack ? kPackRowB : kPackRowQ4B;
+  static constexpr int kInst = (WF == kWfQ8Rows ? kDmaB : 256 * kRowB) / 1024;  // 1 KiB instructions per tile
+  static constexpr int64_t kStride = WF == kWfQ8Rows ? 68 : 256 * kRowB;         // global bytes per K tile
+};
+
+// The B fragment of K step KS (compile time) from one weight row's K tile in LDS: the lane's 8 elements
+// of K granule 2 KS + h, as fp16 MFMA operands.
+// Q8_0: K granule gk = 2 ks + h of the 64 = Q8_0 block b = ks / 2, bytes X + 8 h .. + 8 of the row's 68
+// with X = 34 b + 2 + 16 (ks % 2); for b = 1 those are dword aligned and, in row slices past byte 52,
+// read from the overlapping fifth granule (LDS byte = global byte + 12); for b = 0 they sit two bytes
+// past a dword and are funnel-shifted out of three dwords. Value d * q, one rounding.
+// Q4_K pack: group b = ks / 2 (its nibble half of the 32 bytes), elements 16 (ks % 2) + 8 h .. + 8 =
+// nibble bytes of the same offsets; value a * q + m by one fp16 fused multiply-add (the factors as
+// Deq<Q4_K> forms them, so the products are those of the register-staged kernels).
+template <int WF, int KS>
+__device__ inline half8 b_frag(const uint8_t* row, int h) {
+  constexpr int b = KS >> 1;
+  if constexpr (WF == kWfQ4Pack) {
+    const uint32_t hdr = *reinterpret_cast<const uint32_t*>(row + 4 * b);
+    const half2_t a = h2((hdr & 0xffffu) * 0x10001u), m = h2((hdr >> 16) * 0x10001u);
+    const uint32_t* qw = reinterpret_cast<const uint32_t*>(row + 8 + 16 * (KS & 1) + 8 * h);
+    const uint32_t n0 = (qw[0] >> (4 * b)) & 0x0f0f0f0fu, n1 = (qw[1] >> (4 * b)) & 0x0f0f0f0fu;
+    const half2_t off = h2(0xe400e400u);  // -1024 in each half
+    const uint32_t o0 = u32(__builtin_elementwise_fma(magic_pair(n0, 0) + off, a, m));
+    const uint32_t o1 = u32(__builtin_elementwise_fma(magic_pair(n0, 1) + off, a, m));
+    const uint32_t o2 = u32(__builtin_elementwise_fma(magic_pair(n1, 0) + off, a, m));
+    const uint32_t o3 = u32(__builtin_elementwise_fma(magic_pair(n1, 1) + off, a, m));
+    return __builtin_bit_cast(half8, u32x4{o0, o1, o2, o3});
+  } else {
+    constexpr int X = 34 * b + 2 + 16 * (KS & 1);
+    const uint32_t dbits = b ? (*reinterpret_cast<const uint32_t*>(row + 32) >> 16)
+                             : (*reinterpret_cast<const uint32_t*>(row) & 0xffffu);
+    const half2_t d = h2(dbits * 0x10001u);
+    uint32_t w0, w1;
+    if constexpr (b == 0) {
+      const uint32_t* qw = reinterpret_cast<const uint32_t*>(row + (X & ~3) + 8 * h);
+      w0 = __builtin_amdgcn_alignbit(qw[1], qw[0], 16);
+      w1 = __builtin_amdgcn_alignbit(qw[2], qw[1], 16);
+    } else {
+      const int byte = X + 8 * h;
+      const uint32_t* qw =
+          reinterpret_cast<const uint32_t*>(row + (WF == kWfQ8Pack || byte + 8 <= 64 ? byte : byte + 12));
+      w0 = qw[0];
+      w1 = qw[1];
+    }
+    const half2_t off = h2(0xe480e480u);  // -1152 = -(1024 + 128) in each half
+    const uint32_t q0 = w0 ^ 0x80808080u, q1 = w1 ^ 0x80808080u;
+    const uint32_t o0 = u32((magic_pair(q0, 0) + off) * d), o1 = u32((magic_pair(q0, 1) + off) * d);
+    const uint32_t o2 = u32((magic_pair(q1, 0) + off) * d), o3 = u32((magic_pair(q1, 1) + off) * d);
+    return __builtin_bit_cast(half8, u32x4{o0, o1, o2, o3});
+  }
+}
+
+template <bool GATED, int WF>
 __global__ void __launch_bounds__(kDmaThreads) gemm_dma_q8_kernel(GemmArgs g, int NT) {
   constexpr int BN = GATED ? 128 : 256;
-  constexpr int kRowB = PACKED ? kPackRowB : kDmaRowB;             // LDS bytes per weight row
-  constexpr int kLastB = PACKED ? (int)(kPackTileB / 1024) - 1 : kDmaB / 1024 - 1;  // last weight DMA instruction
+  constexpr int kRowB = DmaW<WF>::kRowB;       // LDS bytes per weight row
+  constexpr int kLastB = DmaW<WF>::kInst - 1;  // last weight DMA instruction
+  constexpr int kDmaInstB = (DmaW<WF>::kInst + 7) / 8;  // weight DMA instructions per wave (the last shared)
+  constexpr int kDmaInst = kDmaInstA + kDmaInstB;
   extern __shared__ __align__(16) uint8_t dsm[];
 
   // block -> (m-tile, n-tile, K split part): XCD b % 8 runs m-tile (b % 8) + 8 ((b / 8) / (NT KS)), so
@@ -484,8 +544,8 @@ __global__ void __launch_bounds__(kDmaThreads) gemm_dma_q8_kernel(GemmArgs g, in
 #pragma unroll
   for (int i = 0; i < kDmaInstB; ++i) {
     const int gb = 64 * min(kDmaInstB * wave + i, kLastB) + lane;
-    if constexpr (PACKED) {
-      srcB[i] = g.Wp + ((int64_t)e * NT + nt) * nk_all * kPackTileB + 16 * gb;
+    if constexpr (WF != kWfQ8Rows) {
+      srcB[i] = g.Wp + ((int64_t)e * NT + nt) * nk_all * DmaW<WF>::kStride + 16 * gb;
     } else {
       const int r = gb / 5, part = gb - 5 * r;
       const int q = GATED ? (r >> 7) : 0;
@@ -501,7 +561,7 @@ __global__ void __launch_bounds__(kDmaThreads) gemm_dma_q8_kernel(GemmArgs g, in
     uint8_t* st = dsm + (kt % kDmaStages) * kDmaStage;
     lds_dma16(srcA[j] + (size_t)kc * GBK * 2, st + 1024 * (kDmaInstA * wave + j));
     if (j < kDmaInstB)
-      lds_dma16(srcB[j] + (size_t)kc * (PACKED ? kPackTileB : 68), st + kDmaA + 1024 * min(kDmaInstB * wave + j, kLastB));
+      lds_dma16(srcB[j] + (size_t)kc * DmaW<WF>::kStride, st + kDmaA + 1024 * min(kDmaInstB * wave + j, kLastB));
   };
   auto issue_all = [&](int kt) {
 #pragma unroll
@@ -522,21 +582,15 @@ __global__ void __launch_bounds__(kDmaThreads) gemm_dma_q8_kernel(GemmArgs g, in
     return wn * 64 + 32 * jn + (lane & 31);
   };
   const int h = lane >> 5;
-  const half2_t off = h2(0xe480e480u);  // -1152 = -(1024 + 128) in each half
 
   // Fragments of K step ks (compile time) of the tile in stage `st`, for the first MS (compile time)
-  // 32-row subtiles. Lane's 8 elements: K granule gk = 2 ks + h of the 64 = Q8_0 block b = ks / 2,
-  // bytes X + 8 h .. + 8 of the row's 68 with X = 34 b + 2 + 16 (ks % 2); for b = 1 those are dword
-  // aligned and, past byte 52, read from the overlapping fifth granule (LDS byte = global byte + 12);
-  // for b = 0 they sit two bytes past a dword and are funnel-shifted out of three dwords.
+  // 32-row subtiles
   struct Frags {
     half8 a[4], b[2];
   };
   auto load_frags = [&](const uint8_t* st, auto KS, auto MSc, Frags& f) {
     constexpr int ks = decltype(KS)::value;
     constexpr int MS = decltype(MSc)::value;
-    constexpr int b = ks >> 1;
-    constexpr int X = 34 * b + 2 + 16 * (ks & 1);
     const int gk = 2 * ks + h;
 #pragma unroll
     for (int i = 0; i < MS; ++i) {
@@ -545,28 +599,7 @@ __global__ void __launch_bounds__(kDmaThreads) gemm_dma_q8_kernel(GemmArgs g, in
     }
     const uint8_t* Bs = st + kDmaA;
 #pragma unroll
-    for (int jn = 0; jn < 2; ++jn) {
-      const uint8_t* row = Bs + kRowB * brow_of(jn);
-      const uint32_t dbits = b ? (*reinterpret_cast<const uint32_t*>(row + 32) >> 16)
-                               : (*reinterpret_cast<const uint32_t*>(row) & 0xffffu);
-      const half2_t d = h2(dbits * 0x10001u);
-      uint32_t w0, w1;
-      if constexpr (b == 0) {
-        const uint32_t* qw = reinterpret_cast<const uint32_t*>(row + (X & ~3) + 8 * h);
-        w0 = __builtin_amdgcn_alignbit(qw[1], qw[0], 16);
-        w1 = __builtin_amdgcn_alignbit(qw[2], qw[1], 16);
-      } else {
-        const int byte = X + 8 * h;
-        // row slices: bytes past 64 sit in the overlapping fifth granule, 12 bytes further on
-        const uint32_t* qw = reinterpret_cast<const uint32_t*>(row + (PACKED || byte + 8 <= 64 ? byte : byte + 12));
-        w0 = qw[0];
-        w1 = qw[1];
-      }
-      const uint32_t q0 = w0 ^ 0x80808080u, q1 = w1 ^ 0x80808080u;
-      const uint32_t o0 = u32((magic_pair(q0, 0) + off) * d), o1 = u32((magic_pair(q0, 1) + off) * d);
-      const uint32_t o2 = u32((magic_pair(q1, 0) + off) * d), o3 = u32((magic_pair(q1, 1) + off) * d);
-      f.b[jn] = __builtin_bit_cast(half8, u32x4{o0, o1, o2, o3});
-    }
+    for (int jn = 0; jn < 2; ++jn) f.b[jn] = b_frag<WF, ks>(Bs + kRowB * brow_of(jn), h);
   };
   auto mfmas = [&](const Frags& f, auto MSc) {
 #pragma unroll
@@ -670,14 +703,14 @@ constexpr int kD64A = kD64BM * GBK * 2;            // 8 KiB
 constexpr int kD64Stage = kD64A + kDmaB;          // + 20 KiB of Q8_0 rows
 constexpr size_t kD64Lds = (size_t)kD64Stages * kD64Stage;
 constexpr int kD64InstA = kD64A / 16 / 64 / 4;     // 2 per wave
-constexpr int kD64InstB = kDmaB / 16 / 64 / 4;     // 5 per wave
 
-// PACKED: weight tiles from the prefill pack, as in gemm_dma_q8_kernel.
-template <bool GATED, bool PACKED>
+// WF: the weight tile format, as in gemm_dma_q8_kernel.
+template <bool GATED, int WF>
 __global__ void __launch_bounds__(kD64Threads) gemm_dma64_q8_kernel(GemmArgs g, int NT) {
   constexpr int BN = GATED ? 128 : 256;
-  constexpr int kRowB = PACKED ? kPackRowB : kDmaRowB;
-  constexpr int kLastB = PACKED ? (int)(kPackTileB / 1024) - 1 : kDmaB / 1024 - 1;
+  constexpr int kRowB = DmaW<WF>::kRowB;
+  constexpr int kLastB = DmaW<WF>::kInst - 1;
+  constexpr int kD64InstB = (DmaW<WF>::kInst + 3) / 4;  // weight DMA instructions per wave (5, 5, 3)
   extern __shared__ __align__(16) uint8_t dsm[];
 
   // block -> (m-tile, n-tile, K split part); part ks covers K tiles [kt0, kt0 + nk)
@@ -714,8 +747,8 @@ __global__ void __launch_bounds__(kD64Threads) gemm_dma64_q8_kernel(GemmArgs g, 
 #pragma unroll
   for (int i = 0; i < kD64InstB; ++i) {
     const int gb = 64 * min(kD64InstB * wave + i, kLastB) + lane;
-    if constexpr (PACKED) {
-      srcB[i] = g.Wp + ((int64_t)e * NT + nt) * nk_all * kPackTileB + 16 * gb;
+    if constexpr (WF != kWfQ8Rows) {
+      srcB[i] = g.Wp + ((int64_t)e * NT + nt) * nk_all * DmaW<WF>::kStride + 16 * gb;
     } else {
       const int r = gb / 5, part = gb - 5 * r;
       const int q = GATED ? (r >> 7) : 0;
@@ -736,7 +769,7 @@ __global__ void __launch_bounds__(kD64Threads) gemm_dma64_q8_kernel(GemmArgs g, 
 #pragma unroll
     for (int i = 0; i < kD64InstB; ++i)
       if ((i * 4) / kD64InstB == j)
-        lds_dma16(srcB[i] + (size_t)kc * (PACKED ? kPackTileB : 68), st + kD64A + 1024 * min(kD64InstB * wave + i, kLastB));
+        lds_dma16(srcB[i] + (size_t)kc * DmaW<WF>::kStride, st + kD64A + 1024 * min(kD64InstB * wave + i, kLastB));
   };
 
   floatx16 acc[2][2];
@@ -752,14 +785,11 @@ __global__ void __launch_bounds__(kD64Threads) gemm_dma64_q8_kernel(GemmArgs g, 
     return wn * 64 + 32 * jn + (lane & 31);
   };
   const int h = lane >> 5;
-  const half2_t off = h2(0xe480e480u);
   struct Frags {
     half8 a[2], b[2];
   };
   auto load_frags = [&](const uint8_t* st, auto KS, Frags& f) {
     constexpr int ks = decltype(KS)::value;
-    constexpr int b = ks >> 1;
-    constexpr int X = 34 * b + 2 + 16 * (ks & 1);
     const int gk = 2 * ks + h;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -768,27 +798,7 @@ __global__ void __launch_bounds__(kD64Threads) gemm_dma64_q8_kernel(GemmArgs g, 
     }
     const uint8_t* Bs = st + kD64A;
 #pragma unroll
-    for (int jn = 0; jn < 2; ++jn) {
-      const uint8_t* row = Bs + kRowB * brow_of(jn);
-      const uint32_t dbits = b ? (*reinterpret_cast<const uint32_t*>(row + 32) >> 16)
-                               : (*reinterpret_cast<const uint32_t*>(row) & 0xffffu);
-      const half2_t d = h2(dbits * 0x10001u);
-      uint32_t w0, w1;
-      if constexpr (b == 0) {
-        const uint32_t* qw = reinterpret_cast<const uint32_t*>(row + (X & ~3) + 8 * h);
-        w0 = __builtin_amdgcn_alignbit(qw[1], qw[0], 16);
-        w1 = __builtin_amdgcn_alignbit(qw[2], qw[1], 16);
-      } else {
-        const int byte = X + 8 * h;
-        const uint32_t* qw = reinterpret_cast<const uint32_t*>(row + (PACKED || byte + 8 <= 64 ? byte : byte + 12));
-        w0 = qw[0];
-        w1 = qw[1];
-      }
-      const uint32_t q0 = w0 ^ 0x80808080u, q1 = w1 ^ 0x80808080u;
-      const uint32_t o0 = u32((magic_pair(q0, 0) + off) * d), o1 = u32((magic_pair(q0, 1) + off) * d);
-      const uint32_t o2 = u32((magic_pair(q1, 0) + off) * d), o3 = u32((magic_pair(q1, 1) + off) * d);
-      f.b[jn] = __builtin_bit_cast(half8, u32x4{o0, o1, o2, o3});
-    }
+    for (int jn = 0; jn < 2; ++jn) f.b[jn] = b_frag<WF, ks>(Bs + kRowB * brow_of(jn), h);
   };
   auto mfmas = [&](const Frags& f) {
 #pragma unroll
@@ -1035,6 +1045,11 @@ static bool dma_enabled() {
   return on;
 }
 
+// The DMA tile kernels take Q8_0 stacks (row slices or the prefill pack) and packed Q4_K stacks.
+bool dma_path(int type, bool packed) {
+  return dma_enabled() && (type == EMBER_TYPE_Q8_0 || (type == EMBER_TYPE_Q4_K && packed));
+}
+
 bool gemm_supported(int type, int K) {
   return (type == EMBER_TYPE_Q8_0 || type == EMBER_TYPE_Q4_K || type == EMBER_TYPE_BF16 || type == EMBER_TYPE_F16) &&
          K % GBK == 0;
@@ -1053,20 +1068,24 @@ int launch_gemm_fmt(const GemmArgs& g, int max_mtiles, hipStream_t st) {
   const int mgroups = (max_mtiles + 7) / 8;
   const unsigned blocks = (unsigned)(8 * mgroups * NT);
   if (max_mtiles == 0 || NT == 0) return EMBER_OK;
-  const bool dma_off = !dma_enabled();
-  if (FMT == EMBER_TYPE_Q8_0 && !dma_off) {
+  if (dma_path(FMT, g.Wp != nullptr)) {
     static const bool dma_ok =
-        hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma_q8_kernel<GATED, false>),
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma_q8_kernel<GATED, kWfQ8Rows>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDmaLds) == hipSuccess &&
-        hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma_q8_kernel<GATED, true>),
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma_q8_kernel<GATED, kWfQ8Pack>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDmaLds) == hipSuccess &&
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma_q8_kernel<GATED, kWfQ4Pack>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDmaLds) == hipSuccess;
     if (!dma_ok) return EMBER_ERR_LAUNCH;
     GemmArgs gk = g;
     if (GATED || gk.ksplit < 1) gk.ksplit = 1;
-    if (gk.Wp)
-      gemm_dma_q8_kernel<GATED, true><<<blocks * (unsigned)gk.ksplit, kDmaThreads, kDmaLds, st>>>(gk, NT);
+    const unsigned nb = blocks * (unsigned)gk.ksplit;
+    if (FMT == EMBER_TYPE_Q4_K)
+      gemm_dma_q8_kernel<GATED, kWfQ4Pack><<<nb, kDmaThreads, kDmaLds, st>>>(gk, NT);
+    else if (gk.Wp)
+      gemm_dma_q8_kernel<GATED, kWfQ8Pack><<<nb, kDmaThreads, kDmaLds, st>>>(gk, NT);
     else
-      gemm_dma_q8_kernel<GATED, false><<<blocks * (unsigned)gk.ksplit, kDmaThreads, kDmaLds, st>>>(gk, NT);
+      gemm_dma_q8_kernel<GATED, kWfQ8Rows><<<nb, kDmaThreads, kDmaLds, st>>>(gk, NT);
     return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
   }
   if (g.split_bf16) return EMBER_ERR_TYPE;  // the split path runs in the 64-token-tile kernel only
@@ -1095,20 +1114,23 @@ int launch_skinny_fmt(GemmArgs g, int max_mtiles, hipStream_t st) {
   const int NT = (g.N + BN - 1) / BN;
   if (max_mtiles == 0 || NT == 0) return EMBER_OK;
   g.max_mt = max_mtiles;
-  const bool dma_off = !dma_enabled();
-  if (FMT == EMBER_TYPE_Q8_0 && !dma_off) {
+  if (dma_path(FMT, g.Wp != nullptr)) {
     static const bool ok =
-        hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma64_q8_kernel<GATED, false>),
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma64_q8_kernel<GATED, kWfQ8Rows>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)kD64Lds) == hipSuccess &&
-        hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma64_q8_kernel<GATED, true>),
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma64_q8_kernel<GATED, kWfQ8Pack>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kD64Lds) == hipSuccess &&
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma64_q8_kernel<GATED, kWfQ4Pack>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)kD64Lds) == hipSuccess;
     if (!ok) return EMBER_ERR_LAUNCH;
     if (GATED || g.ksplit < 1) g.ksplit = 1;
     const unsigned blocks = (unsigned)(max_mtiles * NT * g.ksplit);
-    if (g.Wp)
-      gemm_dma64_q8_kernel<GATED, true><<<blocks, kD64Threads, kD64Lds, st>>>(g, NT);
+    if (FMT == EMBER_TYPE_Q4_K)
+      gemm_dma64_q8_kernel<GATED, kWfQ4Pack><<<blocks, kD64Threads, kD64Lds, st>>>(g, NT);
+    else if (g.Wp)
+      gemm_dma64_q8_kernel<GATED, kWfQ8Pack><<<blocks, kD64Threads, kD64Lds, st>>>(g, NT);
     else
-      gemm_dma64_q8_kernel<GATED, false><<<blocks, kD64Threads, kD64Lds, st>>>(g, NT);
+      gemm_dma64_q8_kernel<GATED, kWfQ8Rows><<<blocks, kD64Threads, kD64Lds, st>>>(g, NT);
     return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
   }
   if constexpr (FMT == EMBER_TYPE_BF16) {
@@ -1138,8 +1160,8 @@ int launch_gemm_skinny(const GemmArgs& g, bool gated, int max_mtiles, hipStream_
 
 int gemm_skinny_max_tiles(int T, int k, int E) { return (T * k + SBM - 1) / SBM + std::min(E, T * k); }
 
-int gemm_ksplit(int type, int T, int k, int E, int N, int K) {
-  if (type != EMBER_TYPE_Q8_0 || !dma_enabled()) return 1;  // the split lives in the Q8_0 DMA kernel
+int gemm_ksplit(int type, bool packed, int T, int k, int E, int N, int K) {
+  if (!dma_path(type, packed)) return 1;  // the split lives in the DMA kernels
   // expected 256-token tiles (segments average T k / E tokens) times n-tiles: aim for >= 4 rounds
   const int est_tiles = (T * k + GBM - 1) / GBM + E / 2;
   const int blocks = est_tiles * ((N + 255) / 256);
@@ -1148,8 +1170,8 @@ int gemm_ksplit(int type, int T, int k, int E, int N, int K) {
   return ks;
 }
 
-int gemm_skinny_ksplit(int type, int max_mtiles, int N, int K) {
-  if (type != EMBER_TYPE_Q8_0 || !dma_enabled()) return 1;  // the split lives in the Q8_0 DMA kernel
+int gemm_skinny_ksplit(int type, bool packed, int max_mtiles, int N, int K) {
+  if (!dma_path(type, packed)) return 1;  // the split lives in the DMA kernels
   const int blocks = max_mtiles * ((N + 255) / 256);
   int ks = 1;
   while (ks < kMaxKSplit && blocks * ks < 512 && K / GBK >= 16 * ks * 2) ks *= 2;
@@ -1222,7 +1244,8 @@ int launch_build_tiles(const int32_t* offsets, int E, bool skinny, int32_t* tile
 }
 
 
-// ---- prefill pack: one thread per (tile, row), 17 dwords each (a one-time copy at weight load)
+// ---- prefill pack: one thread per (tile, row), one pack row each (a one-time copy at weight load)
+template <int FMT>
 __global__ void __launch_bounds__(256) prefill_pack_kernel(const uint8_t* __restrict__ W0, const uint8_t* __restrict__ W1,
                                                            int64_t expert_stride, int64_t row_bytes, int N, int NT,
                                                            int nk, int64_t total_rows, uint8_t* __restrict__ dst) {
@@ -1236,21 +1259,46 @@ __global__ void __launch_bounds__(256) prefill_pack_kernel(const uint8_t* __rest
   const bool gated = W1 != nullptr;
   const int q = gated ? (r >> 7) : 0;
   const int n = min(nt * (gated ? 128 : 256) + (gated ? (r & 127) : r), N - 1);
-  const uint32_t* src = reinterpret_cast<const uint32_t*>((q ? W1 : W0) + (int64_t)e * expert_stride +
-                                                          (int64_t)n * row_bytes + (int64_t)kc * kPackRowB);
-  uint32_t* d = reinterpret_cast<uint32_t*>(dst + i * kPackRowB);
+  const uint8_t* row = (q ? W1 : W0) + (int64_t)e * expert_stride + (int64_t)n * row_bytes;
+  if constexpr (FMT == EMBER_TYPE_Q4_K) {
+    // K tile kc = quarter kc % 4 of super-block kc / 4: its groups 2 (kc % 4) and + 1
+    uint32_t raw[12];
+    Deq<EMBER_TYPE_Q4_K>::load(row, kc, raw);
+    const float dd = half_bits_to_float(raw[0] & 0xffff), dmin = half_bits_to_float(raw[0] >> 16);
+    uint32_t* d = reinterpret_cast<uint32_t*>(dst + i * kPackRowQ4B);
 #pragma unroll
-  for (int w = 0; w < kPackRowB / 4; ++w) d[w] = src[w];
+    for (int gi = 0; gi < 2; ++gi) {
+      int sc, mn;
+      Deq<EMBER_TYPE_Q4_K>::scale_min(raw, 2 * (kc & 3) + gi, &sc, &mn);
+      const half2_t am = {(_Float16)(dd * (float)sc), (_Float16)(-(dmin * (float)mn))};
+      d[gi] = u32(am);
+    }
+#pragma unroll
+    for (int w = 0; w < 8; ++w) d[2 + w] = raw[4 + w];
+  } else {
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(row + (int64_t)kc * kPackRowB);
+    uint32_t* d = reinterpret_cast<uint32_t*>(dst + i * kPackRowB);
+#pragma unroll
+    for (int w = 0; w < kPackRowB / 4; ++w) d[w] = src[w];
+  }
 }
 
-int launch_prefill_pack(const void* W0, const void* W1, int64_t expert_stride, int64_t row_bytes, int E, int N, int K,
-                        uint8_t* dst, hipStream_t st) {
+int launch_prefill_pack(int type, const void* W0, const void* W1, int64_t expert_stride, int64_t row_bytes, int E,
+                        int N, int K, uint8_t* dst, hipStream_t st) {
   const int NT = W1 ? (N + 127) / 128 : (N + 255) / 256, nk = K / 64;
   const int64_t total = (int64_t)E * NT * nk * 256;
   if (total == 0) return EMBER_OK;
   const int64_t blocks = (total + 255) / 256;
-  prefill_pack_kernel<<<dim3((unsigned)blocks), 256, 0, st>>>(static_cast<const uint8_t*>(W0), static_cast<const uint8_t*>(W1),
-                                                             expert_stride, row_bytes, N, NT, nk, total, dst);
+  const uint8_t* w0 = static_cast<const uint8_t*>(W0);
+  const uint8_t* w1 = static_cast<const uint8_t*>(W1);
+  if (type == EMBER_TYPE_Q4_K)
+    prefill_pack_kernel<EMBER_TYPE_Q4_K><<<dim3((unsigned)blocks), 256, 0, st>>>(w0, w1, expert_stride, row_bytes, N, NT,
+                                                                                nk, total, dst);
+  else if (type == EMBER_TYPE_Q8_0)
+    prefill_pack_kernel<EMBER_TYPE_Q8_0><<<dim3((unsigned)blocks), 256, 0, st>>>(w0, w1, expert_stride, row_bytes, N, NT,
+                                                                                nk, total, dst);
+  else
+    return EMBER_ERR_TYPE;
   return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
 }
 

@@ -181,30 +181,37 @@ struct GemmArgs {
   bool split_bf16;
   int64_t a_plane, h_plane;
 };
-// Prefill pack (ember_moe_prefill_pack): Q8_0 tiles of 256 weight rows x 64 columns, 68-byte rows,
-// one tile contiguous; the gate/up section [E][ceil(d_ff / 128)][d / 64] (each tile: the 128 gate rows
-// of an n-tile, then its 128 up rows), then the down section [E][ceil(d / 256)][d_ff / 64]; rows past a
-// matrix's end repeat its last row (as the GEMM's clamped loads would).
+// Prefill pack (ember_moe_prefill_pack): tiles of 256 weight rows x 64 columns, one tile contiguous;
+// the gate/up section [E][ceil(d_ff / 128)][d / 64] (each tile: the 128 gate rows of an n-tile, then
+// its 128 up rows), then the down section [E][ceil(d / 256)][d_ff / 64]; rows past a matrix's end
+// repeat its last row (as the GEMM's clamped loads would). A row's 64 columns:
+//   Q8_0 stacks: the two Q8_0 blocks as they are (68 bytes);
+//   Q4_K stacks: 40 bytes = the fp16 factors {a0, m0, a1, m1} of its two 32-element groups, a = d * sc
+//     and m = -dmin * mn each rounded to fp16 once (weight = a * q + m), then the 32 nibble bytes of the
+//     super-block quarter as they are (low nibbles: group 0, high nibbles: group 1).
 constexpr int kPackRowB = 68;
+constexpr int kPackRowQ4B = 40;
+inline int pack_row_bytes(int type) { return type == EMBER_TYPE_Q4_K ? kPackRowQ4B : kPackRowB; }
+inline int64_t pack_tile_bytes(int type) { return (int64_t)256 * pack_row_bytes(type); }
 constexpr int64_t kPackTileB = (int64_t)256 * kPackRowB;
 struct PackLayout {
   int nt_gu, nk_gu, nt_dn, nk_dn;
   int64_t gu, dn, end;  // byte offsets of the sections, total
 };
-inline PackLayout pack_layout(int d, int d_ff, int E) {
+inline PackLayout pack_layout(int d, int d_ff, int E, int type) {
   PackLayout p;
   p.nt_gu = (d_ff + 127) / 128;
   p.nk_gu = d / 64;
   p.nt_dn = (d + 255) / 256;
   p.nk_dn = d_ff / 64;
   p.gu = 0;
-  p.dn = (int64_t)E * p.nt_gu * p.nk_gu * kPackTileB;
-  p.end = p.dn + (int64_t)E * p.nt_dn * p.nk_dn * kPackTileB;
+  p.dn = (int64_t)E * p.nt_gu * p.nk_gu * pack_tile_bytes(type);
+  p.end = p.dn + (int64_t)E * p.nt_dn * p.nk_dn * pack_tile_bytes(type);
   return p;
 }
-// Fills one section of the pack from ggml Q8_0 rows (W1 non-null: the gate/up section).
-int launch_prefill_pack(const void* W0, const void* W1, int64_t expert_stride, int64_t row_bytes, int E, int N, int K,
-                        uint8_t* dst, hipStream_t st);
+// Fills one section of the pack from ggml rows of `type` (Q8_0 or Q4_K; W1 non-null: the gate/up section).
+int launch_prefill_pack(int type, const void* W0, const void* W1, int64_t expert_stride, int64_t row_bytes, int E,
+                        int N, int K, uint8_t* dst, hipStream_t st);
 bool gemm_supported(int type, int K);
 int gemm_max_tiles(int T, int k, int E);
 int launch_gemm(const GemmArgs& g, bool gated, int max_mtiles, hipStream_t st);
@@ -220,9 +227,11 @@ int gemm_skinny_max_tiles(int T, int k, int E);
 // K split of the skinny path's plain (down) projection: 1..kMaxKSplit, so that the launch has enough
 // blocks for the chip when the output is narrow
 constexpr int kMaxKSplit = 4;
-int gemm_skinny_ksplit(int type, int max_mtiles, int N, int K);
+int gemm_skinny_ksplit(int type, bool packed, int max_mtiles, int N, int K);
 // ... and of the 256-token-tile path's (the down launch of a long prefill has few blocks per n-tile row)
-int gemm_ksplit(int type, int T, int k, int E, int N, int K);
+int gemm_ksplit(int type, bool packed, int T, int k, int E, int N, int K);
+// Whether the DMA tile kernels serve stacks of `type` (packed: with a prefill pack): Q8_0, packed Q4_K.
+bool dma_path(int type, bool packed);
 
 int launch_combine(const float* y, int nparts, int64_t part_stride, const float* gates, const int32_t* pos,
                    const float* y_shared, const float* shared_gate_logit, float scale, int T,

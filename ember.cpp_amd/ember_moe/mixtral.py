@@ -24,7 +24,8 @@ from dataclasses import dataclass
 
 import numpy as np
 
-from . import EmberError, Layer, Q4_K, TYPE_NAMES, _ptr, moe_ffn, quantize, scratch_bytes
+from . import (EmberError, Layer, Q4_K, TYPE_NAMES, _ptr, moe_ffn, prefill_pack, prefill_pack_bytes, quantize,
+               scratch_bytes)
 
 
 @dataclass
@@ -43,6 +44,7 @@ class MixtralSpec:
     expert_type: int = Q4_K
     expert_sets: int = 4
     seed: int = 0
+    prefill_pack: bool = True  # each layer's experts also repacked for the prefill tile GEMMs (ember_moe_prefill_pack)
 
 
 class Mixtral:
@@ -82,13 +84,19 @@ class Mixtral:
             L.gate, L.gate_type = _ptr(gate), s.expert_type
             L.up, L.up_type = _ptr(up), s.expert_type
             L.down, L.down_type = _ptr(down), s.expert_type
-            self.experts.append((gate, up, down))
+            packs = ()
+            if s.prefill_pack and prefill_pack_bytes(L) > 0:
+                buf = torch.empty(prefill_pack_bytes(L), dtype=torch.uint8, device=device)
+                prefill_pack(L, buf)
+                packs = (buf,)
+            self.experts.append((gate, up, down) + packs)
             self.layers.append(L)
         del sets
         torch.cuda.synchronize()
-        self.expert_bytes = sum(sum(t.numel() for t in e) for e in self.experts)
+        self.expert_bytes = sum(sum(t.numel() for t in e[:3]) for e in self.experts)
+        self.pack_bytes = sum(sum(t.numel() for t in e[3:]) for e in self.experts)
         log(f"[e2e] weights ready in {time.time() - t0:.1f}s: {s.n_layers} layers, experts "
-            f"{TYPE_NAMES[s.expert_type]} {self.expert_bytes / 1e9:.1f} GB")
+            f"{TYPE_NAMES[s.expert_type]} {self.expert_bytes / 1e9:.1f} GB (+ prefill packs {self.pack_bytes / 1e9:.1f} GB)")
         # RoPE tables (rotate-half pairing) and the KV cache
         inv = 1.0 / (s.rope_theta ** (torch.arange(0, s.head_dim, 2, device=device, dtype=torch.float64) / s.head_dim))
         ang = torch.arange(max_ctx, device=device, dtype=torch.float64)[:, None] * inv[None, :]

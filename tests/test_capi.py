@@ -109,10 +109,14 @@ def test_prefill_pack_sizes_and_validation():
     L = _layer(d=512, d_ff=704, E=4)
     assert em.prefill_pack_bytes(L) == expect(512, 704, 4)
     assert em.prefill_pack_bytes(_layer(d=4096, d_ff=14336, E=8)) == expect(4096, 14336, 8)
-    # only all-Q8_0 layers with whole 64-column tiles have a pack
+    # only all-Q8_0 / all-Q4_K layers with whole 64-column tiles have a pack
     assert em.prefill_pack_bytes(_layer(gate_type=em.BF16, up_type=em.BF16, down_type=em.BF16)) == 0
     assert em.prefill_pack_bytes(_layer(down_type=em.BF16)) == 0
     assert em.prefill_pack_bytes(_layer(d=512, d_ff=736)) == 0  # d_ff not a multiple of 64
+    # all-Q4_K layers: 40-byte rows (the two groups' fp16 factors and the quarter's nibbles)
+    q4 = dict(gate_type=em.Q4_K, up_type=em.Q4_K, down_type=em.Q4_K)
+    assert em.prefill_pack_bytes(_layer(d=512, d_ff=768, E=4, **q4)) == expect(512, 768, 4) * 40 // 68
+    assert em.prefill_pack_bytes(_layer(d=512, d_ff=768, E=4, gate_type=em.Q4_K, up_type=em.Q4_K)) == 0
     lib = em.lib()
     assert lib.ember_moe_prefill_pack(ctypes.byref(_layer(down_type=em.BF16)), 0x100000, 1 << 30, None) == em.ERR_TYPE
     assert lib.ember_moe_prefill_pack(ctypes.byref(L), 0, 1 << 30, None) == em.ERR_NULL

@@ -21,6 +21,12 @@ pytestmark = pytest.mark.skipif(not O.ref_gguf_available(), reason="oracle/_ref/
                                 "(the reference sources are absent)")
 
 
+@pytest.fixture(autouse=True)
+def _log_in_tmp(tmp_path, monkeypatch):
+    """The reference's logger (logger.cpp) appends to debugging.log in the working directory."""
+    monkeypatch.chdir(tmp_path)
+
+
 def _ours(path):
     with em.Gguf(path) as g:
         ts = []

@@ -1,7 +1,9 @@
 """GPU tests of the prefill pack (ember_moe_prefill_pack): the Q8_0 tile GEMMs reading packed tiles
-gives the same output bits as reading the ggml rows (same values, same arithmetic), on tile-aligned
-and partial-tile shapes, with ragged expert segments, through the down projection's K split; and the
-oracle agrees at the Q8_0 bar."""
+give the same output bits as reading the ggml rows (same values, same arithmetic), on tile-aligned
+and partial-tile shapes, with ragged expert segments, through the down projection's K split; Q4_K
+stacks, whose pack feeds the same DMA tile kernels in place of the register-staged ones, give the same
+bits as those wherever the down projection is not split over K (the factors and the order of the MFMA
+accumulation are the same); and the oracle agrees at the quantized bar."""
 import numpy as np
 import pytest
 
@@ -55,6 +57,37 @@ def test_pack_deepseek_style_with_shared_expert(gpu):
     assert rel_l2(y_pack, run_oracle(hl, x)) < 2e-3
 
 
+# Q4_K: d, d_ff multiples of 256; more than 2 tokens per expert takes the 256-token tiles
+@pytest.mark.parametrize("d,d_ff,E,k,T", [(512, 768, 8, 2, 320), (256, 512, 4, 2, 1000), (768, 512, 16, 4, 700),
+                                          (512, 768, 8, 2, 40)])
+def test_q4_k_pack_same_bits_as_register_staged(gpu, monkeypatch, d, d_ff, E, k, T):
+    """Both runs forced onto the 256-token tiles (EMBER_MOE_PATH=gemm): the packed DMA kernel and the
+    register-staged one form the same fp16 operands and pair the same K elements in each MFMA."""
+    spec = em.LayerSpec(d=d, d_ff=d_ff, E=E, k=k, wtype=em.Q4_K, seed=24)
+    hl = em.make_host_layer(spec)
+    x = em.make_input(spec, T)
+    print(f"prefill pack q4_k d={d} d_ff={d_ff} E={E} T={T}", flush=True)
+    y_default = _run(hl, x, pack=True)
+    monkeypatch.setenv("EMBER_MOE_PATH", "gemm")
+    y_rows = _run(hl, x, pack=False)
+    y_pack = _run(hl, x, pack=True)
+    monkeypatch.delenv("EMBER_MOE_PATH")
+    assert same_bits(y_pack, y_rows)
+    assert rel_l2(y_default, run_oracle(hl, x)) < 2e-3
+
+
+def test_q4_k_pack_with_k_split(gpu):
+    """A long down projection (d_ff 4096) on few blocks: the DMA kernel splits its K and the combine adds
+    the parts in a fixed order, so the bits differ from the unsplit kernel's but the oracle's bar holds."""
+    spec = em.LayerSpec(d=256, d_ff=4096, E=4, k=2, wtype=em.Q4_K, seed=25)
+    hl = em.make_host_layer(spec)
+    x = em.make_input(spec, 512)
+    print("prefill pack q4_k K split", flush=True)
+    y_pack = _run(hl, x, pack=True)
+    assert rel_l2(y_pack, _run(hl, x, pack=False)) < 1e-5
+    assert rel_l2(y_pack, run_oracle(hl, x)) < 2e-3
+
+
 def test_pack_rejected_for_other_layers(gpu):
     import torch
 
@@ -74,17 +107,19 @@ def test_pack_rejected_for_other_layers(gpu):
     assert em.moe_ffn(dl.desc, x, 4, out, scratch) == em.ERR_TYPE
 
 
-@pytest.mark.parametrize("pack", [False, True])
-def test_64_token_tiles_forced(gpu, monkeypatch, pack):
-    """The 64-token-tile Q8_0 kernel (a tuning choice, EMBER_MOE_PATH=skinny) agrees with the default
-    kernel on the oracle's bar, with and without the pack."""
-    spec = em.LayerSpec(d=512, d_ff=704, E=8, k=2, wtype=em.Q8_0, seed=23)
+@pytest.mark.parametrize("wtype,d_ff,pack", [(em.Q8_0, 704, False), (em.Q8_0, 704, True), (em.Q4_K, 768, True)])
+def test_64_token_tiles_forced(gpu, monkeypatch, wtype, d_ff, pack):
+    """The 64-token-tile DMA kernel (a tuning choice, EMBER_MOE_PATH=skinny) agrees with the default
+    kernel on the oracle's bar, with and without the pack (Q4_K: against its register-staged kernel)."""
+    spec = em.LayerSpec(d=512, d_ff=d_ff, E=8, k=2, wtype=wtype, seed=23)
     hl = em.make_host_layer(spec)
     x = em.make_input(spec, 90)
     print(f"64-token tiles forced, pack={pack}", flush=True)
     monkeypatch.setenv("EMBER_MOE_PATH", "skinny")
     y = _run(hl, x, pack=pack)
-    if pack:
-        assert same_bits(y, _run(hl, x, pack=False))  # packed and row-sliced tiles: the same bits
+    if pack and wtype == em.Q8_0:
+        assert same_bits(y, _run(hl, x, pack=False))  # packed tiles and the ggml rows: the same bits
+    elif pack:  # the register-staged 64-token kernel pairs other K elements per MFMA: f32 rounding apart
+        assert rel_l2(y, _run(hl, x, pack=False)) < 1e-5
     monkeypatch.delenv("EMBER_MOE_PATH")
     assert rel_l2(y, run_oracle(hl, x)) < 2e-3
