@@ -74,7 +74,7 @@ class Mixtral:
                 w = randn(*shape, dtype=torch.float32).cpu().numpy().reshape(-1)
                 mats.append(torch.from_numpy(quantize(s.expert_type, w)).to(device))
             sets.append(mats)
-        self.experts, self.layers = [], []
+        self.experts, self.layers, self.packs = [], [], []
         for l in range(s.n_layers):
             gate, up, down = (m.clone() for m in sets[l % len(sets)])
             L = Layer()
@@ -84,17 +84,16 @@ class Mixtral:
             L.gate, L.gate_type = _ptr(gate), s.expert_type
             L.up, L.up_type = _ptr(up), s.expert_type
             L.down, L.down_type = _ptr(down), s.expert_type
-            packs = ()
             if s.prefill_pack and prefill_pack_bytes(L) > 0:
                 buf = torch.empty(prefill_pack_bytes(L), dtype=torch.uint8, device=device)
                 prefill_pack(L, buf)
-                packs = (buf,)
-            self.experts.append((gate, up, down) + packs)
+                self.packs.append(buf)
+            self.experts.append((gate, up, down))
             self.layers.append(L)
         del sets
         torch.cuda.synchronize()
-        self.expert_bytes = sum(sum(t.numel() for t in e[:3]) for e in self.experts)
-        self.pack_bytes = sum(sum(t.numel() for t in e[3:]) for e in self.experts)
+        self.expert_bytes = sum(sum(t.numel() for t in e) for e in self.experts)
+        self.pack_bytes = sum(t.numel() for t in self.packs)
         log(f"[e2e] weights ready in {time.time() - t0:.1f}s: {s.n_layers} layers, experts "
             f"{TYPE_NAMES[s.expert_type]} {self.expert_bytes / 1e9:.1f} GB (+ prefill packs {self.pack_bytes / 1e9:.1f} GB)")
         # RoPE tables (rotate-half pairing) and the KV cache
