@@ -272,7 +272,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-c5", action="store_true", help="skip the end-to-end config 5 run the default c2 run adds")
     ap.add_argument("--no-pack", action="store_true",
-                    help="run prefill on the ggml rows instead of the prefill pack (all-Q8_0 layers)")
+                    help="run prefill without the prefill pack (Q8_0 / Q4_K tiles, BF16 row exponents)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device-to-device copies of MIB MiB (the reference kernel that scales "
                          "rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes), then exit")

@@ -39,6 +39,8 @@ int path_mode(int type_in, int K_in, int type_out, int K_out, double avg_m, int 
   // vs 387 us with the prefill pack, 447 vs 483 without; T = 256: 498 vs 612)
   const bool q8 = type_in == EMBER_TYPE_Q8_0 && type_out == EMBER_TYPE_Q8_0;
   if (q8) return avg_m <= 1.5 ? kGemv : kGemm;
+  // (packed BF16: row exponents for the fp16 MFMA path, which both tile kernels have; without them BF16 runs
+  // the split bf16 MFMA, which only the 64-token-tile kernel implements)
   // packed Q4_K (the same DMA tile kernels): the GEMV up to 1.6 tokens per expert, the 64-token tiles up to
   // 3, the 256-token tiles beyond (Mixtral-shaped: T = 6 GEMV 270 vs 273 us, T = 8 327 vs 275 (64) vs 298
   // (256), T = 16 372 (64) vs 302 (256); Qwen-shaped E = 128: T = 24 170 vs 175, T = 32 186 vs 177)
@@ -58,8 +60,7 @@ int path_mode(int type_in, int K_in, int type_out, int K_out, double avg_m, int 
     return kGemv;
   }
   if (avg_m <= 96.0) return kSkinny;
-  // BF16 stacks run bf16 MFMA with split activations, which only the 64-token-tile kernel implements
-  if (type_in == EMBER_TYPE_BF16 && type_out == EMBER_TYPE_BF16) return kSkinny;
+  if (type_in == EMBER_TYPE_BF16 && type_out == EMBER_TYPE_BF16 && !packed) return kSkinny;
   return kGemm;
 }
 
@@ -97,12 +98,24 @@ bool is_routed(const ember_moe_layer* w) {
   return w->scoring == EMBER_SCORE_SIGMOID || w->selection_bias != nullptr || w->groups_n > 1;
 }
 
-// The prefill pack covers layers whose routed stacks are all Q8_0 with whole 64-column tiles.
-// the prefill pack serves layers whose three routed stacks are all Q8_0 or all Q4_K
+bool bf16_stacks(const ember_moe_layer* w) {
+  return w->gate_type == EMBER_TYPE_BF16 && w->up_type == EMBER_TYPE_BF16 && w->down_type == EMBER_TYPE_BF16;
+}
+bool bf16_shared(const ember_moe_layer* w) {
+  return w->d_ff_shared > 0 && w->gate_shared_type == EMBER_TYPE_BF16 && w->up_shared_type == EMBER_TYPE_BF16 &&
+         w->down_shared_type == EMBER_TYPE_BF16;
+}
+// The prefill pack serves layers whose three routed stacks are all Q8_0 or all Q4_K (tiles for the DMA
+// GEMMs, whole 64-column tiles) or all BF16 (row exponents for the fp16 MFMA path).
 bool packable(const ember_moe_layer* w) {
+  if (bf16_stacks(w)) return true;
   const int t = w->gate_type;
   return (t == EMBER_TYPE_Q8_0 || t == EMBER_TYPE_Q4_K) && w->up_type == t && w->down_type == t && w->d % 64 == 0 &&
          w->d_ff % 64 == 0;
+}
+// a BF16 layer's pack: the row exponents (Bf16ExpLayout)
+Bf16ExpLayout bf16_exps(const ember_moe_layer* w) {
+  return bf16_exp_layout(w->d, w->d_ff, w->E, w->d_ff_shared, bf16_shared(w));
 }
 
 int validate(const ember_moe_layer* w) {
@@ -186,9 +199,10 @@ Layout layout(const ember_moe_layer* w, int T) {
   l.ys = o; o = align_up(o + (w->d_ff_shared > 0 ? (size_t)T * w->d * 4 : 0));
   l.sg = o; o = align_up(o + (w->shared_gate ? (size_t)T * 4 : 0));
   l.mode = path_mode(w->gate_type, w->d, w->down_type, w->d_ff, (double)T * w->k / w->E, w->E, w->prefill_pack != nullptr);
-  l.mode_shared = w->d_ff_shared > 0
-                      ? path_mode(w->gate_shared_type, w->d, w->down_shared_type, w->d_ff_shared, (double)T, 1)
-                      : kGemv;
+  const bool pack_bf16 = w->prefill_pack && bf16_stacks(w);  // row exponents, also the shared expert's if BF16
+  l.mode_shared = w->d_ff_shared > 0 ? path_mode(w->gate_shared_type, w->d, w->down_shared_type, w->d_ff_shared,
+                                                 (double)T, 1, pack_bf16 && bf16_shared(w))
+                                     : kGemv;
   // a shared expert of the routed experts' types rides in the routed decode launches as one more segment
   // (a few µs), while on its own its T rows make a dense MFMA launch of only d_ff_shared / 128 blocks
   // (C4, T = 4: 205 µs with it on the MFMA path, 100 µs in the routed launches)
@@ -199,8 +213,9 @@ Layout layout(const ember_moe_layer* w, int T) {
                        : l.mode == kSkinny ? (size_t)gemm_skinny_max_tiles(T, w->k, w->E)
                                            : 0;
   const bool mfma = l.mode != kGemv, mfma_sh = w->d_ff_shared > 0 && l.mode_shared != kGemv;
-  const bool sp = split_bf16(w->gate_type, w->down_type);
-  const bool sp_sh = w->d_ff_shared > 0 && split_bf16(w->gate_shared_type, w->down_shared_type);
+  const bool sp = split_bf16(w->gate_type, w->down_type) && !pack_bf16;
+  const bool sp_sh = w->d_ff_shared > 0 && split_bf16(w->gate_shared_type, w->down_shared_type) &&
+                     !(pack_bf16 && bf16_shared(w));
   const bool need16 = (mfma && !sp) || (mfma_sh && !sp_sh), needb = (mfma && sp) || (mfma_sh && sp_sh);
   l.x16 = o; o = align_up(o + (need16 ? (size_t)T * w->d * 2 : 0));
   l.xexp = o; o = align_up(o + (need16 ? (size_t)T * 4 : 0));
@@ -351,8 +366,15 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
   const bool shared_fused = shared && !shared_mfma && l.mode == kGemv && w->gate_shared_type == w->gate_type &&
                             w->down_shared_type == w->down_type;
   // the activations of the MFMA paths: row-scaled fp16 (x16, xexp) and / or split bf16 planes (xb)
-  const bool sp = split_bf16(w->gate_type, w->down_type);
-  const bool sp_sh = shared && split_bf16(w->gate_shared_type, w->down_shared_type);
+  // BF16 stacks: split bf16 MFMA, or with a prefill pack (row exponents) the fp16 path
+  const bool pack_bf16 = w->prefill_pack && bf16_stacks(w);
+  const bool pack_bf16_sh = pack_bf16 && bf16_shared(w);
+  const Bf16ExpLayout bx = bf16_exps(w);
+  auto wexp = [&](int64_t off) {
+    return off < 0 ? nullptr : reinterpret_cast<const int16_t*>(static_cast<const uint8_t*>(w->prefill_pack) + off);
+  };
+  const bool sp = split_bf16(w->gate_type, w->down_type) && !pack_bf16;
+  const bool sp_sh = shared && split_bf16(w->gate_shared_type, w->down_shared_type) && !pack_bf16_sh;
   _Float16* x16 = at<_Float16>(scratch, l.x16);
   int32_t* xexp = at<int32_t>(scratch, l.xexp);
   uint16_t* xb = at<uint16_t>(scratch, l.xb);
@@ -406,8 +428,13 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     g.out_h = h16;
     // the prefill pack serves the DMA tile kernels (256- and 64-token tiles alike)
     const PackLayout pl = pack_layout(d, d_ff, E, w->gate_type);
-    const uint8_t* pack = static_cast<const uint8_t*>(w->prefill_pack);
+    const uint8_t* pack = pack_bf16 ? nullptr : static_cast<const uint8_t*>(w->prefill_pack);
     g.Wp = pack ? pack + pl.gu : nullptr;
+    if (pack_bf16) {
+      g.w_exp0 = wexp(bx.gate);
+      g.w_exp1 = wexp(bx.up);
+      g.w_hexp = wexp(bx.hmax);
+    }
     const int mt = skinny ? gemm_skinny_max_tiles(T, k, E) : gemm_max_tiles(T, k, E);
     if ((s = gemm(g, true, mt))) return s;
     mark(ev, 4, st);
@@ -426,6 +453,9 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     g.out_h = nullptr;
     g.out_y = y;
     g.Wp = pack ? pack + pl.dn : nullptr;
+    g.w_exp0 = pack_bf16 ? wexp(bx.down) : nullptr;
+    g.w_exp1 = nullptr;
+    g.w_hexp = nullptr;
     g.ksplit = ksplit = skinny ? gemm_skinny_ksplit(g.type, pack != nullptr, mt, d, d_ff)
                                : gemm_ksplit(g.type, pack != nullptr, T, k, E, d, d_ff);
     g.part_stride = (int64_t)T * k * d;
@@ -567,6 +597,11 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     g.a_exp = sp_sh ? nullptr : xexp;
     g.h_exp = sp_sh ? nullptr : hsexp;
     g.split_bf16 = sp_sh;
+    if (pack_bf16_sh) {
+      g.w_exp0 = wexp(bx.sgate);
+      g.w_exp1 = wexp(bx.sup);
+      g.w_hexp = wexp(bx.shmax);
+    }
     g.a_plane = (int64_t)T * d;
     g.h_plane = (int64_t)T * w->d_ff_shared;
     g.T = T;
@@ -586,6 +621,9 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     g.a_plane = (int64_t)T * w->d_ff_shared;
     g.W0 = w->down_shared;
     g.W1 = nullptr;
+    g.w_exp0 = pack_bf16_sh ? wexp(bx.sdown) : nullptr;
+    g.w_exp1 = nullptr;
+    g.w_hexp = nullptr;
     g.type = w->down_shared_type;
     g.row_bytes = row_bytes(w->down_shared_type, w->d_ff_shared);
     g.N = d;
@@ -713,6 +751,7 @@ int ember_moe_scratch_routing(const ember_moe_layer* w, int T, ember_moe_routing
 
 size_t ember_moe_prefill_pack_bytes(const ember_moe_layer* w) {
   if (validate(w) != EMBER_OK || !packable(w)) return 0;
+  if (bf16_stacks(w)) return (size_t)bf16_exps(w).end;
   return (size_t)pack_layout(w->d, w->d_ff, w->E, w->gate_type).end;
 }
 
@@ -722,6 +761,27 @@ int ember_moe_prefill_pack(const ember_moe_layer* w, void* pack, size_t pack_byt
   if (!packable(w)) return EMBER_ERR_TYPE;
   if (!pack) return EMBER_ERR_NULL;
   if (reinterpret_cast<uintptr_t>(pack) % 256) return EMBER_ERR_ALIGN;
+  if (bf16_stacks(w)) {
+    const Bf16ExpLayout bx = bf16_exps(w);
+    if (pack_bytes < (size_t)bx.end) return EMBER_ERR_SCRATCH;
+    uint8_t* p = static_cast<uint8_t*>(pack);
+    auto o = [&](int64_t off) { return reinterpret_cast<int16_t*>(p + off); };
+    const int64_t rb_gu = row_bytes(EMBER_TYPE_BF16, w->d), rb_dn = row_bytes(EMBER_TYPE_BF16, w->d_ff);
+    if ((s = launch_bf16_row_exps(w->gate, (int64_t)w->E * w->d_ff, w->d, rb_gu, o(bx.gate), st)) ||
+        (s = launch_bf16_row_exps(w->up, (int64_t)w->E * w->d_ff, w->d, rb_gu, o(bx.up), st)) ||
+        (s = launch_bf16_row_exps(w->down, (int64_t)w->E * w->d, w->d_ff, rb_dn, o(bx.down), st)) ||
+        (s = launch_bf16_pair_max(o(bx.gate), o(bx.up), w->E, w->d_ff, o(bx.hmax), st)))
+      return s;
+    if (bx.sgate >= 0) {
+      const int64_t rs_gu = row_bytes(EMBER_TYPE_BF16, w->d), rs_dn = row_bytes(EMBER_TYPE_BF16, w->d_ff_shared);
+      if ((s = launch_bf16_row_exps(w->gate_shared, w->d_ff_shared, w->d, rs_gu, o(bx.sgate), st)) ||
+          (s = launch_bf16_row_exps(w->up_shared, w->d_ff_shared, w->d, rs_gu, o(bx.sup), st)) ||
+          (s = launch_bf16_row_exps(w->down_shared, w->d, w->d_ff_shared, rs_dn, o(bx.sdown), st)) ||
+          (s = launch_bf16_pair_max(o(bx.sgate), o(bx.sup), 1, w->d_ff_shared, o(bx.shmax), st)))
+        return s;
+    }
+    return EMBER_OK;
+  }
   const int t = w->gate_type;
   const PackLayout pl = pack_layout(w->d, w->d_ff, w->E, t);
   if (pack_bytes < (size_t)pl.end) return EMBER_ERR_SCRATCH;

@@ -218,8 +218,10 @@ __device__ inline uint16_t bf16_rne(float v) {
   return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
 }
 __device__ inline float bf16_f32(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
-// h[p][n] = SwiGLU of the unscaled gate and up dots, stored in the A format of the down projection
-__device__ inline void store_h(const GemmArgs& g, size_t o, int p, int e, float ga, float ua, bool first_col) {
+// h[p][n] = SwiGLU of the unscaled gate and up dots, stored in the A format of the down projection; the
+// fp16 form is h times 2^-(2 e + eh), eh the expert's weight-range exponent (GemmArgs::w_hexp)
+__device__ inline void store_h(const GemmArgs& g, size_t o, int p, int e, float ga, float ua, bool first_col,
+                               int eh = 0) {
   const float hv = swiglu_g(__builtin_ldexpf(ga, e), __builtin_ldexpf(ua, e));
   if (g.split_bf16) {
     uint16_t* hb = reinterpret_cast<uint16_t*>(g.out_h);
@@ -227,11 +229,22 @@ __device__ inline void store_h(const GemmArgs& g, size_t o, int p, int e, float 
     hb[o] = hi;
     hb[g.h_plane + o] = bf16_rne(hv - bf16_f32(hi));
   } else {
-    g.out_h[o] = (_Float16)__builtin_ldexpf(hv, -2 * e);
-    if (first_col && g.h_exp) g.h_exp[p] = 2 * e;
+    g.out_h[o] = (_Float16)__builtin_ldexpf(hv, -2 * e - eh);
+    if (first_col && g.h_exp) g.h_exp[p] = 2 * e + eh;
   }
 }
 __device__ inline float unscale_y(float acc, int e) { return __builtin_ldexpf(acc, e); }
+// BF16 weights on the fp16 path: the row's exponent (GemmArgs::w_exp0 / w_exp1; 0 without a table)
+__device__ inline int w_exp_of(const int16_t* t, int e, int N, int n) { return t ? (int)t[(int64_t)e * N + n] : 0; }
+// 16 dwords of bf16 pairs -> fp16 pairs, each value times sc (a power of two, so the only rounding is
+// the fp16 one)
+__device__ inline void bf16_to_f16_scaled(const uint32_t* raw, float sc, uint32_t* out) {
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const half2_t v = {(_Float16)(as_f32(raw[i] << 16) * sc), (_Float16)(as_f32(raw[i] & 0xffff0000u) * sc)};
+    out[i] = u32(v);
+  }
+}
 // the tile's row exponents, looked up once into LDS (rows of the tile: positions p0 .. p0 + rows)
 __device__ inline void load_row_exps(const GemmArgs& g, int p0, int rows, int* s_rexp) {
   for (int r = threadIdx.x; r < rows; r += blockDim.x) s_rexp[r] = row_exp(g, p0 + r);
@@ -288,11 +301,14 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs g, int NT) 
     a_src = g.A + (size_t)(g.perm ? g.perm[p] / g.k : p) * K + 32 * lh;
   }
   const uint8_t* b_row = nullptr;
+  float b_sc = 1.0f;  // BF16: 2^-(the row's exponent)
   {
     const int b_g = GATED ? (lr >> 7) : 0;
     const int b_n = n0 + (GATED ? (lr & 127) : lr);
-    if (b_n < N)
+    if (b_n < N) {
       b_row = static_cast<const uint8_t*>(b_g ? g.W1 : g.W0) + (int64_t)e * g.expert_stride + (int64_t)b_n * g.row_bytes;
+      if (FMT == EMBER_TYPE_BF16) b_sc = __builtin_ldexpf(1.0f, -w_exp_of(b_g ? g.w_exp1 : g.w_exp0, e, N, b_n));
+    }
   }
 
   u32x4 a_reg[4];
@@ -315,7 +331,10 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs g, int NT) 
     for (int v = 0; v < 4; ++v) *reinterpret_cast<u32x4*>(&As[lr * LDK + 32 * lh + 8 * v]) = a_reg[v];
     uint32_t dq[16];
     if (b_row) {
-      D::decode_half(b_raw, kt, lh, dq);
+      if constexpr (FMT == EMBER_TYPE_BF16)
+        bf16_to_f16_scaled(b_raw, b_sc, dq);
+      else
+        D::decode_half(b_raw, kt, lh, dq);
     } else {
 #pragma unroll
       for (int w = 0; w < 16; ++w) dq[w] = 0u;
@@ -376,6 +395,9 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs g, int NT) 
     for (int jn = 0; jn < WN; ++jn) {
       const int n = n0 + wn * (WN * 32) + 32 * jn + (lane & 31);
       if (n >= N) continue;
+      const int we0 = FMT == EMBER_TYPE_BF16 ? w_exp_of(g.w_exp0, e, N, n) : 0;
+      const int we1 = FMT == EMBER_TYPE_BF16 && GATED ? w_exp_of(g.w_exp1, e, N, n) : 0;
+      const int weh = FMT == EMBER_TYPE_BF16 && GATED && g.w_hexp ? (int)g.w_hexp[e] : 0;
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii)
 #pragma unroll
@@ -385,9 +407,10 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs g, int NT) 
           const size_t o = (size_t)(p0 + m) * N + n;
           const int ex = s_rexp[m];
           if constexpr (GATED) {
-            store_h(g, o, p0 + m, ex, acc[0][i][jn][4 * ii + jj], acc[1][i][jn][4 * ii + jj], n == n0);
+            store_h(g, o, p0 + m, ex, __builtin_ldexpf(acc[0][i][jn][4 * ii + jj], we0),
+                    __builtin_ldexpf(acc[1][i][jn][4 * ii + jj], we1), n == n0, weh);
           } else {
-            g.out_y[o] = unscale_y(acc[0][i][jn][4 * ii + jj], ex);
+            g.out_y[o] = unscale_y(__builtin_ldexpf(acc[0][i][jn][4 * ii + jj], we0), ex);
           }
         }
     }
@@ -926,6 +949,16 @@ __global__ void __launch_bounds__(256) gemm_skinny_kernel(GemmArgs g, int NT) {
                           : nullptr;
     }
 
+  // BF16 on the fp16 path: 2^-(row exponent) per B row
+  float b_sc[G][WN];
+#pragma unroll
+  for (int q = 0; q < G; ++q)
+#pragma unroll
+    for (int j = 0; j < WN; ++j) {
+      const int n = ncol0 + 32 * j + nl;
+      b_sc[q][j] = FMT == EMBER_TYPE_BF16 && !SPLIT && n < N ? __builtin_ldexpf(1.0f, -w_exp_of(q ? g.w_exp1 : g.w_exp0, e, N, n))
+                                                            : 1.0f;
+    }
   u32x4 a_reg[NP][2];
   uint32_t b_raw[G][WN][D::NWH];
   auto fetch = [&](int kt) {
@@ -981,6 +1014,8 @@ __global__ void __launch_bounds__(256) gemm_skinny_kernel(GemmArgs g, int NT) {
         if constexpr (SPLIT) {
 #pragma unroll
           for (int w = 0; w < 16; ++w) bq[q][j][w] = b_raw[q][j][w];
+        } else if constexpr (FMT == EMBER_TYPE_BF16) {
+          bf16_to_f16_scaled(b_raw[q][j], b_sc[q][j], bq[q][j]);
         } else {
           D::decode_half(b_raw[q][j], kt, h, bq[q][j]);
         }
@@ -1022,6 +1057,9 @@ __global__ void __launch_bounds__(256) gemm_skinny_kernel(GemmArgs g, int NT) {
     for (int j = 0; j < WN; ++j) {
       const int n = ncol0 + 32 * j + nl;
       if (n >= N) continue;
+      const int we0 = FMT == EMBER_TYPE_BF16 && !SPLIT ? w_exp_of(g.w_exp0, e, N, n) : 0;
+      const int we1 = FMT == EMBER_TYPE_BF16 && !SPLIT && GATED ? w_exp_of(g.w_exp1, e, N, n) : 0;
+      const int weh = FMT == EMBER_TYPE_BF16 && !SPLIT && GATED && g.w_hexp ? (int)g.w_hexp[e] : 0;
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii)
 #pragma unroll
@@ -1031,9 +1069,10 @@ __global__ void __launch_bounds__(256) gemm_skinny_kernel(GemmArgs g, int NT) {
           const size_t o = (size_t)(p0 + m) * N + n;
           const int ex = s_rexp[m];
           if constexpr (GATED) {
-            store_h(g, o, p0 + m, ex, acc[0][i][j][4 * ii + jj], acc[1][i][j][4 * ii + jj], n == n0);
+            store_h(g, o, p0 + m, ex, __builtin_ldexpf(acc[0][i][j][4 * ii + jj], we0),
+                    __builtin_ldexpf(acc[1][i][j][4 * ii + jj], we1), n == n0, weh);
           } else {
-            g.out_y[o] = unscale_y(acc[0][i][j][4 * ii + jj], ex);
+            g.out_y[o] = unscale_y(__builtin_ldexpf(acc[0][i][j][4 * ii + jj], we0), ex);
           }
         }
     }
@@ -1243,6 +1282,54 @@ int launch_build_tiles(const int32_t* offsets, int E, bool skinny, int32_t* tile
   return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
 }
 
+
+// ---- BF16 row exponents (the prefill pack of a BF16 layer): one wave per row
+__global__ void __launch_bounds__(256) bf16_row_exp_kernel(const uint8_t* __restrict__ W, int64_t rows, int K,
+                                                           int64_t row_bytes, int16_t* __restrict__ out) {
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= rows) return;
+  const uint16_t* row = reinterpret_cast<const uint16_t*>(W + r * row_bytes);
+  float m = 0.0f;
+  for (int i = lane; i < K; i += 64) {
+    const float v = fabsf(bf16_f32(row[i]));
+    if (v <= 3.4e38f) m = fmaxf(m, v);  // finite values only (NaN fails the test)
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+  if (lane == 0) {
+    int ex = 0;
+    if (m > 0.0f) (void)__builtin_frexpf(m, &ex);
+    out[r] = (int16_t)max(-120, min(120, ex));
+  }
+}
+
+// per expert: max over its rows n of gate_exp[n] + up_exp[n] (one block per expert)
+__global__ void __launch_bounds__(256) bf16_pair_max_kernel(const int16_t* __restrict__ ge, const int16_t* __restrict__ ue,
+                                                            int N, int16_t* __restrict__ out) {
+  __shared__ int red[4];
+  const int e = blockIdx.x;
+  int m = -32768;
+  for (int n = threadIdx.x; n < N; n += 256) m = max(m, (int)ge[(int64_t)e * N + n] + (int)ue[(int64_t)e * N + n]);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = max(m, __shfl_xor(m, o, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) out[e] = (int16_t)max(max(red[0], red[1]), max(red[2], red[3]));
+}
+
+int launch_bf16_pair_max(const int16_t* ge, const int16_t* ue, int E, int N, int16_t* out, hipStream_t st) {
+  if (E <= 0 || N <= 0) return EMBER_OK;
+  bf16_pair_max_kernel<<<dim3((unsigned)E), 256, 0, st>>>(ge, ue, N, out);
+  return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
+}
+
+int launch_bf16_row_exps(const void* W, int64_t rows, int K, int64_t row_bytes, int16_t* out, hipStream_t st) {
+  if (rows <= 0) return EMBER_OK;
+  bf16_row_exp_kernel<<<dim3((unsigned)((rows + 3) / 4)), 256, 0, st>>>(static_cast<const uint8_t*>(W), rows, K,
+                                                                         row_bytes, out);
+  return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
+}
 
 // ---- prefill pack: one thread per (tile, row), one pack row each (a one-time copy at weight load)
 template <int FMT>

@@ -180,7 +180,45 @@ struct GemmArgs {
   // way (lo at out_h + h_plane). No range scaling: bf16 has f32's exponent range.
   bool split_bf16;
   int64_t a_plane, h_plane;
+  // BF16 weights on the fp16 path (a prefill pack's row exponents): row n of expert e of W0 (W1) enters
+  // the MFMAs times 2^-w_exp0[e N + n] (2^-w_exp1[...]), which puts its largest magnitude in [0.5, 1),
+  // and the epilogue multiplies that output column by 2^w_exp. Null: unscaled.
+  const int16_t* w_exp0;
+  const int16_t* w_exp1;
+  // ... and per expert the largest w_exp0[n] + w_exp1[n] of its rows: the gated epilogue stores h times
+  // 2^-(2 a_exp + w_hexp[e]) (h_exp includes it), so weights far from 1 keep h within fp16's range
+  const int16_t* w_hexp;
 };
+// The prefill pack of a BF16 layer: per weight row the exponent e (int16) that puts the row's largest
+// finite magnitude in [0.5, 1) (clamped to [-120, 120]; 0 for a row of zeros), for the routed gate [E][d_ff],
+// up [E][d_ff], down [E][d], then per expert the largest gate + up exponent of its rows [E]; then, when the
+// shared expert's stacks are BF16 too, its gate [d_ff_shared], up [d_ff_shared], down [d] and gate + up
+// maximum [1]; each section 256-byte aligned.
+struct Bf16ExpLayout {
+  int64_t gate, up, down, hmax, sgate, sup, sdown, shmax, end;  // byte offsets (-1: no section)
+};
+inline Bf16ExpLayout bf16_exp_layout(int d, int d_ff, int E, int d_ff_shared, bool shared) {
+  auto al = [](int64_t v) { return (v + 255) & ~(int64_t)255; };
+  Bf16ExpLayout p;
+  int64_t o = 0;
+  p.gate = o; o = al(o + (int64_t)E * d_ff * 2);
+  p.up = o; o = al(o + (int64_t)E * d_ff * 2);
+  p.down = o; o = al(o + (int64_t)E * d * 2);
+  p.hmax = o; o = al(o + (int64_t)E * 2);
+  p.sgate = p.sup = p.sdown = p.shmax = -1;
+  if (shared) {
+    p.sgate = o; o = al(o + (int64_t)d_ff_shared * 2);
+    p.sup = o; o = al(o + (int64_t)d_ff_shared * 2);
+    p.sdown = o; o = al(o + (int64_t)d * 2);
+    p.shmax = o; o = al(o + 2);
+  }
+  p.end = o;
+  return p;
+}
+// rows BF16 rows of K elements (row_bytes apart) -> their exponents (Bf16ExpLayout)
+int launch_bf16_row_exps(const void* W, int64_t rows, int K, int64_t row_bytes, int16_t* out, hipStream_t st);
+// out[e] = max over n < N of ge[e N + n] + ue[e N + n], e < E
+int launch_bf16_pair_max(const int16_t* ge, const int16_t* ue, int E, int N, int16_t* out, hipStream_t st);
 // Prefill pack (ember_moe_prefill_pack): tiles of 256 weight rows x 64 columns, one tile contiguous;
 // the gate/up section [E][ceil(d_ff / 128)][d / 64] (each tile: the 128 gate rows of an n-tile, then
 // its 128 up rows), then the down section [E][ceil(d / 256)][d_ff / 64]; rows past a matrix's end

@@ -255,7 +255,8 @@ def scratch_bytes(layer: Layer, T: int) -> int:
 
 
 def prefill_pack_bytes(layer: Layer) -> int:
-    """Bytes of the layer's prefill pack (0: the layer has none — not all-Q8_0, or an invalid descriptor)."""
+    """Bytes of the layer's prefill pack (0: the layer has none — not all-Q8_0, all-Q4_K or all-BF16, or an
+    invalid descriptor)."""
     return int(lib().ember_moe_prefill_pack_bytes(ctypes.byref(layer)))
 
 

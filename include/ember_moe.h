@@ -49,8 +49,9 @@ typedef struct ember_moe_layer {
   const void* gate_shared; int gate_shared_type;
   const void* up_shared;   int up_shared_type;
   const void* down_shared; int down_shared_type;
-  /* Optional (NULL: none): the routed Q8_0 stacks repacked for the prefill MFMA path by
-   * ember_moe_prefill_pack. Appended last, so descriptors that zero-initialise keep working. */
+  /* Optional (NULL: none): the prefill pack ember_moe_prefill_pack prepared for this layer's stacks
+   * (Q8_0 / Q4_K tiles, or BF16 row exponents). Appended last, so descriptors that zero-initialise
+   * keep working. */
   const void* prefill_pack;
   /* Optional (NULL: none; requires d_ff_shared > 0): qwen2moe's shared-expert gate ffn_gate_inp_shexp,
    * f32 [d] on the device. The shared expert's output row of token t is scaled by
@@ -81,15 +82,23 @@ typedef struct ember_moe_routing_view {
 int ember_moe_scratch_routing(const ember_moe_layer* w, int T, ember_moe_routing_view* view);
 
 /* Prefill weight packing (no counterpart in the reference, which dequantizes every stack to F32 at
- * load, weight_management.cpp:486-511). The prefill expert GEMM (T k / E > 96 tokens per expert) reads
- * its weights in 256-row x 64-column tiles; ggml rows give it 68-byte row slices 4 KiB-plus apart. A
- * packed copy stores each tile contiguously (gate/up: the tile's 128 gate and 128 up rows; rows past
- * the end repeat the last), which the GEMM then loads as whole tiles and reads at a bank-conflict-free
- * stride. Same values, same arithmetic: outputs are bit-identical with or without the pack.
- * Only for layers whose gate, up and down stacks are all Q8_0 (d and d_ff multiples of 64); for others
- * ember_moe_prefill_pack_bytes returns 0. The pack is as large as the three stacks (it does not
- * replace them: decode streams the ggml rows). ember_moe_prefill_pack fills a caller-owned, 256-byte
- * aligned device buffer on `stream`; set the descriptor's prefill_pack to it afterwards. */
+ * load, weight_management.cpp:486-511): a one-time preparation of a layer's routed stacks for the
+ * prefill MFMA GEMMs (more than ~1.5-2 tokens per expert), which never replaces the stacks (decode
+ * streams the ggml rows).
+ *   All-Q8_0 layers: each 256-row x 64-column tile contiguous (gate/up: the tile's 128 gate and 128 up
+ *     rows; rows past the end repeat the last), 68-byte rows, as large as the three stacks; the GEMM
+ *     loads whole tiles and reads them at a bank-conflict-free stride. Same values, same arithmetic:
+ *     outputs are bit-identical with or without the pack.
+ *   All-Q4_K layers: the same tiles with 40-byte rows (per 32-element group the fp16 factors d * sc and
+ *     -dmin * m, then the 32 nibble bytes), 1.11x the stacks; they feed the DMA tile GEMMs, which
+ *     without the pack only Q8_0 has.
+ *   All-BF16 layers: per weight row an int16 exponent (its largest magnitude lands in [0.5, 1) once
+ *     scaled by 2^-e) and per expert the largest gate + up sum, also for a BF16 shared expert (a few KB).
+ *     With them the MFMA paths run one fp16 product per weight (rows scaled into fp16's range, the
+ *     epilogues scale back exactly) instead of two bf16 products (hi and lo halves of the activations).
+ * Q8_0 / Q4_K need d and d_ff multiples of 64; for other layers ember_moe_prefill_pack_bytes returns 0.
+ * ember_moe_prefill_pack fills a caller-owned, 256-byte aligned device buffer on `stream`; set the
+ * descriptor's prefill_pack to it afterwards. */
 size_t ember_moe_prefill_pack_bytes(const ember_moe_layer* w);
 int ember_moe_prefill_pack(const ember_moe_layer* w, void* pack, size_t pack_bytes, hipStream_t stream);
 

@@ -109,8 +109,18 @@ def test_prefill_pack_sizes_and_validation():
     L = _layer(d=512, d_ff=704, E=4)
     assert em.prefill_pack_bytes(L) == expect(512, 704, 4)
     assert em.prefill_pack_bytes(_layer(d=4096, d_ff=14336, E=8)) == expect(4096, 14336, 8)
-    # only all-Q8_0 / all-Q4_K layers with whole 64-column tiles have a pack
-    assert em.prefill_pack_bytes(_layer(gate_type=em.BF16, up_type=em.BF16, down_type=em.BF16)) == 0
+    # only all-Q8_0 / all-Q4_K layers with whole 64-column tiles and all-BF16 layers have a pack
+    # all-BF16 layers: int16 row exponents of gate, up [E][d_ff] and down [E][d] and a per-expert maximum
+    # [E], each section 256-byte aligned
+    bf = dict(gate_type=em.BF16, up_type=em.BF16, down_type=em.BF16)
+    al = lambda v: -(-v // 256) * 256
+    routed = 2 * al(8 * 512 * 2) + al(8 * 256 * 2) + al(8 * 2)
+    assert em.prefill_pack_bytes(_layer(d=256, d_ff=512, E=8, **bf)) == routed
+    # ... and the shared expert's rows when its stacks are BF16 too
+    sh = dict(d_ff_shared=384, gate_shared=0x5000, gate_shared_type=em.BF16, up_shared=0x6000,
+              up_shared_type=em.BF16, down_shared=0x7000, down_shared_type=em.BF16)
+    assert em.prefill_pack_bytes(_layer(d=256, d_ff=512, E=8, **bf, **sh)) == (
+        routed + 2 * al(384 * 2) + al(256 * 2) + al(2))
     assert em.prefill_pack_bytes(_layer(down_type=em.BF16)) == 0
     assert em.prefill_pack_bytes(_layer(d=512, d_ff=736)) == 0  # d_ff not a multiple of 64
     # all-Q4_K layers: 40-byte rows (the two groups' fp16 factors and the quarter's nibbles)

@@ -91,7 +91,7 @@ def test_q4_k_pack_with_k_split(gpu):
 def test_pack_rejected_for_other_layers(gpu):
     import torch
 
-    spec = em.LayerSpec(d=256, d_ff=512, E=4, k=2, wtype=em.BF16, seed=2)
+    spec = em.LayerSpec(d=256, d_ff=512, E=4, k=2, wtype=em.F16, seed=2)
     dl = em.DeviceLayer.upload(em.make_host_layer(spec))
     assert em.prefill_pack_bytes(dl.desc) == 0
     buf = torch.empty(1 << 20, dtype=torch.uint8, device="cuda")
@@ -123,3 +123,104 @@ def test_64_token_tiles_forced(gpu, monkeypatch, wtype, d_ff, pack):
         assert rel_l2(y, _run(hl, x, pack=False)) < 1e-5
     monkeypatch.delenv("EMBER_MOE_PATH")
     assert rel_l2(y, run_oracle(hl, x)) < 2e-3
+
+
+# ---- BF16 layers: the pack holds row exponents, and the MFMA paths run fp16 operands (each weight row
+# scaled by 2^-e, e putting its largest magnitude in [0.5, 1); the epilogue multiplies the column by 2^e)
+# instead of the split bf16 MFMA (two products per weight)
+
+def _bf16_scaled(spec, scales):
+    """N(0, 0.02) stacks times a per-expert factor (cycled), as BF16."""
+    s = spec
+    hl = em.make_host_layer(s)
+
+    def stack(name, rows, cols):
+        v = em.normal(s.E * rows * cols, s.seed, 40 + len(name), 0.0, 0.02).reshape(s.E, rows, cols)
+        v = v * np.array([scales[e % len(scales)] for e in range(s.E)], np.float32)[:, None, None]
+        return em.quantize(em.BF16, np.ascontiguousarray(v, np.float32).reshape(-1))
+
+    hl.gate = stack("gate", s.d_ff, s.d)
+    hl.up = stack("up", s.d_ff, s.d)
+    hl.down = stack("down_", s.d, s.d_ff)
+    return hl
+
+
+@pytest.mark.parametrize("T", [40, 600])
+def test_bf16_pack_weights_outside_fp16_range(gpu, T):
+    """Experts of ~1e5 and ~1e-6 weights (outside fp16's normal range) and x ~ N(0, 1e3): the row exponents
+    keep the fp16 operands in range (T = 40: 64-token tiles, T = 600: 256-token tiles)."""
+    spec = em.LayerSpec(d=512, d_ff=768, E=8, k=2, wtype=em.BF16, seed=53)
+    hl = _bf16_scaled(spec, [5e6, 5e-5])
+    x = (em.make_input(spec, T, seed=54) * np.float32(1e3)).astype(np.float32)
+    print(f"bf16 pack range T={T}", flush=True)
+    y = _run(hl, x, pack=True)
+    want = run_oracle(hl, x)
+    assert np.all(np.isfinite(y))
+    assert rel_l2(y, want) < 2e-3
+
+
+@pytest.mark.parametrize("T", [16, 200, 700])
+def test_bf16_pack_with_shared_expert(gpu, T):
+    """A DeepSeek-style BF16 layer (selection bias, shared expert, output scale): routed and shared experts
+    take the fp16 path with the pack's exponents; the split path without the pack agrees at the bar."""
+    spec = em.LayerSpec(d=512, d_ff=384, E=16, k=4, wtype=em.BF16, bias_std=2.0, d_ff_shared=768, out_scale=2.5,
+                        seed=55)
+    hl = em.make_host_layer(spec)
+    # (x scaled by 10, not more: with larger logits the selection bias can pick four experts whose softmax
+    # scores all underflow to 0, and the renormalisation then gives NaN gates, in the reference as here)
+    x = (em.make_input(spec, T, seed=56) * np.float32(10.0)).astype(np.float32)
+    print(f"bf16 pack shared T={T}", flush=True)
+    y = _run(hl, x, pack=True)
+    want = run_oracle(hl, x)
+    assert np.all(np.isfinite(want)) and np.all(np.isfinite(y))
+    assert rel_l2(y, want) < 2e-3
+    assert rel_l2(_run(hl, x, pack=False), want) < 2e-3
+
+
+def test_bf16_row_exponents(gpu):
+    """The pack's exponents against numpy: frexp of each row's largest finite magnitude (0 for a row of
+    zeros or of no finite value), clamped to [-120, 120]; rows holding Inf / NaN, huge, tiny and subnormal
+    values included."""
+    import torch
+
+    spec = em.LayerSpec(d=256, d_ff=256, E=4, k=2, wtype=em.BF16, d_ff_shared=512, seed=57)
+    hl = em.make_host_layer(spec)
+    g = hl.gate.view(np.uint16).reshape(spec.E, spec.d_ff, spec.d).copy()
+    bf = lambda v: (np.array([v], np.float32).view(np.uint32) >> 16).astype(np.uint16)[0]
+    g[0, 0, :] = 0
+    g[0, 1, 7] = bf(np.inf)
+    g[0, 2, :] = bf(np.nan)
+    g[0, 3, 5] = bf(-3e30)
+    g[0, 4, :] = bf(1e-39)  # bf16 subnormal: frexp exponent -129, clamped
+    g[0, 5, 9] = bf(-0.75)
+    g[1, 6, :] = bf(np.float32(2.0 ** -100))
+    hl.gate = g.reshape(-1).view(np.uint8).copy()
+    dl = em.DeviceLayer.upload(hl)
+    n = em.prefill_pack_bytes(dl.desc)
+    buf = torch.zeros(n, dtype=torch.uint8, device="cuda")
+    em.prefill_pack(dl.desc, buf)
+    torch.cuda.synchronize()
+    pack = buf.cpu().numpy()
+
+    def want(u16, rows, cols):
+        v = (u16.astype(np.uint32) << 16).view(np.float32).reshape(rows, cols).astype(np.float64)
+        a = np.where(np.isfinite(v), np.abs(v), 0.0).max(axis=1)
+        return np.clip(np.where(a > 0, np.frexp(a)[1], 0), -120, 120).astype(np.int16)
+
+    al = lambda v: -(-v // 256) * 256
+    E, d, f, fs = spec.E, spec.d, spec.d_ff, spec.d_ff_shared
+    off = 0
+    exps = {}
+    # sections: gate, up, down, per-expert max of gate + up; the shared expert's the same
+    for name, rows, cols, nexp in [("gate", E * f, d, E), ("up", E * f, d, E), ("down", E * d, f, E),
+                                   ("gate_sh", fs, d, 1), ("up_sh", fs, d, 1), ("down_sh", d, fs, 1)]:
+        got = pack[off:off + 2 * rows].view(np.int16)
+        exps[name] = want(getattr(hl, name).view(np.uint16), rows, cols)
+        assert np.array_equal(got, exps[name]), name
+        off += al(2 * rows)
+        if name.startswith("down"):
+            g_, u_ = exps["gate" + name[4:]], exps["up" + name[4:]]
+            hmax = (g_.astype(np.int32) + u_).reshape(nexp, -1).max(axis=1)
+            assert np.array_equal(pack[off:off + 2 * nexp].view(np.int16), hmax), name + " max"
+            off += al(2 * nexp)
+    assert off == n
