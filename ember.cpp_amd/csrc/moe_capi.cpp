@@ -25,9 +25,10 @@ constexpr int kMaxK = 64;   // picks live in a 64-entry LDS array per wave
 enum PathMode { kGemv = 0, kSkinny = 1, kGemm = 2 };
 int path_mode(int type_in, int K_in, int type_out, int K_out, double avg_m, int E, bool packed = false) {
   if (!gemm_supported(type_in, K_in) || !gemm_supported(type_out, K_out)) return kGemv;
-  // tuning override: gemv | skinny | gemm (read per call, so a test can select each kernel)
-  const int forced = [] {
-    const char* v = std::getenv("EMBER_MOE_PATH");
+  // tuning override: gemv | skinny | gemm (read per call, so a test can select each kernel); the shared
+  // expert (E = 1 here) reads EMBER_MOE_SHARED_PATH
+  const int forced = [E] {
+    const char* v = std::getenv(E == 1 ? "EMBER_MOE_SHARED_PATH" : "EMBER_MOE_PATH");
     if (!v) return -1;
     const std::string s(v);
     return s == "gemv" ? kGemv : s == "skinny" ? kSkinny : s == "gemm" ? kGemm : -1;
@@ -59,7 +60,9 @@ int path_mode(int type_in, int K_in, int type_out, int K_out, double avg_m, int 
   } else if (avg_m <= 2.0) {
     return kGemv;
   }
-  if (avg_m <= 96.0) return kSkinny;
+  // (one dense matrix, the shared expert: the 64-token tiles, split over K, up to 1024 rows; C4 shape
+  // T = 512: 139 vs 201 us on the 256-token tiles, T = 2048: 234 vs 208)
+  if (avg_m <= (E == 1 ? 1024.0 : 96.0)) return kSkinny;
   if (type_in == EMBER_TYPE_BF16 && type_out == EMBER_TYPE_BF16 && !packed) return kSkinny;
   return kGemm;
 }
@@ -177,7 +180,9 @@ struct Layout {
   size_t flag;  // the fused routing's flag words (ProjArgs::Route), at a fixed place: offset 0
   size_t logits, idx, gates, offsets, perm, h, y, hs, ys, sg;
   size_t x16, xexp, xb, h16, hexp, hs16, hsexp, tiles, n_tiles;  // MFMA paths
+  size_t shpart;                          // the shared expert's partial gate / up dots (K split)
   int mode, mode_shared;                  // PathMode of the routed experts and of the shared expert
+  int ks_sh_gu, ks_sh_dn;                 // K split of the shared expert's 64-token-tile launches
   RouteLayout r;
   size_t end;
 };
@@ -196,7 +201,6 @@ Layout layout(const ember_moe_layer* w, int T) {
   // y holds kMaxKSplit partial sums per row when an MFMA path splits the down projection's K
   l.y = o; o = align_up(o + slots * w->d * 4 * kMaxKSplit);
   l.hs = o; o = align_up(o + (size_t)T * w->d_ff_shared * 4);
-  l.ys = o; o = align_up(o + (w->d_ff_shared > 0 ? (size_t)T * w->d * 4 : 0));
   l.sg = o; o = align_up(o + (w->shared_gate ? (size_t)T * 4 : 0));
   l.mode = path_mode(w->gate_type, w->d, w->down_type, w->d_ff, (double)T * w->k / w->E, w->E, w->prefill_pack != nullptr);
   const bool pack_bf16 = w->prefill_pack && bf16_stacks(w);  // row exponents, also the shared expert's if BF16
@@ -209,6 +213,17 @@ Layout layout(const ember_moe_layer* w, int T) {
   if (w->d_ff_shared > 0 && l.mode == kGemv && w->gate_shared_type == w->gate_type &&
       w->down_shared_type == w->down_type)
     l.mode_shared = kGemv;
+  // the shared expert's dense launches on 64-token tiles have d_ff_shared / 128 (gate/up) and d / 256
+  // (down) blocks per 64 tokens: split over K until the chip is filled (C4 shape, T = 16: 128 -> 25 us)
+  l.ks_sh_gu = l.ks_sh_dn = 1;
+  if (w->d_ff_shared > 0 && l.mode_shared == kSkinny) {
+    l.ks_sh_gu = gemm_dense_ksplit(true, T, w->d_ff_shared, w->d,
+                                   2 * (int64_t)w->d_ff_shared * row_bytes(w->gate_shared_type, w->d));
+    l.ks_sh_dn = gemm_dense_ksplit(false, T, w->d, w->d_ff_shared,
+                                   (int64_t)w->d * row_bytes(w->down_shared_type, w->d_ff_shared));
+  }
+  l.ys = o; o = align_up(o + (w->d_ff_shared > 0 ? (size_t)l.ks_sh_dn * T * w->d * 4 : 0));
+  l.shpart = o; o = align_up(o + (l.ks_sh_gu > 1 ? (size_t)l.ks_sh_gu * T * 2 * w->d_ff_shared * 4 : 0));
   const size_t tiles = l.mode == kGemm     ? (size_t)gemm_max_tiles(T, w->k, w->E)
                        : l.mode == kSkinny ? (size_t)gemm_skinny_max_tiles(T, w->k, w->E)
                                            : 0;
@@ -614,6 +629,9 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     g.out_h = hs16;
     const bool skinny = l.mode_shared == kSkinny;  // one dense segment of T rows
     const int mt = skinny ? gemm_skinny_max_tiles(T, 1, 0) : gemm_max_tiles(T, 1, 0);
+    g.ksplit = skinny ? l.ks_sh_gu : 1;
+    g.part_h = g.ksplit > 1 ? at<float>(scratch, l.shpart) : nullptr;
+    g.part_rows = T;
     if ((s = skinny ? launch_gemm_skinny(g, true, mt, st) : launch_gemm(g, true, mt, st))) return s;
     g.A = hs16;
     g.a_exp = sp_sh ? nullptr : hsexp;
@@ -630,6 +648,9 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     g.K = w->d_ff_shared;
     g.out_h = nullptr;
     g.out_y = ys;
+    g.ksplit = skinny ? l.ks_sh_dn : 1;
+    g.part_stride = (int64_t)T * d;
+    g.part_h = nullptr;
     if ((s = skinny ? launch_gemm_skinny(g, false, mt, st) : launch_gemm(g, false, mt, st))) return s;
   } else if (shared && !shared_fused) {
     ProjArgs b{};
@@ -654,7 +675,9 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     if ((s = launch_projection(b, st))) return s;
   }
   mark(ev, 6, st);
-  s = launch_combine(y, ksplit, (int64_t)T * k * d, gates, ds.pos, ys, sg, out_scale, T, k, d, out, st);
+  const int ys_parts = shared_mfma && l.mode_shared == kSkinny ? l.ks_sh_dn : 1;
+  s = launch_combine(y, ksplit, (int64_t)T * k * d, gates, ds.pos, ys, ys_parts, (int64_t)T * d, sg, out_scale, T, k,
+                     d, out, st);
   mark(ev, 7, st);
   return s;
 }

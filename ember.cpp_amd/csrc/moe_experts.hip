@@ -949,8 +949,8 @@ bool type_quantizes_activations(int type) { return type == EMBER_TYPE_Q8_0 || ty
 // from 0 (utils.cpp:736, 744-747); then (x * scale) + 0 (the IR's affine, graph_ir.cpp:923, 2727)
 // and + the shared expert's row (graph_ir.cpp:926-928), which qwen2moe first scales by its token's gate
 // sigmoid(s) = 1 / (1 + expf(-s)) of the gate logit s (graph_ir.cpp:704-705; graph_ir_ops.cpp:22, 61).
-// A y row given as nparts K-split partial sums is their sum in ascending part order. One thread per
-// output element.
+// A y row given as nparts K-split partial sums is their sum in ascending part order, and so is a shared
+// row given as s_parts. One thread per output element.
 __device__ inline float y_at(const float* __restrict__ y, int nparts, int64_t part_stride, size_t i) {
   float v = y[i];
   for (int s = 1; s < nparts; ++s) v = v + y[s * part_stride + i];
@@ -958,7 +958,7 @@ __device__ inline float y_at(const float* __restrict__ y, int nparts, int64_t pa
 }
 __global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ y, int nparts, int64_t part_stride,
                                                       const float* __restrict__ gates, const int32_t* __restrict__ pos,
-                                                      const float* __restrict__ y_shared,
+                                                      const float* __restrict__ y_shared, int s_parts, int64_t s_stride,
                                                       const float* __restrict__ sg_logit, float scale, int k, int d,
                                                       float* __restrict__ out) {
   const int t = blockIdx.y;
@@ -972,14 +972,17 @@ __global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ 
     if (p >= 0) acc = acc + g * y_at(y, nparts, part_stride, (size_t)p * d + o);
   }
   if (scale != 1.0f) acc = acc * scale + 0.0f;
-  if (y_shared) acc = acc + (sg_logit ? y_shared[(size_t)t * d + o] * c : y_shared[(size_t)t * d + o]);
+  if (y_shared) {
+    const float v = y_at(y_shared, s_parts, s_stride, (size_t)t * d + o);
+    acc = acc + (sg_logit ? v * c : v);
+  }
   out[(size_t)t * d + o] = acc;
 }
 
 // The same with four consecutive outputs per thread (d % 4 == 0): 16-byte loads of y rows.
 __global__ void __launch_bounds__(256) combine4_kernel(const float* __restrict__ y, int nparts, int64_t part_stride,
                                                        const float* __restrict__ gates, const int32_t* __restrict__ pos,
-                                                       const float* __restrict__ y_shared,
+                                                       const float* __restrict__ y_shared, int s_parts, int64_t s_stride,
                                                        const float* __restrict__ sg_logit, float scale, int k, int d,
                                                        float* __restrict__ out) {
   const int t = blockIdx.y;
@@ -1012,6 +1015,13 @@ __global__ void __launch_bounds__(256) combine4_kernel(const float* __restrict__
   }
   if (y_shared) {
     float4 v = *reinterpret_cast<const float4*>(y_shared + (size_t)t * d + o);
+    for (int s = 1; s < s_parts; ++s) {
+      const float4 w = *reinterpret_cast<const float4*>(y_shared + s * s_stride + (size_t)t * d + o);
+      v.x = v.x + w.x;
+      v.y = v.y + w.y;
+      v.z = v.z + w.z;
+      v.w = v.w + w.w;
+    }
     if (sg_logit) {
       const float c = shared_gate_sigmoid(sg_logit[t]);
       v.x = v.x * c;
@@ -1028,15 +1038,18 @@ __global__ void __launch_bounds__(256) combine4_kernel(const float* __restrict__
 }
 
 int launch_combine(const float* y, int nparts, int64_t part_stride, const float* gates, const int32_t* pos,
-                   const float* y_shared, const float* sg, float scale, int T, int k, int d, float* out, hipStream_t st) {
+                   const float* y_shared, int s_parts, int64_t s_stride, const float* sg, float scale, int T, int k,
+                   int d, float* out, hipStream_t st) {
   if (T <= 0) return EMBER_OK;
   if (d % 4 == 0) {
     dim3 grid((d / 4 + 255) / 256, T);
-    combine4_kernel<<<grid, 256, 0, st>>>(y, nparts, part_stride, gates, pos, y_shared, sg, scale, k, d, out);
+    combine4_kernel<<<grid, 256, 0, st>>>(y, nparts, part_stride, gates, pos, y_shared, s_parts, s_stride, sg, scale,
+                                          k, d, out);
     return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
   }
   dim3 grid((d + 255) / 256, T);
-  combine_kernel<<<grid, 256, 0, st>>>(y, nparts, part_stride, gates, pos, y_shared, sg, scale, k, d, out);
+  combine_kernel<<<grid, 256, 0, st>>>(y, nparts, part_stride, gates, pos, y_shared, s_parts, s_stride, sg, scale, k,
+                                       d, out);
   return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
 }
 

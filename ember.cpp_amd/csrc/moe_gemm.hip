@@ -910,7 +910,10 @@ __global__ void __launch_bounds__(256) gemm_skinny_kernel(GemmArgs g, int NT) {
   constexpr int NP = SPLIT ? 2 : 1;     // A planes
   __shared__ __align__(16) _Float16 As[2][NP][SBM][LDK];
 
-  const int mt = blockIdx.x % g.max_mt, nt = blockIdx.x / g.max_mt;
+  // block -> (m-tile, n-tile, K split part); part ks covers K tiles [kt0, kt0 + nk)
+  const int mt = blockIdx.x % g.max_mt, rest = blockIdx.x / g.max_mt;
+  const int nt = rest % NT, ks = rest / NT;
+  const int KS = g.ksplit < 1 ? 1 : g.ksplit;
   int e = 0, p0 = 0, rows = 0;
   if (g.tiles) {
     if (mt >= *g.n_tiles) return;
@@ -923,8 +926,8 @@ __global__ void __launch_bounds__(256) gemm_skinny_kernel(GemmArgs g, int NT) {
     if (p0 >= g.T) return;
     rows = min(SBM, g.T - p0);
   }
-  (void)NT;
-  const int K = g.K, N = g.N, nk = K / GBK;
+  const int K = g.K, N = g.N, nk_all = K / GBK;
+  const int kt0 = ks * nk_all / KS, nk = (ks + 1) * nk_all / KS - kt0;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int h = lane >> 5, nl = lane & 31;
   const int n0 = nt * BN;
@@ -961,7 +964,8 @@ __global__ void __launch_bounds__(256) gemm_skinny_kernel(GemmArgs g, int NT) {
     }
   u32x4 a_reg[NP][2];
   uint32_t b_raw[G][WN][D::NWH];
-  auto fetch = [&](int kt) {
+  auto fetch = [&](int kl) {  // K tile kt0 + kl
+    const int kt = kt0 + kl;
 #pragma unroll
     for (int pl = 0; pl < NP; ++pl)
 #pragma unroll
@@ -1017,7 +1021,7 @@ __global__ void __launch_bounds__(256) gemm_skinny_kernel(GemmArgs g, int NT) {
         } else if constexpr (FMT == EMBER_TYPE_BF16) {
           bf16_to_f16_scaled(b_raw[q][j], b_sc[q][j], bq[q][j]);
         } else {
-          D::decode_half(b_raw[q][j], kt, h, bq[q][j]);
+          D::decode_half(b_raw[q][j], kt0 + kt, h, bq[q][j]);
         }
       }
     if (kt + 1 < nk) fetch(kt + 1);
@@ -1069,13 +1073,39 @@ __global__ void __launch_bounds__(256) gemm_skinny_kernel(GemmArgs g, int NT) {
           const size_t o = (size_t)(p0 + m) * N + n;
           const int ex = s_rexp[m];
           if constexpr (GATED) {
-            store_h(g, o, p0 + m, ex, __builtin_ldexpf(acc[0][i][j][4 * ii + jj], we0),
-                    __builtin_ldexpf(acc[1][i][j][4 * ii + jj], we1), n == n0, weh);
+            if (KS > 1) {  // raw partial dots; swiglu_parts_kernel finishes the rows
+              float* part = g.part_h + ((size_t)ks * g.part_rows + p0 + m) * 2 * N + n;
+              part[0] = acc[0][i][j][4 * ii + jj];
+              part[N] = acc[1][i][j][4 * ii + jj];
+            } else {
+              store_h(g, o, p0 + m, ex, __builtin_ldexpf(acc[0][i][j][4 * ii + jj], we0),
+                      __builtin_ldexpf(acc[1][i][j][4 * ii + jj], we1), n == n0, weh);
+            }
           } else {
-            g.out_y[o] = unscale_y(__builtin_ldexpf(acc[0][i][j][4 * ii + jj], we0), ex);
+            g.out_y[ks * g.part_stride + o] = unscale_y(__builtin_ldexpf(acc[0][i][j][4 * ii + jj], we0), ex);
           }
         }
     }
+}
+
+// The gated projection split over K (dense rows, GemmArgs::part_h): h[p][n] from the KS partial gate and
+// up dots summed in ascending part order, then the skinny epilogue's scaling and SwiGLU. One thread per
+// (row, column).
+__global__ void __launch_bounds__(256) swiglu_parts_kernel(GemmArgs g, int rows, int KS) {
+  const int N = g.N;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)rows * N) return;
+  const int p = (int)(i / N), n = (int)(i % N);
+  const float* part = g.part_h + (size_t)p * 2 * N + n;
+  const size_t stride = (size_t)g.part_rows * 2 * N;
+  float ga = part[0], ua = part[N];
+  for (int s = 1; s < KS; ++s) {
+    ga = ga + part[s * stride];
+    ua = ua + part[s * stride + N];
+  }
+  const int we0 = w_exp_of(g.w_exp0, 0, N, n), we1 = w_exp_of(g.w_exp1, 0, N, n);
+  const int weh = g.w_hexp ? (int)g.w_hexp[0] : 0;
+  store_h(g, (size_t)p * N + n, p, row_exp(g, p), __builtin_ldexpf(ga, we0), __builtin_ldexpf(ua, we1), n == 0, weh);
 }
 
 // EMBER_GEMM_DMA=0 routes Q8_0 to the register-staged kernels (a debugging switch); they have no K split
@@ -1172,14 +1202,24 @@ int launch_skinny_fmt(GemmArgs g, int max_mtiles, hipStream_t st) {
       gemm_dma64_q8_kernel<GATED, kWfQ8Rows><<<blocks, kD64Threads, kD64Lds, st>>>(g, NT);
     return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
   }
+  // K split: plain projections into out_y parts; gated ones (dense rows only) into part_h, then finished
+  if (g.ksplit < 1 || (GATED && (g.tiles || !g.part_h))) g.ksplit = 1;
+  const unsigned blocks = (unsigned)(max_mtiles * NT * g.ksplit);
+  bool launched = false;
   if constexpr (FMT == EMBER_TYPE_BF16) {
     if (g.split_bf16) {
-      gemm_skinny_kernel<FMT, GATED, true><<<(unsigned)(max_mtiles * NT), 256, 0, st>>>(g, NT);
-      return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
+      gemm_skinny_kernel<FMT, GATED, true><<<blocks, 256, 0, st>>>(g, NT);
+      launched = true;
     }
   }
-  gemm_skinny_kernel<FMT, GATED><<<(unsigned)(max_mtiles * NT), 256, 0, st>>>(g, NT);
-  return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
+  if (!launched) gemm_skinny_kernel<FMT, GATED><<<blocks, 256, 0, st>>>(g, NT);
+  if (hipGetLastError() != hipSuccess) return EMBER_ERR_LAUNCH;
+  if (GATED && g.ksplit > 1) {
+    const int64_t n = (int64_t)g.T * g.N;
+    swiglu_parts_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(g, g.T, g.ksplit);
+    if (hipGetLastError() != hipSuccess) return EMBER_ERR_LAUNCH;
+  }
+  return EMBER_OK;
 }
 
 template <bool GATED>
@@ -1197,6 +1237,16 @@ int launch_gemm_skinny(const GemmArgs& g, bool gated, int max_mtiles, hipStream_
   return gated ? launch_skinny_t<true>(g, max_mtiles, st) : launch_skinny_t<false>(g, max_mtiles, st);
 }
 
+int gemm_dense_ksplit(bool gated, int T, int N, int K, int64_t weight_bytes) {
+  const int mt = (T + SBM - 1) / SBM, nt = (N + (gated ? 127 : 255)) / (gated ? 128 : 256), nk = K / GBK;
+  const int64_t part_row = (int64_t)T * N * 4 * (gated ? 2 : 1);  // bytes of one part
+  int ks = 1;
+  while (2 * ks <= kMaxDenseKSplit && (int64_t)mt * nt * ks < 512 && nk / (2 * ks) >= 2 &&
+         2 * ks * part_row <= weight_bytes)
+    ks *= 2;
+  return ks;
+}
+
 int gemm_skinny_max_tiles(int T, int k, int E) { return (T * k + SBM - 1) / SBM + std::min(E, T * k); }
 
 int gemm_ksplit(int type, bool packed, int T, int k, int E, int N, int K) {
@@ -1210,7 +1260,8 @@ int gemm_ksplit(int type, bool packed, int T, int k, int E, int N, int K) {
 }
 
 int gemm_skinny_ksplit(int type, bool packed, int max_mtiles, int N, int K) {
-  if (!dma_path(type, packed)) return 1;  // the split lives in the DMA kernels
+  (void)type;
+  (void)packed;
   const int blocks = max_mtiles * ((N + 255) / 256);
   int ks = 1;
   while (ks < kMaxKSplit && blocks * ks < 512 && K / GBK >= 16 * ks * 2) ks *= 2;

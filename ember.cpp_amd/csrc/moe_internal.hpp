@@ -188,6 +188,10 @@ struct GemmArgs {
   // ... and per expert the largest w_exp0[n] + w_exp1[n] of its rows: the gated epilogue stores h times
   // 2^-(2 a_exp + w_hexp[e]) (h_exp includes it), so weights far from 1 keep h within fp16's range
   const int16_t* w_hexp;
+  // gated projections of dense rows split over K (64-token tiles): raw partial gate / up dots of part s at
+  // part_h + (s * part_rows + p) * 2N (+ N for up), finished by a SwiGLU pass
+  float* part_h;
+  int part_rows;
 };
 // The prefill pack of a BF16 layer: per weight row the exponent e (int16) that puts the row's largest
 // finite magnitude in [0.5, 1) (clamped to [-120, 120]; 0 for a row of zeros), for the routed gate [E][d_ff],
@@ -266,13 +270,18 @@ int gemm_skinny_max_tiles(int T, int k, int E);
 // blocks for the chip when the output is narrow
 constexpr int kMaxKSplit = 4;
 int gemm_skinny_ksplit(int type, bool packed, int max_mtiles, int N, int K);
+// ... and of a dense projection (the shared expert's T rows) on the 64-token tiles, gated or plain: up to
+// kMaxDenseKSplit parts, until the launch has 512 blocks, each part keeps >= 2 K tiles and the partial
+// sums (f32) stay within the weights' bytes
+constexpr int kMaxDenseKSplit = 16;
+int gemm_dense_ksplit(bool gated, int T, int N, int K, int64_t weight_bytes);
 // ... and of the 256-token-tile path's (the down launch of a long prefill has few blocks per n-tile row)
 int gemm_ksplit(int type, bool packed, int T, int k, int E, int N, int K);
 // Whether the DMA tile kernels serve stacks of `type` (packed: with a prefill pack): Q8_0, packed Q4_K.
 bool dma_path(int type, bool packed);
 
 int launch_combine(const float* y, int nparts, int64_t part_stride, const float* gates, const int32_t* pos,
-                   const float* y_shared, const float* shared_gate_logit, float scale, int T,
+                   const float* y_shared, int s_parts, int64_t s_stride, const float* shared_gate_logit, float scale, int T,
                    int k, int d, float* out, hipStream_t st);
 
 }  // namespace ember_moe

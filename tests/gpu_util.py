@@ -12,11 +12,16 @@ def rel_l2(a, b) -> float:
     return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
 
 
-def run_gpu(hl: em.HostLayer, x: np.ndarray):
-    """Uploads the layer and x, runs ember_moe_ffn, returns out as numpy."""
+def run_gpu(hl: em.HostLayer, x: np.ndarray, pack: bool = False):
+    """Uploads the layer and x (pack: with the layer's prefill pack), runs ember_moe_ffn, returns out as
+    numpy."""
     import torch
 
     dl = em.DeviceLayer.upload(hl)
+    if pack:
+        buf = torch.empty(em.prefill_pack_bytes(dl.desc), dtype=torch.uint8, device="cuda")
+        em.prefill_pack(dl.desc, buf)
+        dl.tensors["pack"] = buf
     xd = torch.from_numpy(np.ascontiguousarray(x, np.float32)).cuda()
     out, _ = dl.forward(xd)
     torch.cuda.synchronize()

@@ -14,11 +14,12 @@ pytestmark = pytest.mark.gpu
 F32_MAXABS, F32_RELL2, Q_RELL2 = 1e-4, 1e-5, 2e-3
 
 
-def check(spec, T, seed=None):
+def check(spec, T, seed=None, pack=False):
     hl = em.make_host_layer(spec)
     x = em.make_input(spec, T, seed)
-    print(f"layer {em.TYPE_NAMES[spec.wtype]} d={spec.d} d_ff={spec.d_ff} E={spec.E} k={spec.k} T={T}", flush=True)
-    y = run_gpu(hl, x)
+    print(f"layer {em.TYPE_NAMES[spec.wtype]} d={spec.d} d_ff={spec.d_ff} E={spec.E} k={spec.k} T={T} pack={pack}",
+          flush=True)
+    y = run_gpu(hl, x, pack=pack)
     want = run_oracle(hl, x)
     assert np.all(np.isfinite(y))
     if spec.wtype == em.F32 and (spec.d_ff_shared == 0 or spec.shared_type in (None, em.F32)):
@@ -142,6 +143,19 @@ def test_shared_expert_multi_token_gemv(gpu, monkeypatch, shape, T, forced):
         spec = em.LayerSpec(d=1024, d_ff=768, E=16, k=4, wtype=em.BF16, d_ff_shared=1536, shared_type=em.Q8_0,
                             seed=23)
     check(spec, T, seed=300 + T)
+
+
+@pytest.mark.parametrize("T", [16, 100, 300])
+@pytest.mark.parametrize("wtype,shared_type,pack,gated", [(em.BF16, None, True, False), (em.BF16, None, False, False),
+                                                          (em.Q8_0, em.BF16, True, False), (em.F16, None, False, False),
+                                                          (em.Q8_0, None, False, True)])
+def test_shared_expert_k_split(gpu, wtype, shared_type, pack, gated, T):
+    """The shared expert's dense launches on 64-token tiles split over K when they have few blocks (at this
+    shape 8 parts at T = 16, 2 at T = 100, none at T = 300): raw partial gate / up dots finished by a SwiGLU
+    pass, down partials summed by the combine in part order; BF16 with the pack (fp16) and without (split
+    bf16), a Q8_0 shared expert (its DMA kernel splits only down), qwen2moe's gated shared expert."""
+    check(em.LayerSpec(d=1024, d_ff=512, E=16, k=4, wtype=wtype, d_ff_shared=1024, shared_type=shared_type,
+                       shared_gated=gated, renorm=not gated, seed=61), T, pack=pack)
 
 
 @pytest.mark.parametrize("wtype,T", [(em.BF16, 1), (em.BF16, 3), (em.BF16, 40), (em.BF16, 300), (em.Q8_0, 1),
