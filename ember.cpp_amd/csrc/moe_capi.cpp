@@ -259,6 +259,8 @@ DispatchScratch dispatch_scratch(void* scratch, const RouteLayout& r, int32_t* o
   ds.n_used = at<int32_t>(scratch, r.n_used);
   ds.perm = perm;
   ds.pos = at<int32_t>(scratch, r.pos);
+  ds.tiles = ds.n_tiles = nullptr;
+  ds.tile_bm = 0;
   return ds;
 }
 
@@ -350,7 +352,12 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
   float* gates = at<float>(scratch, l.gates);
   int32_t* offsets = at<int32_t>(scratch, l.offsets);
   int32_t* perm = at<int32_t>(scratch, l.perm);
-  const DispatchScratch ds = dispatch_scratch(scratch, l.r, offsets, perm);
+  DispatchScratch ds = dispatch_scratch(scratch, l.r, offsets, perm);
+  if (l.mode != kGemv) {  // the dispatch also writes the MFMA GEMMs' tile table
+    ds.tiles = at<int32_t>(scratch, l.tiles);
+    ds.n_tiles = at<int32_t>(scratch, l.n_tiles);
+    ds.tile_bm = gemm_tile_rows(l.mode == kSkinny);
+  }
   float* h = at<float>(scratch, l.h);
   float* y = at<float>(scratch, l.y);
   int ksplit = 1;  // partial sums per y row (K split of the down projection)
@@ -364,16 +371,6 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
   // (the router blocks are one per expert and must fit the device's CUs: fewer CUs than experts take the
   // unfused launches)
   const bool fuse_route = fuse_ok && l.mode == kGemv && T == 1 && fused_route_fits(w->gate_type, d, E, k) && E <= device_cus();
-  auto* flag = at<unsigned long long>(scratch, l.flag);
-  mark(ev, 0, st);
-  if (!fuse_route && (s = launch_router_logits(x, T, d, E, w->router, logits, st))) return s;
-  mark(ev, 1, st);
-  if (!fuse_route && (s = launch_route_dispatch(logits, T, E, k, renorm, routed, sigmoid, w->selection_bias, groups_n,
-                                                groups_top, idx, gates, ds, st)))
-    return s;
-  mark(ev, 2, st);
-  mark(ev, 3, st);
-
   const bool shared = w->d_ff_shared > 0;
   const bool shared_mfma = shared && l.mode_shared != kGemv;
   const float out_scale = w->out_scale == 0.0f ? 1.0f : w->out_scale;
@@ -393,10 +390,28 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
   _Float16* x16 = at<_Float16>(scratch, l.x16);
   int32_t* xexp = at<int32_t>(scratch, l.xexp);
   uint16_t* xb = at<uint16_t>(scratch, l.xb);
-  if ((l.mode != kGemv && !sp) || (shared_mfma && !sp_sh))
-    if ((s = launch_to_f16_rows(x, T, d, x16, xexp, st))) return s;
-  if ((l.mode != kGemv && sp) || (shared_mfma && sp_sh))
-    if ((s = launch_to_bf16x2(x, (int64_t)T * d, xb, (int64_t)T * d, st))) return s;
+  // the MFMA paths' activations, converted by extra blocks of the routing launch (or on their own when the
+  // routing is fused into the decode launch)
+  ActConv conv{};
+  conv.x = x;
+  conv.rows = T;
+  conv.K = d;
+  conv.y16 = (l.mode != kGemv && !sp) || (shared_mfma && !sp_sh) ? x16 : nullptr;
+  conv.yexp = xexp;
+  conv.yb = (l.mode != kGemv && sp) || (shared_mfma && sp_sh) ? xb : nullptr;
+  conv.plane = (int64_t)T * d;
+  const bool need_conv = conv.y16 || conv.yb;
+  auto* flag = at<unsigned long long>(scratch, l.flag);
+  mark(ev, 0, st);
+  if (!fuse_route && (s = launch_router_logits(x, T, d, E, w->router, logits, st))) return s;
+  mark(ev, 1, st);
+  if (!fuse_route && (s = launch_route_dispatch(logits, T, E, k, renorm, routed, sigmoid, w->selection_bias, groups_n,
+                                                groups_top, idx, gates, ds, need_conv ? &conv : nullptr, st)))
+    return s;
+  if (fuse_route && need_conv && (s = launch_act_conv(conv, st))) return s;
+  mark(ev, 2, st);
+  mark(ev, 3, st);
+
   float* ys = shared ? at<float>(scratch, l.ys) : nullptr;
   float* hs = at<float>(scratch, l.hs);
   // one token on the decode path: the down launch also forms the output rows (combine fused in)
@@ -415,9 +430,8 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     auto gemm = [&](const GemmArgs& g, bool gated, int mt) {
       return skinny ? launch_gemm_skinny(g, gated, mt, st) : launch_gemm(g, gated, mt, st);
     };
-    int32_t* tiles = at<int32_t>(scratch, l.tiles);
-    int32_t* n_tiles = at<int32_t>(scratch, l.n_tiles);
-    if ((s = launch_build_tiles(offsets, E, skinny, tiles, n_tiles, st))) return s;
+    int32_t* tiles = ds.tiles;
+    int32_t* n_tiles = ds.n_tiles;
     _Float16* h16 = at<_Float16>(scratch, l.h16);
     int32_t* hexp = at<int32_t>(scratch, l.hexp);
     GemmArgs g{};
@@ -842,7 +856,7 @@ int ember_moe_route(const float* logits, int T, int E, int k, int renorm, int sc
   const bool routed = scoring == EMBER_SCORE_SIGMOID || selection_bias || groups_n > 1;
   return launch_route_dispatch(logits, T, E, k, renorm ? 1 : 0, routed ? 1 : 0, scoring == EMBER_SCORE_SIGMOID ? 1 : 0,
                                selection_bias, groups_n, groups_top, idx, gates,
-                               dispatch_scratch(scratch, r, offsets, perm), st);
+                               dispatch_scratch(scratch, r, offsets, perm), nullptr, st);
 }
 
 }  // extern "C"

@@ -20,7 +20,7 @@
 #include <cstdlib>
 #include <type_traits>
 
-#include "moe_internal.hpp"
+#include "moe_conv.hpp"
 
 namespace ember_moe {
 using namespace ember_math;
@@ -212,12 +212,6 @@ __device__ inline float swiglu_g(float g, float u) { return g * __frcp_rn(1.0f +
 __device__ inline int row_exp(const GemmArgs& g, int p) {
   return g.a_exp ? g.a_exp[g.perm ? g.perm[p] / g.k : p] : 0;
 }
-__device__ inline uint16_t bf16_rne(float v) {
-  const uint32_t u = __builtin_bit_cast(uint32_t, v);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // NaN stays NaN
-  return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
-}
-__device__ inline float bf16_f32(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
 // h[p][n] = SwiGLU of the unscaled gate and up dots, stored in the A format of the down projection; the
 // fp16 form is h times 2^-(2 e + eh), eh the expert's weight-range exponent (GemmArgs::w_hexp)
 __device__ inline void store_h(const GemmArgs& g, size_t o, int p, int e, float ga, float ua, bool first_col,
@@ -1268,70 +1262,19 @@ int gemm_skinny_ksplit(int type, bool packed, int max_mtiles, int N, int K) {
   return ks;
 }
 
-// x [rows][K] -> fp16 rows scaled by 2^-e, e chosen per row so that its largest magnitude m lands in
-// [0.5, 1) (frexp's exponent; 0 for an all-zero or non-finite row). One block per row.
-__global__ void __launch_bounds__(256) to_f16_rows_kernel(const float* __restrict__ x, int K, _Float16* __restrict__ y,
-                                                          int32_t* __restrict__ row_exp) {
-  __shared__ float red[4];
-  const float* xr = x + (size_t)blockIdx.x * K;
-  float m = 0.0f;
-  for (int i = threadIdx.x; i < K; i += 256) m = fmaxf(m, fabsf(xr[i]));
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
-  __syncthreads();
-  m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  int e = 0;
-  if (m > 0.0f && m <= 3.4028235e38f) (void)__builtin_frexpf(m, &e);
-  if (threadIdx.x == 0) row_exp[blockIdx.x] = e;
-  _Float16* yr = y + (size_t)blockIdx.x * K;
-  for (int i = threadIdx.x; i < K; i += 256) yr[i] = (_Float16)__builtin_ldexpf(xr[i], -e);
-}
+// The activation conversion on its own (act_conv_row): one block per row.
+__global__ void __launch_bounds__(256) act_conv_kernel(ActConv c) { act_conv_row(c, blockIdx.x); }
 
-int launch_to_f16_rows(const float* x, int rows, int K, _Float16* y, int32_t* row_exp, hipStream_t st) {
-  if (rows <= 0) return EMBER_OK;
-  to_f16_rows_kernel<<<(unsigned)rows, 256, 0, st>>>(x, K, y, row_exp);
-  return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
-}
-
-// x -> bf16 hi = RNE(x) and lo = RNE(x - hi) planes (x - hi is exact in f32).
-__global__ void __launch_bounds__(256) to_bf16x2_kernel(const float* __restrict__ x, int64_t n, uint16_t* __restrict__ y,
-                                                        int64_t plane) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  const float v = x[i];
-  const uint16_t hi = bf16_rne(v);
-  y[i] = hi;
-  y[plane + i] = bf16_rne(v - bf16_f32(hi));
-}
-
-int launch_to_bf16x2(const float* x, int64_t n, uint16_t* y, int64_t plane, hipStream_t st) {
-  if (n <= 0) return EMBER_OK;
-  to_bf16x2_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(x, n, y, plane);
+int launch_act_conv(const ActConv& c, hipStream_t st) {
+  if (c.rows <= 0 || (!c.y16 && !c.yb)) return EMBER_OK;
+  act_conv_kernel<<<(unsigned)c.rows, 256, 0, st>>>(c);
   return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
 }
 
 // Tile table for the grouped GEMMs: (expert, first token) of every bm-token tile of every expert
 // segment with tokens, ascending by expert. One thread; E entries of offsets.
-__global__ void build_tiles_kernel(const int32_t* __restrict__ offsets, int E, int bm, int32_t* __restrict__ tiles,
-                                   int32_t* __restrict__ n_tiles) {
-  if (threadIdx.x != 0 || blockIdx.x != 0) return;
-  int n = 0;
-  for (int e = 0; e < E; ++e) {
-    const int cnt = offsets[e + 1] - offsets[e];
-    for (int m0 = 0; m0 < cnt; m0 += bm) {
-      tiles[2 * n] = e;
-      tiles[2 * n + 1] = m0;
-      ++n;
-    }
-  }
-  *n_tiles = n;
-}
 
-int launch_build_tiles(const int32_t* offsets, int E, bool skinny, int32_t* tiles, int32_t* n_tiles, hipStream_t st) {
-  build_tiles_kernel<<<1, 64, 0, st>>>(offsets, E, skinny ? SBM : GBM, tiles, n_tiles);
-  return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
-}
+int gemm_tile_rows(bool skinny) { return skinny ? SBM : GBM; }
 
 
 // ---- BF16 row exponents (the prefill pack of a BF16 layer): one wave per row

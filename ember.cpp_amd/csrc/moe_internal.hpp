@@ -29,6 +29,18 @@ __device__ inline void copy16_to_lds(void* dst, const void* src, int n) {
 }
 
 // Device buffers of the dispatch step, carved from the caller's scratch.
+// Activation conversion for the MFMA paths (act_conv_row): x [rows][K] f32 into fp16 rows scaled by 2^-e
+// (y16, e in yexp; null: not needed) and / or split bf16 planes (yb, lo plane `plane` elements on; null:
+// not needed).
+struct ActConv {
+  const float* x;
+  int rows, K;
+  _Float16* y16;
+  int32_t* yexp;
+  uint16_t* yb;
+  int64_t plane;
+};
+
 struct DispatchScratch {
   int32_t* rank;       // [T*k] rank of each slot among equal experts in its 64-slot chunk
   int32_t* chunk_cnt;  // [ceil(T*k/64)][E] counts, then per-chunk base positions
@@ -37,16 +49,22 @@ struct DispatchScratch {
   int32_t* n_used;     // [1]
   int32_t* perm;       // [T*k] sorted position -> slot t*k+j
   int32_t* pos;        // [T*k] slot -> sorted position (-1: no pick)
+  // optional (null: none): the MFMA GEMMs' tile table, written by the dispatch's last step: tiles of
+  // tile_bm rows over each expert's segment, experts ascending, as (expert, first row) pairs
+  int32_t* tiles;
+  int32_t* n_tiles;
+  int tile_bm;
 };
 
 int launch_router_logits(const float* x, int T, int d, int E, const float* R, float* logits, hipStream_t st);
+// conv (nullable): activation conversion run by extra blocks of the same launch
 int launch_route(const float* logits, int T, int E, int k, int renorm, int routed, int sigmoid, const float* bias,
-                 int groups_n, int groups_top, int32_t* idx, float* gates, hipStream_t st);
+                 int groups_n, int groups_top, int32_t* idx, float* gates, const ActConv* conv, hipStream_t st);
 int launch_dispatch(const int32_t* idx, int T, int k, int E, const DispatchScratch& ds, hipStream_t st);
 // Routing + dispatch; one fused kernel for decode-sized batches, else launch_route + launch_dispatch.
 int launch_route_dispatch(const float* logits, int T, int E, int k, int renorm, int routed, int sigmoid,
                           const float* bias, int groups_n, int groups_top, int32_t* idx, float* gates,
-                          const DispatchScratch& ds, hipStream_t st);
+                          const DispatchScratch& ds, const ActConv* conv, hipStream_t st);
 
 bool type_quantizes_activations(int type);
 // Compute units of the current device (0 on error); cached per device.
@@ -257,12 +275,10 @@ int launch_prefill_pack(int type, const void* W0, const void* W1, int64_t expert
 bool gemm_supported(int type, int K);
 int gemm_max_tiles(int T, int k, int E);
 int launch_gemm(const GemmArgs& g, bool gated, int max_mtiles, hipStream_t st);
-// x [rows][K] f32 -> fp16 rows scaled by 2^-e (e per row: the row's largest magnitude lands in
-// [0.5, 1)), e -> row_exp[row] (GemmArgs::a_exp).
-int launch_to_f16_rows(const float* x, int rows, int K, _Float16* y, int32_t* row_exp, hipStream_t st);
-// x (f32, n elements) -> bf16 hi plane y[0..n) and lo plane y[plane..plane+n) (GemmArgs::split_bf16).
-int launch_to_bf16x2(const float* x, int64_t n, uint16_t* y, int64_t plane, hipStream_t st);
-int launch_build_tiles(const int32_t* offsets, int E, bool skinny, int32_t* tiles, int32_t* n_tiles, hipStream_t st);
+// The activation conversion (ActConv) as a launch of its own: one block per row.
+int launch_act_conv(const ActConv& c, hipStream_t st);
+// rows per tile of the MFMA GEMMs' tile table (DispatchScratch::tile_bm): 64-token or 256-token tiles
+int gemm_tile_rows(bool skinny);
 // Skinny variant for segments of a few dozen tokens (64-token tiles).
 int launch_gemm_skinny(const GemmArgs& g, bool gated, int max_mtiles, hipStream_t st);
 int gemm_skinny_max_tiles(int T, int k, int E);

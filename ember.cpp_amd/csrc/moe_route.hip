@@ -10,6 +10,7 @@
 //    (moe_math.hpp); the DeepSeek-style router runs the reference's float algorithm serially.
 // The dispatch permutation has no reference counterpart: slots s = t*k + j are stably sorted by
 // expert id (offsets[E+1], perm[p] = s, pos[s] = p), built without atomics on global memory.
+#include "moe_conv.hpp"
 #include "moe_route_dev.hpp"
 
 namespace ember_moe {
@@ -247,8 +248,13 @@ __global__ void __launch_bounds__(256) router_logits_tiled(const float* __restri
 __global__ void __launch_bounds__(256) route_kernel(const float* __restrict__ logits, int T, int E, int k, int renorm,
                                                     int routed, int sigmoid, const float* __restrict__ bias,
                                                     int groups_n, int groups_top, int32_t* __restrict__ idx,
-                                                    float* __restrict__ gates) {
+                                                    float* __restrict__ gates, ActConv conv) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
+  const int nroute = (T + 3) / 4;  // blocks past these convert activations (act_conv_row)
+  if ((int)blockIdx.x >= nroute) {
+    act_conv_row(conv, blockIdx.x - nroute);
+    return;
+  }
   const int wave = threadIdx.x >> 6;
   const int t = blockIdx.x * 4 + wave;
   if (t >= T) return;
@@ -300,8 +306,10 @@ __global__ void __launch_bounds__(kChunk) dispatch_count(const int32_t* __restri
 // One block of 1024 threads (E <= 1024): offsets[E+1], used[] / n_used, and chunk_cnt overwritten with
 // each chunk's base position per expert.
 __global__ void __launch_bounds__(1024) dispatch_scan(int32_t* __restrict__ chunk_cnt, int nchunks, int E,
-                                                      int32_t* __restrict__ offsets, int32_t* __restrict__ used,
-                                                      int32_t* __restrict__ n_used) {
+                                                      DispatchScratch ds) {
+  int32_t* __restrict__ offsets = ds.offsets;
+  int32_t* __restrict__ used = ds.used;
+  int32_t* __restrict__ n_used = ds.n_used;
   __shared__ int tmp[16];
   const int e = threadIdx.x;
   int tot = 0;
@@ -324,6 +332,7 @@ __global__ void __launch_bounds__(1024) dispatch_scan(int32_t* __restrict__ chun
     offsets[E] = all;
     *n_used = nu;
   }
+  write_tiles(e, E, tot, ds, tmp);
 }
 
 __global__ void __launch_bounds__(256) dispatch_scatter(const int32_t* __restrict__ idx, int nslots, int E,
@@ -349,9 +358,12 @@ __global__ void __launch_bounds__(256) dispatch_scatter(const int32_t* __restric
 // three-kernel sort, so only single-chunk dispatches take it.
 constexpr int kOneBlockChunks = 1, kOneBlockE = 256;
 __global__ void __launch_bounds__(kChunk) dispatch_one_block(const int32_t* __restrict__ idx, int nslots, int E,
-                                                             int32_t* __restrict__ offsets, int32_t* __restrict__ used,
-                                                             int32_t* __restrict__ n_used, int32_t* __restrict__ perm,
-                                                             int32_t* __restrict__ pos) {
+                                                             DispatchScratch ds) {
+  int32_t* __restrict__ offsets = ds.offsets;
+  int32_t* __restrict__ used = ds.used;
+  int32_t* __restrict__ n_used = ds.n_used;
+  int32_t* __restrict__ perm = ds.perm;
+  int32_t* __restrict__ pos = ds.pos;
   __shared__ int wcnt[16 * kOneBlockE];
   __shared__ int ccnt[kOneBlockChunks * kOneBlockE];
   __shared__ int tmp[16];
@@ -412,6 +424,7 @@ __global__ void __launch_bounds__(kChunk) dispatch_one_block(const int32_t* __re
     offsets[E] = all;
     *n_used = nu;
   }
+  write_tiles(e, E, tot, ds, tmp);
   __syncthreads();
 #pragma unroll
   for (int c = 0; c < kOneBlockChunks; ++c) {
@@ -436,8 +449,13 @@ __global__ void __launch_bounds__(512) route_dispatch_small(const float* __restr
                                                             int renorm, int routed, int sigmoid,
                                                             const float* __restrict__ bias, int groups_n,
                                                             int groups_top, int32_t* __restrict__ idx,
-                                                            float* __restrict__ gates, DispatchScratch ds) {
+                                                            float* __restrict__ gates, DispatchScratch ds,
+                                                            ActConv conv) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
+  if (blockIdx.x > 0) {  // blocks past the first convert activations (act_conv_row)
+    act_conv_row(conv, blockIdx.x - 1);
+    return;
+  }
   const int wave = threadIdx.x >> 6;
   const size_t wl = route_wave_lds(E);
   int* sidx = reinterpret_cast<int*>(lds_raw + kSmallT * wl);
@@ -470,6 +488,7 @@ __global__ void __launch_bounds__(512) route_dispatch_small(const float* __restr
       if (c > 0) ds.used[upos] = q;
     }
     __syncthreads();
+    write_tiles(q, E, c, ds, cnt + E);
     if (q < E) cnt[q] = off;
     if (q == 0) {
       ds.offsets[E] = all;
@@ -658,11 +677,12 @@ int launch_router_logits(const float* x, int T, int d, int E, const float* R, fl
 }
 
 int launch_route(const float* logits, int T, int E, int k, int renorm, int routed, int sigmoid, const float* bias,
-                 int groups_n, int groups_top, int32_t* idx, float* gates, hipStream_t st) {
+                 int groups_n, int groups_top, int32_t* idx, float* gates, const ActConv* conv, hipStream_t st) {
   if (T <= 0) return EMBER_OK;
   const size_t lds = 4 * route_wave_lds(E);
-  route_kernel<<<(T + 3) / 4, 256, lds, st>>>(logits, T, E, k, renorm, routed, sigmoid, bias, groups_n, groups_top, idx,
-                                              gates);
+  const ActConv c = conv ? *conv : ActConv{};
+  route_kernel<<<(T + 3) / 4 + c.rows, 256, lds, st>>>(logits, T, E, k, renorm, routed, sigmoid, bias, groups_n,
+                                                       groups_top, idx, gates, c);
   return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
 }
 
@@ -670,10 +690,10 @@ bool route_dispatch_fused(int T, int E, int k) { return T <= kSmallT && T * k <=
 
 int launch_route_dispatch(const float* logits, int T, int E, int k, int renorm, int routed, int sigmoid,
                           const float* bias, int groups_n, int groups_top, int32_t* idx, float* gates,
-                          const DispatchScratch& ds, hipStream_t st) {
+                          const DispatchScratch& ds, const ActConv* conv, hipStream_t st) {
   if (T <= 0) return EMBER_OK;
   if (!route_dispatch_fused(T, E, k)) {
-    int s = launch_route(logits, T, E, k, renorm, routed, sigmoid, bias, groups_n, groups_top, idx, gates, st);
+    int s = launch_route(logits, T, E, k, renorm, routed, sigmoid, bias, groups_n, groups_top, idx, gates, conv, st);
     return s ? s : launch_dispatch(idx, T, k, E, ds, st);
   }
   const size_t lds = kSmallT * route_wave_lds(E) + (size_t)(2 * kSmallSlots + E + 16) * sizeof(int);
@@ -683,8 +703,9 @@ int launch_route_dispatch(const float* logits, int T, int E, int k, int renorm, 
                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)most) == hipSuccess;
   }();
   if (!lds_ok) return EMBER_ERR_LAUNCH;
-  route_dispatch_small<<<1, 512, lds, st>>>(logits, T, E, k, renorm, routed, sigmoid, bias, groups_n, groups_top, idx,
-                                            gates, ds);
+  const ActConv c = conv ? *conv : ActConv{};
+  route_dispatch_small<<<1 + c.rows, 512, lds, st>>>(logits, T, E, k, renorm, routed, sigmoid, bias, groups_n,
+                                                     groups_top, idx, gates, ds, c);
   return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
 }
 
@@ -693,11 +714,11 @@ int launch_dispatch(const int32_t* idx, int T, int k, int E, const DispatchScrat
   const int nchunks = (nslots + kChunk - 1) / kChunk;
   if (nslots <= 0) return EMBER_OK;
   if (nchunks <= kOneBlockChunks && E <= kOneBlockE) {
-    dispatch_one_block<<<1, kChunk, 0, st>>>(idx, nslots, E, ds.offsets, ds.used, ds.n_used, ds.perm, ds.pos);
+    dispatch_one_block<<<1, kChunk, 0, st>>>(idx, nslots, E, ds);
     return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
   }
   dispatch_count<<<nchunks, kChunk, 16 * (size_t)E * sizeof(int), st>>>(idx, nslots, E, ds.rank, ds.chunk_cnt);
-  dispatch_scan<<<1, 1024, 0, st>>>(ds.chunk_cnt, nchunks, E, ds.offsets, ds.used, ds.n_used);
+  dispatch_scan<<<1, 1024, 0, st>>>(ds.chunk_cnt, nchunks, E, ds);
   dispatch_scatter<<<(nslots + 255) / 256, 256, 0, st>>>(idx, nslots, E, ds.rank, ds.chunk_cnt, ds.perm, ds.pos);
   return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
 }

@@ -473,4 +473,19 @@ __device__ inline int block_exclusive_scan(int v, int* tmp, int* total) {
   return base + x - v;
 }
 
+// The GEMM tile table (DispatchScratch::tiles) from the per-expert segment sizes, by the block that
+// computed them: thread q holds expert q's count (q < E; other threads 0). Every thread of the block
+// calls it (the scan synchronises), after which ds.tiles holds ceil(count / tile_bm) tiles per expert.
+__device__ inline void write_tiles(int q, int E, int cnt, const DispatchScratch& ds, int* tmp) {
+  if (!ds.tiles) return;  // uniform over the block
+  const int nt = q < E ? (cnt + ds.tile_bm - 1) / ds.tile_bm : 0;
+  int all = 0;
+  const int base = block_exclusive_scan(nt, tmp, &all);
+  for (int i = 0; i < nt; ++i) {
+    ds.tiles[2 * (base + i)] = q;
+    ds.tiles[2 * (base + i) + 1] = i * ds.tile_bm;
+  }
+  if (q == 0) *ds.n_tiles = all;
+}
+
 }  // namespace ember_moe
