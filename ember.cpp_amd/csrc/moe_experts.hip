@@ -1015,12 +1015,21 @@ __global__ void __launch_bounds__(256) combine4_kernel(const float* __restrict__
   }
   if (y_shared) {
     float4 v = *reinterpret_cast<const float4*>(y_shared + (size_t)t * d + o);
-    for (int s = 1; s < s_parts; ++s) {
-      const float4 w = *reinterpret_cast<const float4*>(y_shared + s * s_stride + (size_t)t * d + o);
-      v.x = v.x + w.x;
-      v.y = v.y + w.y;
-      v.z = v.z + w.z;
-      v.w = v.w + w.w;
+    if (s_parts > 1) {  // every part's load issued before the ordered sum
+      float4 w[kMaxDenseKSplit - 1];
+#pragma unroll
+      for (int s = 1; s < kMaxDenseKSplit; ++s)
+        w[s - 1] = s < s_parts ? *reinterpret_cast<const float4*>(y_shared + s * s_stride + (size_t)t * d + o)
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int s = 1; s < kMaxDenseKSplit; ++s) {
+        if (s < s_parts) {
+          v.x = v.x + w[s - 1].x;
+          v.y = v.y + w[s - 1].y;
+          v.z = v.z + w[s - 1].z;
+          v.w = v.w + w[s - 1].w;
+        }
+      }
     }
     if (sg_logit) {
       const float c = shared_gate_sigmoid(sg_logit[t]);

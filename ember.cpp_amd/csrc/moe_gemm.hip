@@ -1092,10 +1092,20 @@ __global__ void __launch_bounds__(256) swiglu_parts_kernel(GemmArgs g, int rows,
   const int p = (int)(i / N), n = (int)(i % N);
   const float* part = g.part_h + (size_t)p * 2 * N + n;
   const size_t stride = (size_t)g.part_rows * 2 * N;
-  float ga = part[0], ua = part[N];
-  for (int s = 1; s < KS; ++s) {
-    ga = ga + part[s * stride];
-    ua = ua + part[s * stride + N];
+  // every part's loads issued before the ordered sum
+  float pg[kMaxDenseKSplit], pu[kMaxDenseKSplit];
+#pragma unroll
+  for (int s = 0; s < kMaxDenseKSplit; ++s) {
+    pg[s] = s < KS ? part[s * stride] : 0.0f;
+    pu[s] = s < KS ? part[s * stride + N] : 0.0f;
+  }
+  float ga = pg[0], ua = pu[0];
+#pragma unroll
+  for (int s = 1; s < kMaxDenseKSplit; ++s) {
+    if (s < KS) {
+      ga = ga + pg[s];
+      ua = ua + pu[s];
+    }
   }
   const int we0 = w_exp_of(g.w_exp0, 0, N, n), we1 = w_exp_of(g.w_exp1, 0, N, n);
   const int weh = g.w_hexp ? (int)g.w_hexp[0] : 0;

@@ -305,16 +305,24 @@ __global__ void __launch_bounds__(kChunk) dispatch_count(const int32_t* __restri
 
 // One block of 1024 threads (E <= 1024): offsets[E+1], used[] / n_used, and chunk_cnt overwritten with
 // each chunk's base position per expert.
+// The counts are staged in LDS with coalesced loads (one memory latency, not one per chunk) when they fit
+// (cnt_lds), and the bases written back the same way.
 __global__ void __launch_bounds__(1024) dispatch_scan(int32_t* __restrict__ chunk_cnt, int nchunks, int E,
-                                                      DispatchScratch ds) {
+                                                      DispatchScratch ds, int cnt_lds) {
+  extern __shared__ __align__(16) int cc[];  // [nchunks][E] when cnt_lds
   int32_t* __restrict__ offsets = ds.offsets;
   int32_t* __restrict__ used = ds.used;
   int32_t* __restrict__ n_used = ds.n_used;
   __shared__ int tmp[16];
-  const int e = threadIdx.x;
+  const int e = threadIdx.x, n = nchunks * E;
+  int* cnt = cnt_lds ? cc : chunk_cnt;
+  if (cnt_lds) {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) cc[i] = chunk_cnt[i];
+    __syncthreads();
+  }
   int tot = 0;
   if (e < E)
-    for (int c = 0; c < nchunks; ++c) tot += chunk_cnt[(size_t)c * E + e];
+    for (int c = 0; c < nchunks; ++c) tot += cnt[(size_t)c * E + e];
   int all = 0, nu = 0;
   const int off = block_exclusive_scan(e < E ? tot : 0, tmp, &all);
   const int upos = block_exclusive_scan(e < E && tot > 0 ? 1 : 0, tmp, &nu);
@@ -323,9 +331,9 @@ __global__ void __launch_bounds__(1024) dispatch_scan(int32_t* __restrict__ chun
     if (tot > 0) used[upos] = e;
     int run = off;
     for (int c = 0; c < nchunks; ++c) {
-      const int n = chunk_cnt[(size_t)c * E + e];
-      chunk_cnt[(size_t)c * E + e] = run;
-      run += n;
+      const int v = cnt[(size_t)c * E + e];
+      cnt[(size_t)c * E + e] = run;
+      run += v;
     }
   }
   if (e == 0) {
@@ -333,6 +341,10 @@ __global__ void __launch_bounds__(1024) dispatch_scan(int32_t* __restrict__ chun
     *n_used = nu;
   }
   write_tiles(e, E, tot, ds, tmp);
+  if (cnt_lds) {
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += blockDim.x) chunk_cnt[i] = cc[i];
+  }
 }
 
 __global__ void __launch_bounds__(256) dispatch_scatter(const int32_t* __restrict__ idx, int nslots, int E,
@@ -718,7 +730,9 @@ int launch_dispatch(const int32_t* idx, int T, int k, int E, const DispatchScrat
     return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
   }
   dispatch_count<<<nchunks, kChunk, 16 * (size_t)E * sizeof(int), st>>>(idx, nslots, E, ds.rank, ds.chunk_cnt);
-  dispatch_scan<<<1, 1024, 0, st>>>(ds.chunk_cnt, nchunks, E, ds);
+  const size_t cnt_bytes = (size_t)nchunks * E * sizeof(int);
+  const int cnt_lds = cnt_bytes <= 48 * 1024;
+  dispatch_scan<<<1, 1024, cnt_lds ? cnt_bytes : 0, st>>>(ds.chunk_cnt, nchunks, E, ds, cnt_lds);
   dispatch_scatter<<<(nslots + 255) / 256, 256, 0, st>>>(idx, nslots, E, ds.rank, ds.chunk_cnt, ds.perm, ds.pos);
   return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
 }
