@@ -573,16 +573,18 @@ __global__ void __launch_bounds__(kDmaThreads) gemm_dma_q8_kernel(GemmArgs g, in
   }
   // DMA of tile kt (clamped: tiles past the end reload the last, never multiplied), part j of 4 so
   // that the issue is spread over the K steps of a tile: activation instruction j, weight instruction j
-  auto issue = [&](int kt, int j) {
+  // NOA (compile time): this wave loads no activation rows (its rows lie past the tile's tokens), so its
+  // per-tile DMA count, and the waits that count it, are the weights' alone
+  auto issue = [&](int kt, int j, auto NOAc) {
     const int kc = kt0 + min(kt, nk - 1);
     uint8_t* st = dsm + (kt % kDmaStages) * kDmaStage;
-    lds_dma16(srcA[j] + (size_t)kc * GBK * 2, st + 1024 * (kDmaInstA * wave + j));
+    if constexpr (!decltype(NOAc)::value) lds_dma16(srcA[j] + (size_t)kc * GBK * 2, st + 1024 * (kDmaInstA * wave + j));
     if (j < kDmaInstB)
       lds_dma16(srcB[j] + (size_t)kc * DmaW<WF>::kStride, st + kDmaA + 1024 * min(kDmaInstB * wave + j, kLastB));
   };
-  auto issue_all = [&](int kt) {
+  auto issue_all = [&](int kt, auto NOAc) {
 #pragma unroll
-    for (int j = 0; j < kDmaInstA; ++j) issue(kt, j);
+    for (int j = 0; j < kDmaInstA; ++j) issue(kt, j, NOAc);
   };
 
   floatx16 acc[4][2];
@@ -639,35 +641,36 @@ __global__ void __launch_bounds__(kDmaThreads) gemm_dma_q8_kernel(GemmArgs g, in
   // MFMAs of K step 3 of tile kt run. (The last iteration reads tile nk, a clamped reload, unused.)
   // A wave whose M half holds no tokens (MS = 0) only loads and keeps the barriers.
   static_assert(kDmaStages == 3, "the waits below assume one tile in flight beyond the current one");
-  auto k_loop = [&](auto MSc) {
+  auto k_loop = [&](auto MSc, auto NOAc) {
+    constexpr int kInst = decltype(NOAc)::value ? kDmaInstB : kDmaInst;  // this wave's DMA per tile
     using K0 = std::integral_constant<int, 0>;
     using K1 = std::integral_constant<int, 1>;
     using K2 = std::integral_constant<int, 2>;
     using K3 = std::integral_constant<int, 3>;
-    issue_all(0);
-    issue_all(1);
-    wait_vmcnt<kDmaInst>();
+    issue_all(0, NOAc);
+    issue_all(1, NOAc);
+    wait_vmcnt<kInst>();
     barrier();
     Frags f0, f1;
     if constexpr (decltype(MSc)::value > 0) load_frags(dsm, K0{}, MSc, f0);
     for (int kt = 0; kt < nk; ++kt) {
       if constexpr (decltype(MSc)::value == 0) {
-        issue_all(kt + 2);
-        wait_vmcnt<kDmaInst>();
+        issue_all(kt + 2, NOAc);
+        wait_vmcnt<kInst>();
         barrier();
       } else {
         const uint8_t* st = dsm + (kt % kDmaStages) * kDmaStage;
         load_frags(st, K1{}, MSc, f1);
-        issue(kt + 2, 0);
+        issue(kt + 2, 0, NOAc);
         mfmas(f0, MSc);
         load_frags(st, K2{}, MSc, f0);
-        issue(kt + 2, 1);
+        issue(kt + 2, 1, NOAc);
         mfmas(f1, MSc);
         load_frags(st, K3{}, MSc, f1);
-        issue(kt + 2, 2);
+        issue(kt + 2, 2, NOAc);
         mfmas(f0, MSc);
-        issue(kt + 2, 3);
-        wait_vmcnt<kDmaInst>();
+        issue(kt + 2, 3, NOAc);
+        wait_vmcnt<kInst>();
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of tile kt are complete
         barrier();
         load_frags(dsm + ((kt + 1) % kDmaStages) * kDmaStage, K0{}, MSc, f0);
@@ -677,12 +680,26 @@ __global__ void __launch_bounds__(kDmaThreads) gemm_dma_q8_kernel(GemmArgs g, in
   };
   __shared__ int s_rexp[GBM];
   load_row_exps(g, p0, rows, s_rexp);
-  switch (msub) {  // wave-uniform
-    case 4: k_loop(std::integral_constant<int, 4>{}); break;
-    case 3: k_loop(std::integral_constant<int, 3>{}); break;
-    case 2: k_loop(std::integral_constant<int, 2>{}); break;
-    case 1: k_loop(std::integral_constant<int, 1>{}); break;
-    default: k_loop(std::integral_constant<int, 0>{}); break;
+  // waves whose activation rows (32 w .. 32 w + 31) lie past the tile's tokens load none: a short tile's
+  // DMA is then its weights and only the activation rows it holds (wave-uniform)
+  using A1 = std::integral_constant<bool, false>;
+  using A0 = std::integral_constant<bool, true>;
+  if (32 * wave >= rows) {
+    switch (msub) {
+      case 4: k_loop(std::integral_constant<int, 4>{}, A0{}); break;
+      case 3: k_loop(std::integral_constant<int, 3>{}, A0{}); break;
+      case 2: k_loop(std::integral_constant<int, 2>{}, A0{}); break;
+      case 1: k_loop(std::integral_constant<int, 1>{}, A0{}); break;
+      default: k_loop(std::integral_constant<int, 0>{}, A0{}); break;
+    }
+  } else {
+    switch (msub) {
+      case 4: k_loop(std::integral_constant<int, 4>{}, A1{}); break;
+      case 3: k_loop(std::integral_constant<int, 3>{}, A1{}); break;
+      case 2: k_loop(std::integral_constant<int, 2>{}, A1{}); break;
+      case 1: k_loop(std::integral_constant<int, 1>{}, A1{}); break;
+      default: k_loop(std::integral_constant<int, 0>{}, A1{}); break;
+    }
   }
   wait_vmcnt<0>();  // no DMA may still target LDS when the block exits
   __syncthreads();  // the row exponents are visible
