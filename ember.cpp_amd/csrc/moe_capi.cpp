@@ -42,11 +42,12 @@ int path_mode(int type_in, int K_in, int type_out, int K_out, double avg_m, int 
   if (q8) return avg_m <= 1.5 ? kGemv : kGemm;
   // (packed BF16: row exponents for the fp16 MFMA path, which both tile kernels have; without them BF16 runs
   // the split bf16 MFMA, which only the 64-token-tile kernel implements)
-  // packed Q4_K (the same DMA tile kernels): the GEMV up to 1.6 tokens per expert, the 64-token tiles up to
-  // 3, the 256-token tiles beyond (Mixtral-shaped: T = 6 GEMV 270 vs 273 us, T = 8 327 vs 275 (64) vs 298
-  // (256), T = 16 372 (64) vs 302 (256); Qwen-shaped E = 128: T = 24 170 vs 175, T = 32 186 vs 177)
+  // packed Q4_K (the same DMA tile kernels): the GEMV up to 1.25 tokens per expert, the 64-token tiles up
+  // to 1.75, the 256-token tiles beyond (Mixtral-shaped: T = 4 GEMV 182 vs 258 (64), T = 6 280 vs 205
+  // (64), T = 8 345 (64) vs 278 (256); Qwen-shaped E = 128: T = 16 128 vs 140 (64), T = 24 167 vs 146
+  // (64), T = 32 159 either tiling)
   if (packed && type_in == EMBER_TYPE_Q4_K && type_out == EMBER_TYPE_Q4_K)
-    return avg_m <= 1.6 ? kGemv : avg_m <= 3.0 ? kSkinny : kGemm;
+    return avg_m <= 1.25 ? kGemv : avg_m <= 1.75 ? kSkinny : kGemm;
   // BF16 / F16: by the expected tokens per expert HIT, T*k / (E (1 - (1 - 1/E)^(T*k))), since the GEMV's
   // cost follows the token passes over the hit experts and the MFMA tiles' the hit experts' weights; the
   // GEMV wins up to ~1.5 (C4-shaped routed experts: T = 8 183 vs 184 us, T = 12 254 vs 202; Qwen-shaped

@@ -793,10 +793,12 @@ __global__ void __launch_bounds__(kD64Threads) gemm_dma64_q8_kernel(GemmArgs g, 
   }
   // DMA of tile kt (clamped past the end), part j of 4: A granule j / 2 on even parts, weight
   // granules spread over the four parts
-  auto issue = [&](int kt, int j) {  // kt: tile index within this block's K range
+  // NOA (compile time): this wave's activation rows (16 w .. 16 w + 15) lie past the tile's tokens, so it
+  // loads none and its per-tile DMA count is the weights' alone
+  auto issue = [&](int kt, int j, auto NOAc) {  // kt: tile index within this block's K range
     const int kc = kt0 + min(kt, nk - 1);
     uint8_t* st = dsm + (kt % kD64Stages) * kD64Stage;
-    if ((j & 1) == 0) {
+    if (!decltype(NOAc)::value && (j & 1) == 0) {
       const int i = j >> 1;
       lds_dma16(srcA[i] + (size_t)kc * GBK * 2, st + 1024 * (kD64InstA * wave + i));
     }
@@ -841,38 +843,44 @@ __global__ void __launch_bounds__(kD64Threads) gemm_dma64_q8_kernel(GemmArgs g, 
       for (int jn = 0; jn < 2; ++jn)
         acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[i], f.b[jn], acc[i][jn], 0, 0, 0);
   };
-  auto compute = [&](int kt) {
+  auto compute = [&](int kt, auto NOAc) {
     const uint8_t* st = dsm + (kt % kD64Stages) * kD64Stage;
     Frags f0, f1;
     load_frags(st, std::integral_constant<int, 0>{}, f0);
-    issue(kt + kD64Stages - 1, 0);
+    issue(kt + kD64Stages - 1, 0, NOAc);
     load_frags(st, std::integral_constant<int, 1>{}, f1);
     mfmas(f0);
-    issue(kt + kD64Stages - 1, 1);
+    issue(kt + kD64Stages - 1, 1, NOAc);
     load_frags(st, std::integral_constant<int, 2>{}, f0);
     mfmas(f1);
-    issue(kt + kD64Stages - 1, 2);
+    issue(kt + kD64Stages - 1, 2, NOAc);
     load_frags(st, std::integral_constant<int, 3>{}, f1);
     mfmas(f0);
-    issue(kt + kD64Stages - 1, 3);
+    issue(kt + kD64Stages - 1, 3, NOAc);
     mfmas(f1);
   };
 
   __shared__ int s_rexp[kD64BM];
   load_row_exps(g, p0, rows, s_rexp);
-  constexpr int kPerTile = kD64InstA + kD64InstB;
-  static_assert(kD64Stages == 5, "the wait below keeps three tiles in flight beyond the current one");
+  auto k_loop = [&](auto NOAc) {
+    constexpr int kPerTile = (decltype(NOAc)::value ? 0 : kD64InstA) + kD64InstB;
+    static_assert(kD64Stages == 5, "the wait below keeps three tiles in flight beyond the current one");
 #pragma unroll
-  for (int t = 0; t < kD64Stages - 1; ++t)
+    for (int t = 0; t < kD64Stages - 1; ++t)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) issue(t, j);
-  for (int kt = 0; kt < nk; ++kt) {
-    wait_vmcnt<3 * kPerTile>();  // this wave's part of tile kt has landed
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();  // ... every wave's; stage (kt + 4) % 5 is free again
-    asm volatile("" ::: "memory");
-    compute(kt);
-  }
+      for (int j = 0; j < 4; ++j) issue(t, j, NOAc);
+    for (int kt = 0; kt < nk; ++kt) {
+      wait_vmcnt<3 * kPerTile>();  // this wave's part of tile kt has landed
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();  // ... every wave's; stage (kt + 4) % 5 is free again
+      asm volatile("" ::: "memory");
+      compute(kt, NOAc);
+    }
+  };
+  if (16 * wave >= rows)
+    k_loop(std::integral_constant<bool, true>{});
+  else
+    k_loop(std::integral_constant<bool, false>{});
   wait_vmcnt<0>();
   __syncthreads();  // the row exponents are visible
 
