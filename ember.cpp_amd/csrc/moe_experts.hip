@@ -790,6 +790,17 @@ __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) 
       __hip_atomic_store(a.clear_flag + i, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int t = threadIdx.x;
   EMBER_STAMP(1, 0);
+  // the picks' h rows, quantizing formats with one 32-element block per thread: one token's valid picks
+  // sit at dispatch positions 0 .. np-1, so rows 0 .. k-1 are loaded into registers at once, before the
+  // picks are read and before the first down rows are requested (loads complete in order, so they do not
+  // wait for the weight loads); quantized into LDS once those are in flight
+  const int nbh = a.K / 32;
+  const bool h_early = F::QX && a.K % 32 == 0 && a.k * nbh <= NT;
+  float hv[32];
+  if (h_early && t < a.k * nbh) {
+    const int m = t / nbh, b = t - m * nbh;
+    load_block32(a.h + (size_t)m * a.K + (size_t)b * 32, hv);
+  }
   if (t < 64) {  // the valid picks in ascending order (the combine's order): one round of loads, compacted
     int p = -1, e = 0;
     float g = 0.0f;
@@ -833,10 +844,22 @@ __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) 
   // the first down rows are requested before every pick's h row (then the shared expert's) is staged
   auto stage = [&] {
     if (np > 0) {
-      if constexpr (F::QX)
-        stage_rows_quant<F::PLANES>(a.h, a.K, pos_s, np, act_lds, row_lds);
-      else
+      if constexpr (F::QX) {
+        if (h_early) {
+          if (t < np * nbh) {
+            const int m = t / nbh, b = t - m * nbh;
+            uint32_t packed[16];
+            float sc;
+            int sm;
+            quant_block32_v(hv, packed, &sc, &sm);
+            store_block_quant<F::PLANES>(packed, sc, sm, b, a.K, act_lds + m * row_lds);
+          }
+        } else {
+          stage_rows_quant<F::PLANES>(a.h, a.K, pos_s, np, act_lds, row_lds);
+        }
+      } else {
         stage_rows_f32<F::NGL>(a.h, a.K, pos_s, np, act_lds, row_lds);
+      }
     }
     if (a.s_w) {
       if constexpr (F::QX)

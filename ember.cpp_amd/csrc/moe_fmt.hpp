@@ -335,8 +335,7 @@ __device__ inline void stage_rows(bool qx, const StageSrc& a, const int* rows, i
 // Per-32-element-block int16 quantization of one block of activations, the values quantize_act_kernel
 // writes: s = amax / 32767, q = rint(x * (32767 / amax)) clamped to +-32767 (q = 0, s = 0 for an
 // all-zero block), plus the block's sum of q.
-__device__ inline void quant_block32(const float* src, uint32_t* packed, float* scale, int* sum) {
-  float v[32];
+__device__ inline void load_block32(const float* src, float* v) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const float4 t = reinterpret_cast<const float4*>(src)[i];
@@ -345,6 +344,9 @@ __device__ inline void quant_block32(const float* src, uint32_t* packed, float* 
     v[4 * i + 2] = t.z;
     v[4 * i + 3] = t.w;
   }
+}
+// 32 values (in registers) -> int16 pairs, scale, sum
+__device__ inline void quant_block32_v(const float* v, uint32_t* packed, float* scale, int* sum) {
   float amax = 0.0f;
 #pragma unroll
   for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
@@ -360,10 +362,32 @@ __device__ inline void quant_block32(const float* src, uint32_t* packed, float* 
   *scale = amax / 32767.0f;
   *sum = tot;
 }
+__device__ inline void quant_block32(const float* src, uint32_t* packed, float* scale, int* sum) {
+  float v[32];
+  load_block32(src, v);
+  quant_block32_v(v, packed, scale, sum);
+}
 
 // Stages f32 activation rows rows[0..nrows) of [*][K] into LDS already quantized (act_lds_bytes
 // layout for the quantizing formats: int16 values in rotated 64-element chunks, then the per-block
 // scales, then the per-block sums). One thread per 32-element block.
+// One block's store into the staged row (act_lds_bytes layout), from its quantized values.
+template <bool PLANES = false>
+__device__ inline void store_block_quant(const uint32_t* packed, float sc, int sm, int b, int K, uint8_t* row) {
+  const int nb = K / 32;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    u32x4 gr{packed[4 * g], packed[4 * g + 1], packed[4 * g + 2], packed[4 * g + 3]};
+    if constexpr (PLANES) {
+      gr = u32x4{__builtin_amdgcn_perm(gr.y, gr.x, 0x06040200u), __builtin_amdgcn_perm(gr.w, gr.z, 0x06040200u),
+                 __builtin_amdgcn_perm(gr.y, gr.x, 0x07050301u), __builtin_amdgcn_perm(gr.w, gr.z, 0x07050301u)};
+    }
+    *reinterpret_cast<u32x4*>(row + 16 * swz_granule<3>(b >> 1, (b & 1) * 4 + g)) = gr;
+  }
+  reinterpret_cast<float*>(row + K * 2)[b] = sc;
+  reinterpret_cast<int*>(row + K * 2 + nb * 4)[b] = sm;
+}
+
 template <bool PLANES = false>
 __device__ inline void stage_rows_quant(const float* in, int K, const int* rows, int nrows, uint8_t* lds, int row_lds) {
   const int nb = K / 32;
