@@ -244,10 +244,26 @@ __device__ inline void load_row_exps(const GemmArgs& g, int p0, int rows, int* s
   for (int r = threadIdx.x; r < rows; r += blockDim.x) s_rexp[r] = row_exp(g, p0 + r);
 }
 
-// Blocks are laid out XCD-aware: the hardware hands block b to XCD b % 8, and block b works on
-// m-tile (b % 8) + 8 * ((b / 8) / NT) and n-tile (b / 8) % NT, so the blocks resident on one XCD at a
-// time share one m-tile of activations (read into that XCD's L2 once) while consecutive m-tiles of an
-// expert run on neighbouring XCDs at the same time (their weight tiles meet in the shared MALL).
+// m-tiles of a launch: the device-side tile count, or the dense rows' tiles of bm tokens
+__device__ inline int launch_mtiles(const GemmArgs& g, int bm) {
+  return g.tiles ? *g.n_tiles : (g.T + bm - 1) / bm;
+}
+
+// XCD-balanced work item of block b for the 256-token-tile kernels: the W = M x NT x KS work items (m-tile
+// major, then n-tile, then K part) are cut into 8 equal runs, one per XCD (the hardware hands block b to
+// XCD b % 8), and XCD x's j-th block takes item x ceil(W / 8) + j. Every XCD gets the same share whatever
+// the (data-dependent) m-tile count, and the blocks an XCD holds at once mostly share one m-tile of
+// activations in its L2. False: no item (the grid is sized for the largest M).
+__device__ inline bool xcd_item(int M, int NT, int KS, int& mt, int& rem) {
+  const int W = M * NT * KS, C = (W + 7) / 8;
+  const int j = blockIdx.x / 8, w = (blockIdx.x % 8) * C + j;
+  if (j >= C || w >= W) return false;
+  mt = w / (NT * KS);
+  rem = w % (NT * KS);
+  return true;
+}
+
+// Blocks take their tiles XCD-balanced (xcd_item).
 //
 // 512 threads = 8 waves in a 4 (M) x 2 (N) arrangement (two waves per SIMD, so one wave's waits and
 // decode overlap the other's MFMAs), each wave a 64 x 128 tile of accumulators; every thread loads
@@ -268,11 +284,10 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs g, int NT) 
   extern __shared__ __align__(16) _Float16 smem[];
 
   // ---- the tile
-  const int xcd = blockIdx.x % 8, j = blockIdx.x / 8;
-  const int mt = xcd + 8 * (j / NT), nt = j % NT;
+  int mt, nt;
+  if (!xcd_item(launch_mtiles(g, GBM), NT, 1, mt, nt)) return;
   int e = 0, p0 = 0, rows = 0;
   if (g.tiles) {
-    if (mt >= *g.n_tiles) return;
     e = g.tiles[2 * mt];
     const int m0 = g.tiles[2 * mt + 1];
     p0 = g.offsets[e] + m0;
@@ -512,15 +527,13 @@ __global__ void __launch_bounds__(kDmaThreads) gemm_dma_q8_kernel(GemmArgs g, in
   constexpr int kDmaInst = kDmaInstA + kDmaInstB;
   extern __shared__ __align__(16) uint8_t dsm[];
 
-  // block -> (m-tile, n-tile, K split part): XCD b % 8 runs m-tile (b % 8) + 8 ((b / 8) / (NT KS)), so
-  // the blocks an XCD holds at once share their activation tile in its L2
+  // block -> (m-tile, n-tile, K split part), XCD-balanced
   const int KS = GATED ? 1 : g.ksplit;
-  const int xcd = blockIdx.x % 8, jb = blockIdx.x / 8;
-  const int mt = xcd + 8 * (jb / (NT * KS)), rem = jb % (NT * KS);
+  int mt, rem;
+  if (!xcd_item(launch_mtiles(g, GBM), NT, KS, mt, rem)) return;
   const int nt = rem / KS, ks = rem % KS;
   int e = 0, p0 = 0, rows = 0;
   if (g.tiles) {
-    if (mt >= *g.n_tiles) return;
     e = g.tiles[2 * mt];
     const int m0 = g.tiles[2 * mt + 1];
     p0 = g.offsets[e] + m0;
@@ -748,11 +761,14 @@ __global__ void __launch_bounds__(kD64Threads) gemm_dma64_q8_kernel(GemmArgs g, 
   extern __shared__ __align__(16) uint8_t dsm[];
 
   // block -> (m-tile, n-tile, K split part); part ks covers K tiles [kt0, kt0 + nk)
-  const int mt = blockIdx.x % g.max_mt, rest = blockIdx.x / g.max_mt;
+  // (items m-tile fastest, numbered densely: no block of the grid's tail is left waiting behind
+  // empty slots)
+  const int M = launch_mtiles(g, kD64BM);
+  if ((int)blockIdx.x >= M * NT * (g.ksplit < 1 ? 1 : g.ksplit)) return;
+  const int mt = blockIdx.x % M, rest = blockIdx.x / M;
   const int nt = rest % NT, ks = rest / NT;
   int e = 0, p0 = 0, rows = 0;
   if (g.tiles) {
-    if (mt >= *g.n_tiles) return;
     e = g.tiles[2 * mt];
     const int m0 = g.tiles[2 * mt + 1];
     p0 = g.offsets[e] + m0;
@@ -930,12 +946,15 @@ __global__ void __launch_bounds__(256) gemm_skinny_kernel(GemmArgs g, int NT) {
   __shared__ __align__(16) _Float16 As[2][NP][SBM][LDK];
 
   // block -> (m-tile, n-tile, K split part); part ks covers K tiles [kt0, kt0 + nk)
-  const int mt = blockIdx.x % g.max_mt, rest = blockIdx.x / g.max_mt;
+  // (items m-tile fastest, numbered densely: no block of the grid's tail is left waiting behind
+  // empty slots)
+  const int M = launch_mtiles(g, SBM);
+  if ((int)blockIdx.x >= M * NT * (g.ksplit < 1 ? 1 : g.ksplit)) return;
+  const int mt = blockIdx.x % M, rest = blockIdx.x / M;
   const int nt = rest % NT, ks = rest / NT;
   const int KS = g.ksplit < 1 ? 1 : g.ksplit;
   int e = 0, p0 = 0, rows = 0;
   if (g.tiles) {
-    if (mt >= *g.n_tiles) return;
     e = g.tiles[2 * mt];
     const int m0 = g.tiles[2 * mt + 1];
     p0 = g.offsets[e] + m0;
@@ -1211,7 +1230,6 @@ int launch_skinny_fmt(GemmArgs g, int max_mtiles, hipStream_t st) {
   constexpr int BN = GATED ? 128 : 256;
   const int NT = (g.N + BN - 1) / BN;
   if (max_mtiles == 0 || NT == 0) return EMBER_OK;
-  g.max_mt = max_mtiles;
   if (dma_path(FMT, g.Wp != nullptr)) {
     static const bool ok =
         hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma64_q8_kernel<GATED, kWfQ8Rows>),

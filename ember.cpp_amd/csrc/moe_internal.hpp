@@ -182,7 +182,6 @@ struct GemmArgs {
   const int32_t* offsets;
   _Float16* out_h;         // gated: silu(gate) * up as fp16 [pos][N]
   float* out_y;            // plain: f32 [pos][N]
-  int max_mt;              // m-tile slots of the launch (set by the launcher)
   int ksplit;              // plain projections: K split over this many blocks, partial sums to
   int64_t part_stride;     // out_y + s * part_stride (floats), summed in order by the combine
   const uint8_t* Wp;       // non-null: this projection's tiles in the prefill pack (Q8_0, 256-token tiles)
