@@ -252,7 +252,7 @@ P* at(void* base, size_t off) {
 }
 
 DispatchScratch dispatch_scratch(void* scratch, const RouteLayout& r, int32_t* offsets, int32_t* perm) {
-  DispatchScratch ds;
+  DispatchScratch ds{};
   ds.rank = at<int32_t>(scratch, r.rank);
   ds.chunk_cnt = at<int32_t>(scratch, r.chunk_cnt);
   ds.offsets = offsets;

@@ -51,9 +51,9 @@ struct DispatchScratch {
   int32_t* pos;        // [T*k] slot -> sorted position (-1: no pick)
   // optional (null: none): the MFMA GEMMs' tile table, written by the dispatch's last step: tiles of
   // tile_bm rows over each expert's segment, experts ascending, as (expert, first row) pairs
-  int32_t* tiles;
-  int32_t* n_tiles;
-  int tile_bm;
+  int32_t* tiles = nullptr;
+  int32_t* n_tiles = nullptr;
+  int tile_bm = 0;
 };
 
 int launch_router_logits(const float* x, int T, int d, int E, const float* R, float* logits, hipStream_t st);
