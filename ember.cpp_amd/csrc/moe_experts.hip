@@ -101,20 +101,27 @@ __device__ inline float wave_incl_scan(float v) {
 }
 __device__ inline int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
-template <bool GATED, int MT>
+// ONE_TOKEN: every routed segment holds one token (a one-token launch, at most 64 picks), so each has the
+// same work w and the prefix sums are s w (integer-valued floats: the same values the scans give)
+template <bool GATED, int MT, bool ONE_TOKEN = false>
 __device__ inline bool seg_view(const ProjArgs& a, const Dispatch& dp, int b, int G, SegView& v) {
   const int nseg = a.used ? dp.n_used : 0;
   const int lane = threadIdx.x & 63;
   // routed work: total, then this block's segment from the prefix sums
   float w_routed = 0.0f;
-  for (int s0 = 0; s0 < nseg; s0 += 64) {
-    const int s = s0 + lane;
-    float w = 0.0f;
-    if (s < nseg) {
-      const int e = dp.used[s];
-      w = seg_work(a.rows, dp.offsets[e + 1] - dp.offsets[e], MT);
+  const float w1 = seg_work(a.rows, 1, MT);
+  if constexpr (ONE_TOKEN) {
+    w_routed = (float)nseg * w1;
+  } else {
+    for (int s0 = 0; s0 < nseg; s0 += 64) {
+      const int s = s0 + lane;
+      float w = 0.0f;
+      if (s < nseg) {
+        const int e = dp.used[s];
+        w = seg_work(a.rows, dp.offsets[e + 1] - dp.offsets[e], MT);
+      }
+      w_routed += __shfl(wave_incl_scan(w), 63, 64);
     }
-    w_routed += __shfl(wave_incl_scan(w), 63, 64);
   }
   const float w_shared = a.s_w0 ? seg_work(a.s_rows, a.T, MT) : 0.0f;
   if (w_routed + w_shared == 0.0f) return false;
@@ -128,12 +135,17 @@ __device__ inline bool seg_view(const ProjArgs& a, const Dispatch& dp, int b, in
     float carry = 0.0f;
     for (int s0 = 0; s0 < nseg; s0 += 64) {
       const int s = s0 + lane;
-      float w = 0.0f;
-      if (s < nseg) {
-        const int e = dp.used[s];
-        w = seg_work(a.rows, dp.offsets[e + 1] - dp.offsets[e], MT);
+      float w = 0.0f, incl;
+      if constexpr (ONE_TOKEN) {
+        w = s < nseg ? w1 : 0.0f;
+        incl = (float)min(s + 1, nseg) * w1;
+      } else {
+        if (s < nseg) {
+          const int e = dp.used[s];
+          w = seg_work(a.rows, dp.offsets[e + 1] - dp.offsets[e], MT);
+        }
+        incl = carry + wave_incl_scan(w);
       }
-      const float incl = carry + wave_incl_scan(w);
       const float excl = incl - w;
       const int start = s + min(Gr - nseg, (int)(spare * (excl / w_routed)));
       const int next = s + 1 + min(Gr - nseg, (int)(spare * (incl / w_routed)));
@@ -442,6 +454,46 @@ __device__ inline void fused_dispatch(const int* picks, int nv, int E, int32_t* 
   if (t == 0) *s_n = nv;
 }
 
+// Block 0's record of the routing for the later launches (logits, idx, gates, pos, used, perm, offsets,
+// n_used). gates: the picks' gates are still to be computed (from the logits in the routing area).
+template <int NT, bool ROUTED>
+__device__ void route_publish(const ProjArgs& a, uint8_t* ra, bool gates) {
+  const ProjArgs::Route& r = a.route;
+  const int t = threadIdx.x;
+  float* lg = reinterpret_cast<float*>(ra);
+  int32_t* pidx = reinterpret_cast<int32_t*>(ra + 2048);
+  float* pgate = reinterpret_cast<float*>(ra + 2048 + 256);
+  uint8_t* wl = ra + 2048 + 512;
+  const int E = r.E, k = a.k;
+  if (gates) {
+    __syncthreads();
+    if (t < 64)
+      route_token<ROUTED>(lg, E, k, r.renorm, r.routed, r.sigmoid, r.bias, r.groups_n, r.groups_top, wl, pidx, pgate,
+                          true);
+    __syncthreads();
+  }
+  int nv = 0;
+  for (int j = 0; j < k; ++j) nv += pidx[j] >= 0;
+  {
+    for (int e = t; e < E; e += NT) r.logits[e] = lg[e];
+    if (t < k) {
+      r.idx[t] = pidx[t];
+      r.gates[t] = pgate[t];
+      r.pos[t] = t < nv ? t : -1;
+    }
+    if (t < nv) {
+      r.used[t] = pidx[t];
+      r.perm[t] = t;
+    }
+    for (int e = t; e <= E; e += NT) {
+      int cnt = 0;
+      for (int j = 0; j < nv; ++j) cnt += pidx[j] < e;
+      r.offsets[e] = cnt;
+    }
+    if (t == 0) *r.n_used = nv;
+  }
+}
+
 // Every block (router blocks after their own logit): collects every expert's tagged logit (bounded
 // wait), runs route_token (exp tables staged at the start of the launch; every block computes the same
 // routing, so no second hop through one block is needed) and fills its dispatch arrays; block 0 also
@@ -479,7 +531,7 @@ __device__ float router_logit_slow(const ProjArgs& a, int e, uint8_t* lds) {
 }
 
 template <int NT, bool ROUTED>
-__device__ void route_block(const ProjArgs& a, uint8_t* lds, uint8_t* ra, int32_t* s_off, int32_t* s_used,
+__device__ bool route_block(const ProjArgs& a, uint8_t* lds, uint8_t* ra, int32_t* s_off, int32_t* s_used,
                             int32_t* s_n, int32_t* s_perm) {
   __shared__ uint8_t missing[kMaxRouteE];
   __shared__ int any_missing;
@@ -515,33 +567,40 @@ __device__ void route_block(const ProjArgs& a, uint8_t* lds, uint8_t* ra, int32_
     if (t == 0) __hip_atomic_fetch_add(r.flag, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
   }
-  if (t < 64)
-    route_token<ROUTED>(lg, E, k, r.renorm, r.routed, r.sigmoid, r.bias, r.groups_n, r.groups_top, wl, pidx, pgate,
-                        true);
-  __syncthreads();
+  // The softmax router's picks are the top k of the logits themselves: with finite logits every block
+  // takes only them (the launch's dispatch needs nothing else), and block 0 computes the gates and writes
+  // the routing after its own rows (route_publish); otherwise every block runs the whole routing here.
+  bool deferred = false;
+  if constexpr (!ROUTED) {
+    __shared__ int s_nan;
+    if (t < 64) {
+      bool nan = false;
+      for (int e = t; e < E; e += 64) nan |= lg[e] != lg[e];
+      nan = __any(nan);
+      if (!nan) {
+        const int kk = wave_topk(lg, nullptr, E, min(k, E), pidx);
+        if (t >= kk && t < k) pidx[t] = -1;
+      }
+      if (t == 0) s_nan = nan;
+    }
+    __syncthreads();
+    deferred = !s_nan;
+  }
+  if (!deferred) {
+    if (t < 64)
+      route_token<ROUTED>(lg, E, k, r.renorm, r.routed, r.sigmoid, r.bias, r.groups_n, r.groups_top, wl, pidx, pgate,
+                          true);
+    __syncthreads();
+  }
   int nv = 0;  // valid picks: a prefix (route_token puts the -1 entries last)
   for (int j = 0; j < k; ++j) nv += pidx[j] >= 0;
-  if (blockIdx.x == 0) {
-    for (int e = t; e < E; e += NT) r.logits[e] = lg[e];
-    if (t < k) {
-      r.idx[t] = pidx[t];
-      r.gates[t] = pgate[t];
-      r.pos[t] = t < nv ? t : -1;
-    }
-    if (t < nv) {
-      r.used[t] = pidx[t];
-      r.perm[t] = t;
-    }
-    for (int e = t; e <= E; e += NT) {
-      int cnt = 0;
-      for (int j = 0; j < nv; ++j) cnt += pidx[j] < e;
-      r.offsets[e] = cnt;
-    }
-    if (t == 0) *r.n_used = nv;
-  }
+  if (blockIdx.x == 0 && !deferred) route_publish<NT, ROUTED>(a, ra, false);
   fused_dispatch(pidx, nv, E, s_off, s_used, s_n, s_perm);
   __syncthreads();
+  return deferred;
 }
+
+
 
 // ROUTE: 0 none; 1 the fused one-token routing with a softmax router; 2 with the DeepSeek-style options
 template <int FMT, int MT, bool GATED, int NB, int NT, int WPE, int ROUTE>
@@ -579,14 +638,15 @@ __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) 
       else
         stage_rows_f32<F::NGL>(a.route.x, a.route.d, &zero_row, 1, xs, act_lds_bytes(false, a.route.d));
     }
-    route_block<NT, ROUTE == 2>(a, prod, ra, s_off, s_used, &s_n, s_perm);
+    const bool deferred = route_block<NT, ROUTE == 2>(a, prod, ra, s_off, s_used, &s_n, s_perm);
     EMBER_STAMP(0, 3);
     __syncthreads();
     Dispatch dp{s_n, s_used, s_off, s_perm};
     SegView v;
-    const bool act = seg_view<GATED, MT>(a, dp, blockIdx.x, gridDim.x, v);
+    const bool act = seg_view<GATED, MT, true>(a, dp, blockIdx.x, gridDim.x, v);
     EMBER_STAMP(0, 4);
     if (act) proj_body<FMT, MT, GATED, NB, NT, false, true>(a, dp, v);
+    if (b == 0 && deferred) route_publish<NT, ROUTE == 2>(a, ra, true);
     EMBER_STAMP(0, 7);
   } else {
     Dispatch dp{a.used ? *a.n_used : 0, a.used, a.offsets, a.perm};
