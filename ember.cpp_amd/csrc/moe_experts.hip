@@ -455,23 +455,15 @@ __device__ inline void fused_dispatch(const int* picks, int nv, int E, int32_t* 
 }
 
 // Block 0's record of the routing for the later launches (logits, idx, gates, pos, used, perm, offsets,
-// n_used). gates: the picks' gates are still to be computed (from the logits in the routing area).
+// n_used), from the routing area.
 template <int NT, bool ROUTED>
-__device__ void route_publish(const ProjArgs& a, uint8_t* ra, bool gates) {
+__device__ void route_publish(const ProjArgs& a, uint8_t* ra) {
   const ProjArgs::Route& r = a.route;
   const int t = threadIdx.x;
   float* lg = reinterpret_cast<float*>(ra);
   int32_t* pidx = reinterpret_cast<int32_t*>(ra + 2048);
   float* pgate = reinterpret_cast<float*>(ra + 2048 + 256);
-  uint8_t* wl = ra + 2048 + 512;
   const int E = r.E, k = a.k;
-  if (gates) {
-    __syncthreads();
-    if (t < 64)
-      route_token<ROUTED>(lg, E, k, r.renorm, r.routed, r.sigmoid, r.bias, r.groups_n, r.groups_top, wl, pidx, pgate,
-                          true);
-    __syncthreads();
-  }
   int nv = 0;
   for (int j = 0; j < k; ++j) nv += pidx[j] >= 0;
   {
@@ -531,7 +523,7 @@ __device__ float router_logit_slow(const ProjArgs& a, int e, uint8_t* lds) {
 }
 
 template <int NT, bool ROUTED>
-__device__ bool route_block(const ProjArgs& a, uint8_t* lds, uint8_t* ra, int32_t* s_off, int32_t* s_used,
+__device__ void route_block(const ProjArgs& a, uint8_t* lds, uint8_t* ra, int32_t* s_off, int32_t* s_used,
                             int32_t* s_n, int32_t* s_perm) {
   __shared__ uint8_t missing[kMaxRouteE];
   __shared__ int any_missing;
@@ -568,10 +560,11 @@ __device__ bool route_block(const ProjArgs& a, uint8_t* lds, uint8_t* ra, int32_
     __syncthreads();
   }
   // The softmax router's picks are the top k of the logits themselves: with finite logits every block
-  // takes only them (the launch's dispatch needs nothing else), and block 0 computes the gates and writes
-  // the routing after its own rows (route_publish); otherwise every block runs the whole routing here.
-  bool deferred = false;
-  if constexpr (!ROUTED) {
+  // but block 0 takes only them (the launch's dispatch needs nothing else); block 0 (and every block
+  // when a logit is NaN, or with the DeepSeek router) runs the whole routing, and block 0 writes it for
+  // the later launches.
+  bool picks_only = false;
+  if (!ROUTED && blockIdx.x != 0) {
     __shared__ int s_nan;
     if (t < 64) {
       bool nan = false;
@@ -584,9 +577,9 @@ __device__ bool route_block(const ProjArgs& a, uint8_t* lds, uint8_t* ra, int32_
       if (t == 0) s_nan = nan;
     }
     __syncthreads();
-    deferred = !s_nan;
+    picks_only = !s_nan;
   }
-  if (!deferred) {
+  if (!picks_only) {
     if (t < 64)
       route_token<ROUTED>(lg, E, k, r.renorm, r.routed, r.sigmoid, r.bias, r.groups_n, r.groups_top, wl, pidx, pgate,
                           true);
@@ -594,10 +587,9 @@ __device__ bool route_block(const ProjArgs& a, uint8_t* lds, uint8_t* ra, int32_
   }
   int nv = 0;  // valid picks: a prefix (route_token puts the -1 entries last)
   for (int j = 0; j < k; ++j) nv += pidx[j] >= 0;
-  if (blockIdx.x == 0 && !deferred) route_publish<NT, ROUTED>(a, ra, false);
+  if (blockIdx.x == 0) route_publish<NT, ROUTED>(a, ra);
   fused_dispatch(pidx, nv, E, s_off, s_used, s_n, s_perm);
   __syncthreads();
-  return deferred;
 }
 
 
@@ -638,7 +630,7 @@ __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) 
       else
         stage_rows_f32<F::NGL>(a.route.x, a.route.d, &zero_row, 1, xs, act_lds_bytes(false, a.route.d));
     }
-    const bool deferred = route_block<NT, ROUTE == 2>(a, prod, ra, s_off, s_used, &s_n, s_perm);
+    route_block<NT, ROUTE == 2>(a, prod, ra, s_off, s_used, &s_n, s_perm);
     EMBER_STAMP(0, 3);
     __syncthreads();
     Dispatch dp{s_n, s_used, s_off, s_perm};
@@ -646,7 +638,6 @@ __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) 
     const bool act = seg_view<GATED, MT, true>(a, dp, blockIdx.x, gridDim.x, v);
     EMBER_STAMP(0, 4);
     if (act) proj_body<FMT, MT, GATED, NB, NT, false, true>(a, dp, v);
-    if (b == 0 && deferred) route_publish<NT, ROUTE == 2>(a, ra, true);
     EMBER_STAMP(0, 7);
   } else {
     Dispatch dp{a.used ? *a.n_used : 0, a.used, a.offsets, a.perm};
