@@ -331,12 +331,37 @@ size_t ember_moe_scratch_bytes(const ember_moe_layer* w, int T) {
 
 namespace {
 // Records ev[i] on the stream at phase boundary i when ev is non-null (ember_moe_ffn_timed).
+// A side stream and its fork / join events, one set per (host thread, device), created on first use
+// (default priority, non-blocking). Null when creation fails: the caller then stays on one stream.
+struct SideStream {
+  hipStream_t s = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+  bool failed = false;
+};
+SideStream* side_stream() {
+  constexpr int kMaxDev = 64;
+  thread_local SideStream tab[kMaxDev];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return nullptr;
+  SideStream& ss = tab[dev];
+  if (!ss.s && !ss.failed) {
+    if (hipStreamCreateWithFlags(&ss.s, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&ss.join, hipEventDisableTiming) != hipSuccess) {
+      ss.failed = true;
+      (void)hipGetLastError();
+    }
+  }
+  return ss.failed ? nullptr : &ss;
+}
+
 inline void mark(hipEvent_t* ev, int i, hipStream_t st) {
   if (ev) hipEventRecord(ev[i], st);
 }
 
+// fork_ok: the shared expert's dense launches may run on a side stream (see run_shared)
 int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* scratch, size_t scratch_bytes,
-            hipStream_t st, hipEvent_t* ev, hipEvent_t* kev = nullptr, int* kev_used = nullptr) {
+            hipStream_t st, hipEvent_t* ev, hipEvent_t* kev = nullptr, int* kev_used = nullptr, bool fork_ok = false) {
   int s = validate(w);
   if (s) return s;
   if (T < 0) return EMBER_ERR_SHAPE;
@@ -425,6 +450,69 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
   // qwen2moe's shared-expert gate logit per token: a one-row router (the same FP64 fixed-order dot)
   float* sg = w->shared_gate ? at<float>(scratch, l.sg) : nullptr;
   if (sg && (s = launch_router_logits(x, T, d, 1, w->shared_gate, sg, st))) return s;
+
+  // The shared expert's dense MFMA launches (its T rows) depend only on the converted activations, not
+  // on the routed launches: when the caller allows it they run on a side stream, forked here after the
+  // routing and joined before the combine, so that their blocks fill the CUs the routed launches leave
+  // idle (their tail rounds) instead of running alone on a few hundred blocks.
+  auto run_shared = [&](hipStream_t sst) -> int {
+    int s = EMBER_OK;
+    _Float16* hs16 = at<_Float16>(scratch, l.hs16);
+    int32_t* hsexp = at<int32_t>(scratch, l.hsexp);
+    GemmArgs g{};
+    g.A = sp_sh ? reinterpret_cast<const _Float16*>(xb) : x16;
+    g.a_exp = sp_sh ? nullptr : xexp;
+    g.h_exp = sp_sh ? nullptr : hsexp;
+    g.split_bf16 = sp_sh;
+    if (pack_bf16_sh) {
+      g.w_exp0 = wexp(bx.sgate);
+      g.w_exp1 = wexp(bx.sup);
+      g.w_hexp = wexp(bx.shmax);
+    }
+    g.a_plane = (int64_t)T * d;
+    g.h_plane = (int64_t)T * w->d_ff_shared;
+    g.T = T;
+    g.W0 = w->gate_shared;
+    g.W1 = w->up_shared;
+    g.type = w->gate_shared_type;
+    g.row_bytes = row_bytes(w->gate_shared_type, d);
+    g.N = w->d_ff_shared;
+    g.K = d;
+    g.out_h = hs16;
+    const bool skinny = l.mode_shared == kSkinny;  // one dense segment of T rows
+    const int mt = skinny ? gemm_skinny_max_tiles(T, 1, 0) : gemm_max_tiles(T, 1, 0);
+    g.ksplit = skinny ? l.ks_sh_gu : 1;
+    g.part_h = g.ksplit > 1 ? at<float>(scratch, l.shpart) : nullptr;
+    g.part_rows = T;
+    if ((s = skinny ? launch_gemm_skinny(g, true, mt, sst) : launch_gemm(g, true, mt, sst))) return s;
+    g.A = hs16;
+    g.a_exp = sp_sh ? nullptr : hsexp;
+    g.h_exp = nullptr;
+    g.a_plane = (int64_t)T * w->d_ff_shared;
+    g.W0 = w->down_shared;
+    g.W1 = nullptr;
+    g.w_exp0 = pack_bf16_sh ? wexp(bx.sdown) : nullptr;
+    g.w_exp1 = nullptr;
+    g.w_hexp = nullptr;
+    g.type = w->down_shared_type;
+    g.row_bytes = row_bytes(w->down_shared_type, w->d_ff_shared);
+    g.N = d;
+    g.K = w->d_ff_shared;
+    g.out_h = nullptr;
+    g.out_y = ys;
+    g.ksplit = skinny ? l.ks_sh_dn : 1;
+    g.part_stride = (int64_t)T * d;
+    g.part_h = nullptr;
+    if ((s = skinny ? launch_gemm_skinny(g, false, mt, sst) : launch_gemm(g, false, mt, sst))) return s;
+    return s;
+  };
+  SideStream* side = shared_mfma && fork_ok ? side_stream() : nullptr;
+  if (side) {
+    if (hipEventRecord(side->fork, st) != hipSuccess || hipStreamWaitEvent(side->s, side->fork, 0) != hipSuccess)
+      return EMBER_ERR_LAUNCH;
+    if ((s = run_shared(side->s))) return s;
+    if (hipEventRecord(side->join, side->s) != hipSuccess) return EMBER_ERR_LAUNCH;
+  }
 
   if (l.mode != kGemv) {
     const bool skinny = l.mode == kSkinny;
@@ -620,53 +708,7 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     mark(ev, 5, st);
   }
   if (shared_mfma) {
-    _Float16* hs16 = at<_Float16>(scratch, l.hs16);
-    int32_t* hsexp = at<int32_t>(scratch, l.hsexp);
-    GemmArgs g{};
-    g.A = sp_sh ? reinterpret_cast<const _Float16*>(xb) : x16;
-    g.a_exp = sp_sh ? nullptr : xexp;
-    g.h_exp = sp_sh ? nullptr : hsexp;
-    g.split_bf16 = sp_sh;
-    if (pack_bf16_sh) {
-      g.w_exp0 = wexp(bx.sgate);
-      g.w_exp1 = wexp(bx.sup);
-      g.w_hexp = wexp(bx.shmax);
-    }
-    g.a_plane = (int64_t)T * d;
-    g.h_plane = (int64_t)T * w->d_ff_shared;
-    g.T = T;
-    g.W0 = w->gate_shared;
-    g.W1 = w->up_shared;
-    g.type = w->gate_shared_type;
-    g.row_bytes = row_bytes(w->gate_shared_type, d);
-    g.N = w->d_ff_shared;
-    g.K = d;
-    g.out_h = hs16;
-    const bool skinny = l.mode_shared == kSkinny;  // one dense segment of T rows
-    const int mt = skinny ? gemm_skinny_max_tiles(T, 1, 0) : gemm_max_tiles(T, 1, 0);
-    g.ksplit = skinny ? l.ks_sh_gu : 1;
-    g.part_h = g.ksplit > 1 ? at<float>(scratch, l.shpart) : nullptr;
-    g.part_rows = T;
-    if ((s = skinny ? launch_gemm_skinny(g, true, mt, st) : launch_gemm(g, true, mt, st))) return s;
-    g.A = hs16;
-    g.a_exp = sp_sh ? nullptr : hsexp;
-    g.h_exp = nullptr;
-    g.a_plane = (int64_t)T * w->d_ff_shared;
-    g.W0 = w->down_shared;
-    g.W1 = nullptr;
-    g.w_exp0 = pack_bf16_sh ? wexp(bx.sdown) : nullptr;
-    g.w_exp1 = nullptr;
-    g.w_hexp = nullptr;
-    g.type = w->down_shared_type;
-    g.row_bytes = row_bytes(w->down_shared_type, w->d_ff_shared);
-    g.N = d;
-    g.K = w->d_ff_shared;
-    g.out_h = nullptr;
-    g.out_y = ys;
-    g.ksplit = skinny ? l.ks_sh_dn : 1;
-    g.part_stride = (int64_t)T * d;
-    g.part_h = nullptr;
-    if ((s = skinny ? launch_gemm_skinny(g, false, mt, st) : launch_gemm(g, false, mt, st))) return s;
+    if (!side && (s = run_shared(st))) return s;
   } else if (shared && !shared_fused) {
     ProjArgs b{};
     b.gated = true;
@@ -689,6 +731,7 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     b.s_out = ys;
     if ((s = launch_projection(b, st))) return s;
   }
+  if (side && hipStreamWaitEvent(st, side->join, 0) != hipSuccess) return EMBER_ERR_LAUNCH;
   mark(ev, 6, st);
   const int ys_parts = shared_mfma && l.mode_shared == kSkinny ? l.ks_sh_dn : 1;
   s = launch_combine(y, ksplit, (int64_t)T * k * d, gates, ds.pos, ys, ys_parts, (int64_t)T * d, sg, out_scale, T, k,
@@ -700,7 +743,7 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
 
 int ember_moe_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* scratch, size_t scratch_bytes,
                   hipStream_t st) {
-  return run_ffn(w, x, T, out, scratch, scratch_bytes, st, nullptr);
+  return run_ffn(w, x, T, out, scratch, scratch_bytes, st, nullptr, nullptr, nullptr, true);
 }
 
 }  // extern "C"
