@@ -222,7 +222,74 @@ __device__ __attribute__((always_inline)) inline int wave_topk_regs(const float*
   return n;
 }
 
+// Largest of a wave's 32-bit values, every lane's (DPP: row_shr 1, 2, 4, 8 within rows of 16 lanes, then
+// row_bcast 15 and 31 across rows; lane 63 ends with the maximum).
+__device__ __attribute__((always_inline)) inline uint32_t wave_max_u32(uint32_t v) {
+  auto step = [](uint32_t x, auto CTRL, auto ROWS) {
+    const uint32_t y = (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, decltype(CTRL)::value,
+                                                             decltype(ROWS)::value, 0xf, false);
+    return x > y ? x : y;
+  };
+  using I = std::integral_constant<int, 0xf>;
+  v = step(v, std::integral_constant<int, 0x111>{}, I{});
+  v = step(v, std::integral_constant<int, 0x112>{}, I{});
+  v = step(v, std::integral_constant<int, 0x114>{}, I{});
+  v = step(v, std::integral_constant<int, 0x118>{}, I{});
+  v = step(v, std::integral_constant<int, 0x142>{}, std::integral_constant<int, 0xa>{});
+  v = step(v, std::integral_constant<int, 0x143>{}, std::integral_constant<int, 0xc>{});
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+// The same selection as wave_topk_regs for small k (E <= 64 Q): the reference's k argmax passes
+// themselves, each a wave maximum of the candidates' order keys (larger value first) and the lowest index
+// holding it (ties to the lower index); picks returned in ascending index order.
+template <int Q>
+__device__ __attribute__((always_inline)) inline int wave_topk_argmax(const float* val, const char* cand, int E, int k,
+                                                                      int* picks) {
+  const int lane = threadIdx.x & 63;
+  E = __builtin_amdgcn_readfirstlane(E);
+  k = __builtin_amdgcn_readfirstlane(k);
+  uint32_t key[Q];
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    const int e = lane + 64 * q;
+    key[q] = e < E && (!cand || cand[e]) ? order_key(val[e]) : 0u;  // a candidate's key is > 0
+  }
+  uint64_t sel[Q];
+#pragma unroll
+  for (int q = 0; q < Q; ++q) sel[q] = 0;
+  for (int j = 0; j < k; ++j) {
+    uint32_t mine = key[0];
+#pragma unroll
+    for (int q = 1; q < Q; ++q) mine = mine > key[q] ? mine : key[q];
+    const uint32_t m = wave_max_u32(mine);
+    if (m == 0u) break;  // fewer candidates than k
+    bool done = false;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      const uint64_t hit = __ballot(key[q] == m);
+      if (!done && hit) {
+        const int l = __builtin_ctzll(hit);
+        sel[q] |= 1ull << l;
+        if (lane == l) key[q] = 0u;
+        done = true;
+      }
+    }
+  }
+  const uint64_t below = (1ull << lane) - 1;
+  int n = 0;
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    if ((sel[q] >> lane) & 1) picks[n + __builtin_popcountll(sel[q] & below)] = lane + 64 * q;
+    n += __builtin_popcountll(sel[q]);
+  }
+  wave_sync_lds();
+  return n;
+}
+
 __device__ __attribute__((always_inline)) inline int wave_topk(const float* val, const char* cand, int E, int k, int* picks) {
+  if (k <= 8 && E <= 64) return wave_topk_argmax<1>(val, cand, E, k, picks);
+  if (k <= 8 && E <= 128) return wave_topk_argmax<2>(val, cand, E, k, picks);
   if (E <= 64) return wave_topk_regs<1>(val, cand, E, k, picks);
   if (E <= 128) return wave_topk_regs<2>(val, cand, E, k, picks);
   if (E <= 256) return wave_topk_regs<4>(val, cand, E, k, picks);
