@@ -356,7 +356,7 @@ SideStream* side_stream() {
 }
 
 inline void mark(hipEvent_t* ev, int i, hipStream_t st) {
-  if (ev) hipEventRecord(ev[i], st);
+  if (ev) (void)hipEventRecord(ev[i], st);  // a failed record shows up as a failed elapsed-time query
 }
 
 // fork_ok: the shared expert's dense launches may run on a side stream (see run_shared)
@@ -808,7 +808,7 @@ int ember_moe_ffn_timed(const ember_moe_layer* w, const float* x, int T, float* 
     if (s == EMBER_OK && (kev_used & 2) && hipEventElapsedTime(&phase_ms[4], ev[10], ev[11]) != hipSuccess)
       s = EMBER_ERR_LAUNCH;
   }
-  for (int i = 0; i < 12; ++i) hipEventDestroy(ev[i]);
+  for (int i = 0; i < 12; ++i) (void)hipEventDestroy(ev[i]);
   return s;
 }
 
