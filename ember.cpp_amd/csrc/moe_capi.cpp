@@ -191,7 +191,7 @@ Layout layout(const ember_moe_layer* w, int T) {
   Layout l;
   const size_t slots = (size_t)T * w->k;
   size_t o = 0;
-  l.flag = o; o = align_up(o + (size_t)8 * (w->E + 2));
+  l.flag = o; o = align_up(o + (size_t)8 * (2 * w->E + 2));
   l.logits = o; o = align_up(o + (size_t)T * w->E * 4);
   l.idx = o; o = align_up(o + slots * 4);
   l.gates = o; o = align_up(o + slots * 4);
@@ -663,7 +663,7 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
       b.scale = out_scale;
       b.out = out;
       b.clear_flag = fuse_route ? flag + 2 : nullptr;
-      b.clear_n = E;
+      b.clear_n = 2 * E;
       if ((s = launch_projection(a, st))) return s;
       mark(ev, 4, st);
       if (kev) {
@@ -681,7 +681,7 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     mark(ev, 4, st);
     a.route = ProjArgs::Route{};
     a.clear_flag = fuse_route ? flag + 2 : nullptr;  // the down launch resets the logit words for the next call
-    a.clear_n = E;
+    a.clear_n = 2 * E;
     a.type = w->down_type;
     a.gated = false;
     a.w0 = w->down;
@@ -827,6 +827,7 @@ int ember_moe_scratch_routing(const ember_moe_layer* w, int T, ember_moe_routing
   v->used = l.r.used;
   v->n_used = l.r.n_used;
   v->fallbacks = l.flag;
+  v->mismatches = l.flag + 8;
   return EMBER_OK;
 }
 

@@ -331,11 +331,35 @@ __device__ inline void proj_body(const ProjArgs& a, const Dispatch& dp, const Se
 }
 
 // ---- routing fused into a one-token gate/up launch (ProjArgs::route)
-// Words of the flag area: [0], [1] unused; [2 + e] expert e's logit under kLogitTag (the f32 bits in
-// the low half). A word is read with one device-coherent load and carries its own data, so no
+// Words of the flag area: [0] the count of blocks that computed a missing logit themselves, [1] the
+// count of calls whose exact picks differed from the fast ones; [2 + e] expert e's logit under
+// kLogitTag (the f32 bits in the low half). A word is read with one device-coherent load and carries its own data, so no
 // ordering between a payload and a flag is needed.
 constexpr int kFusedMaxK = 8;
 constexpr uint32_t kLogitTag = 0x10617ed5u;
+// Words [2 + E + e]: expert e's fast logit under kFastTag — the same exact products summed as a tree (so
+// available ~4 us before the reference's eight chains are added), as binary32 with the low 8 mantissa
+// bits replaced by a bound: |fast - the reference's double logit| <= 2^(low byte - 160) (255: no bound).
+constexpr uint32_t kFastTag = 0x0fa57106u;
+
+// The fast word of a logit whose exact products sum to s (tree order) with sum |p| = S, for a dot of
+// nq groups of eight. Bound (Higham, recursive sums): a sum of exact terms whose every term passes
+// through at most D additions is within D u / (1 - D u) * S of the true sum, u = 2^-53. The tree's D is
+// at most 16 products per thread + 7 tail products + 6 wave levels + 16 wave partials = 45; the
+// reference's chains add nq terms, then 3 combining levels and the tail (an fma chain of at most 7
+// exact products, then one add): D <= nq + 11. 2 (nq + 64) u S covers both with room for the rounding
+// of S itself; truncating the binary32 value to 16 significant bits adds at most 2^-14 |s| + 2^-140.
+__device__ inline unsigned long long fast_word(double s, double S, int nq) {
+  const float f = (float)s;
+  uint32_t eb = 255;
+  const double B = 2.0 * (double)(nq + 64) * 0x1p-53 * S + fabs(s) * 0x1p-14 + 0x1p-140;
+  if (__builtin_isfinite(f) && __builtin_isfinite(B)) {
+    // B >= 2^-140 is a normal double: its exponent field is floor(log2 B), so 2^ex > B
+    const int ex = (int)((__builtin_bit_cast(unsigned long long, B) >> 52) & 0x7ff) - 1023 + 1;
+    eb = ex + 160 < 0 ? 0u : ex + 160 > 254 ? 255u : (uint32_t)(ex + 160);
+  }
+  return ((unsigned long long)kFastTag << 32) | (__builtin_bit_cast(uint32_t, f) & 0xffffff00u) | eb;
+}
 // LDS of a router block (the products, f64, chain-major) and, after it, every block's routing area
 // (logits, picks, gates, one routing wave's work area)
 __host__ __device__ inline size_t fused_router_lds(int d) { return (size_t)8 * d + 8 * 8 * 6 + 256; }
@@ -350,7 +374,7 @@ __host__ __device__ inline size_t fused_x_lds(int type, int d) {
 // Every product (exact in f64) is formed from one round of 16-byte loads and stored chain-major, then
 // eight lanes add their chain's products in order — the rounding sequence of acc += (double)r * (double)x.
 // Returns the logit in thread 0.
-template <int NT>
+template <int NT, bool FAST>
 __device__ float router_block_logit(const ProjArgs& a, int e, uint8_t* lds) {
   const ProjArgs::Route& r = a.route;
   const int t = threadIdx.x, d = r.d, n8 = d - d % 8, nq = n8 / 8;
@@ -359,6 +383,9 @@ __device__ float router_block_logit(const ProjArgs& a, int e, uint8_t* lds) {
   const int ld = (nq + 3) / 4 * 4 + 2;
   double* pd = reinterpret_cast<double*>(lds);
   const float* row = r.router + (size_t)e * d;
+  constexpr int NW = NT / 64;
+  __shared__ double fpart[2 * NW];
+  double fs = 0.0, fa = 0.0;  // this thread's products: sum, sum of magnitudes (the fast word)
   if (d % 4 == 0) {
     constexpr int PER = 4;  // float4s per thread: d <= 16 * NT
     const int n4 = n8 / 4;
@@ -376,16 +403,50 @@ __device__ float router_block_logit(const ProjArgs& a, int e, uint8_t* lds) {
       const int i4 = t + j * NT;
       if (i4 < n4) {
         const int c0 = (4 * i4) & 7, q = i4 >> 1;
-        pd[(c0 + 0) * ld + q] = (double)rv[j].x * (double)xv[j].x;
-        pd[(c0 + 1) * ld + q] = (double)rv[j].y * (double)xv[j].y;
-        pd[(c0 + 2) * ld + q] = (double)rv[j].z * (double)xv[j].z;
-        pd[(c0 + 3) * ld + q] = (double)rv[j].w * (double)xv[j].w;
+        const double p0 = (double)rv[j].x * (double)xv[j].x, p1 = (double)rv[j].y * (double)xv[j].y;
+        const double p2 = (double)rv[j].z * (double)xv[j].z, p3 = (double)rv[j].w * (double)xv[j].w;
+        pd[(c0 + 0) * ld + q] = p0;
+        pd[(c0 + 1) * ld + q] = p1;
+        pd[(c0 + 2) * ld + q] = p2;
+        pd[(c0 + 3) * ld + q] = p3;
+        fs = fs + p0 + p1 + p2 + p3;
+        fa = fa + fabs(p0) + fabs(p1) + fabs(p2) + fabs(p3);
       }
     }
   } else {
-    for (int i = t; i < n8; i += NT) pd[(i & 7) * ld + (i >> 3)] = (double)row[i] * (double)r.x[i];
+    for (int i = t; i < n8; i += NT) {
+      const double p = (double)row[i] * (double)r.x[i];
+      pd[(i & 7) * ld + (i >> 3)] = p;
+      fs = fs + p;
+      fa = fa + fabs(p);
+    }
+  }
+  if constexpr (FAST) {
+    if (t == 0)
+      for (int i = n8; i < d; ++i) {
+        const double p = (double)row[i] * (double)r.x[i];
+        fs = fs + p;
+        fa = fa + fabs(p);
+      }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      fs = fs + __shfl_xor(fs, off, 64);
+      fa = fa + __shfl_xor(fa, off, 64);
+    }
+    if ((t & 63) == 0) {
+      fpart[t >> 6] = fs;
+      fpart[NW + (t >> 6)] = fa;
+    }
   }
   __syncthreads();
+  if (FAST && (t == 64 || (NT == 64 && t == 0))) {  // the fast word, published while wave 0 adds the chains
+    double s = 0.0, S = 0.0;
+    for (int w = 0; w < NW; ++w) {
+      s = s + fpart[w];
+      S = S + fpart[NW + w];
+    }
+    __hip_atomic_store(r.flag + 2 + r.E + e, fast_word(s, S, nq), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
   double acc = 0.0;
   if (t < 8) {
     // the chain in order, in bursts of 16 products (8 pair reads) held in two alternating buffers: one
@@ -522,6 +583,101 @@ __device__ float router_logit_slow(const ProjArgs& a, int e, uint8_t* lds) {
   return v;
 }
 
+// The softmax router's pick set from the fast words, when they prove it. The reference picks the top k
+// of the binary32 logits r_e = (float)c_e (c_e its double dot), ties to the lower index, ascending. With
+// every c_e in [v_e - h_e, v_e + h_e] (the fast words), the top k of the v_e (same tie rule) are the
+// picks when the lowest lower bound among them, m1, and the highest upper bound among the others, m2,
+// satisfy m1 - m2 > 2^-22 max(|m1|, |m2|) + 2^-140: then every picked c_e and unpicked c_u round to
+// binary32 values r_e > r_u (rounding is monotone and moves each by at most half an ulp, an ulp being
+// <= 2^-23 |x| for normal x and 2^-149 below), so no tie can reorder them. Returns false (block-uniform)
+// when a word is missing after the wait's bound, carries no bound, or the margin is too small; the
+// caller then routes from the exact logits. On true the block's one-token dispatch is built.
+template <int NT>
+__device__ bool fast_route(const ProjArgs& a, uint8_t* ra, int32_t* s_off, int32_t* s_used, int32_t* s_n,
+                           int32_t* s_perm) {
+  __shared__ float fv[kMaxRouteE];
+  __shared__ uint8_t feb[kMaxRouteE];
+  __shared__ int s_ok;
+  const ProjArgs::Route& r = a.route;
+  int32_t* pidx = reinterpret_cast<int32_t*>(ra + 2048);
+  const int t = threadIdx.x, E = r.E, kk = min(a.k, r.E);
+  if (t == 0) s_ok = 1;
+  __syncthreads();
+  for (int e = t; e < E; e += NT) {
+    unsigned long long w;
+    unsigned n = 0;
+    while (((w = __hip_atomic_load(r.flag + 2 + E + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) >> 32) !=
+           kFastTag) {
+      if (++n > r.spin_limit) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    const float v = __builtin_bit_cast(float, (uint32_t)w & 0xffffff00u);
+    if ((w >> 32) != kFastTag || (w & 0xff) == 0xff || v != v) s_ok = 0;
+    fv[e] = v;
+    feb[e] = (uint8_t)(w & 0xff);
+  }
+  __syncthreads();
+  if (!s_ok) return false;
+  if (t < 64) {
+    const int n = wave_topk(fv, nullptr, E, kk, pidx);
+    double lo = __builtin_inf(), hi = -__builtin_inf();
+    for (int e = t; e < E; e += 64) {
+      bool picked = false;
+      for (int j = 0; j < n; ++j) picked |= pidx[j] == e;
+      const double h = __builtin_bit_cast(double, (unsigned long long)((int)feb[e] - 160 + 1023) << 52);  // 2^(b-160)
+      if (picked)
+        lo = fmin(lo, (double)fv[e] - h);
+      else
+        hi = fmax(hi, (double)fv[e] + h);
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      lo = fmin(lo, __shfl_xor(lo, off, 64));
+      hi = fmax(hi, __shfl_xor(hi, off, 64));
+    }
+    const bool ok = n == kk && (kk == E || lo - hi > 0x1p-22 * fmax(fabs(lo), fabs(hi)) + 0x1p-140);
+    if (t == 0) s_ok = ok;
+  }
+  __syncthreads();
+  if (!s_ok) return false;
+  fused_dispatch(pidx, kk, E, s_off, s_used, s_n, s_perm);
+  __syncthreads();
+  return true;
+}
+
+// Block 0's check of the other blocks' fast pick sets against its exact picks (used[0 .. n)). A set
+// proven from the fast words differs from the exact one only if some unpicked expert's lower bound
+// lies above some picked expert's upper bound: the exact logits would then break the bounds. Such a
+// contradiction (never expected) is counted in the flag area's word 1. Words not (yet) published are
+// skipped: the blocks that missed them routed from the exact logits.
+template <int NT>
+__device__ void fast_check(const ProjArgs& a, const int32_t* used, int n) {
+  const ProjArgs::Route& r = a.route;
+  const int t = threadIdx.x;
+  if (t < 64) {
+    double lo_out = -__builtin_inf(), hi_in = __builtin_inf();  // bounds of the unpicked / picked
+    for (int e = t; e < r.E; e += 64) {
+      const unsigned long long w = __hip_atomic_load(r.flag + 2 + r.E + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if ((w >> 32) != kFastTag || (w & 0xff) == 0xff) continue;
+      const double v = (double)__builtin_bit_cast(float, (uint32_t)w & 0xffffff00u);
+      const double h = __builtin_bit_cast(double, (unsigned long long)((int)(w & 0xff) - 160 + 1023) << 52);
+      bool picked = false;
+      for (int j = 0; j < n; ++j) picked |= used[j] == e;
+      if (picked)
+        hi_in = fmin(hi_in, v + h);
+      else
+        lo_out = fmax(lo_out, v - h);
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      hi_in = fmin(hi_in, __shfl_xor(hi_in, off, 64));
+      lo_out = fmax(lo_out, __shfl_xor(lo_out, off, 64));
+    }
+    if (t == 0 && lo_out > hi_in)
+      __hip_atomic_fetch_add(r.flag + 1, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 template <int NT, bool ROUTED>
 __device__ void route_block(const ProjArgs& a, uint8_t* lds, uint8_t* ra, int32_t* s_off, int32_t* s_used,
                             int32_t* s_n, int32_t* s_perm) {
@@ -615,7 +771,7 @@ __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) 
     if (threadIdx.x == 0) zero_row = 0;
     if (threadIdx.x < 64) route_stage_tables(ra + 2048 + 512);
     if (b < a.route.E && !a.route.no_publish) {  // router block: its expert's logit, published tagged
-      const float v = router_block_logit<NT>(a, b, prod);
+      const float v = router_block_logit<NT, ROUTE == 1>(a, b, prod);
       EMBER_STAMP(0, 1);
       if (threadIdx.x == 0) {
         __hip_atomic_store(a.route.flag + 2 + b, ((unsigned long long)kLogitTag << 32) | __builtin_bit_cast(uint32_t, v),
@@ -630,12 +786,29 @@ __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) 
       else
         stage_rows_f32<F::NGL>(a.route.x, a.route.d, &zero_row, 1, xs, act_lds_bytes(false, a.route.d));
     }
-    route_block<NT, ROUTE == 2>(a, prod, ra, s_off, s_used, &s_n, s_perm);
+    // softmax router: the pick set from the fast words when they prove it (block 0 then writes the
+    // exact routing record after its rows); otherwise, and for the DeepSeek-style router, from the
+    // exact logits
+    bool fast = false;
+    if constexpr (ROUTE == 1) {
+      if (b != 0) fast = fast_route<NT>(a, ra, s_off, s_used, &s_n, s_perm);
+    }
+    if (!fast) route_block<NT, ROUTE == 2>(a, prod, ra, s_off, s_used, &s_n, s_perm);
+    if constexpr (ROUTE == 1) {
+      if (b == 0) {
+        // block 0 routes from the exact logits (and writes the record); the pick set the other blocks
+        // may have proven from the fast words must be the same: a difference (never expected) is
+        // counted in the flag area's word 1, which the routing readback exposes
+        fast_check<NT>(a, s_used, s_n);
+      }
+    }
     EMBER_STAMP(0, 3);
     __syncthreads();
     Dispatch dp{s_n, s_used, s_off, s_perm};
     SegView v;
-    const bool act = seg_view<GATED, MT, true>(a, dp, blockIdx.x, gridDim.x, v);
+    // softmax router: block 0 (the exact routing and its record) takes no rows; blocks 1 .. G-1 share them
+    constexpr int B0 = ROUTE == 1 ? 1 : 0;
+    const bool act = b >= B0 && seg_view<GATED, MT, true>(a, dp, b - B0, gridDim.x - B0, v);
     EMBER_STAMP(0, 4);
     if (act) proj_body<FMT, MT, GATED, NB, NT, false, true>(a, dp, v);
     EMBER_STAMP(0, 7);

@@ -114,7 +114,7 @@ struct ProjArgs {
   // uninitialised scratch matches a 32-bit tag by chance with probability 2^-32). Word 0 counts the
   // blocks that computed a missing logit themselves.
   struct Route {
-    unsigned long long* flag;  // E + 2 words
+    unsigned long long* flag;  // 2 E + 2 words
     const float* x;       // the token [d]
     const float* router;  // [E][d]
     int d, E, renorm, routed, sigmoid, groups_n, groups_top;

@@ -63,7 +63,8 @@ class RoutingView(ctypes.Structure):
     """ember_moe_routing_view (include/ember_moe.h): byte offsets of a call's routing in its scratch."""
 
     _fields_ = [(n, ctypes.c_size_t) for n in
-                ("logits", "idx", "gates", "offsets", "perm", "pos", "used", "n_used", "fallbacks")]
+                ("logits", "idx", "gates", "offsets", "perm", "pos", "used", "n_used", "fallbacks",
+                 "mismatches")]
 
 
 _lib = None
@@ -278,7 +279,7 @@ def moe_ffn(layer: Layer, x, T: int, out, scratch, scratch_nbytes: Optional[int]
 
 def scratch_routing(layer: Layer, T: int, scratch) -> dict:
     """The routing a completed ember_moe_ffn call left in `scratch` (a uint8 device tensor), copied to the
-    host: logits [T][E], idx / gates [T][k], offsets [E+1], perm / pos [T*k], used [n_used], fallbacks."""
+    host: logits [T][E], idx / gates [T][k], offsets [E+1], perm / pos [T*k], used [n_used], fallbacks, mismatches."""
     v = RoutingView()
     st = lib().ember_moe_scratch_routing(ctypes.byref(layer), T, ctypes.byref(v))
     if st:
@@ -294,7 +295,8 @@ def scratch_routing(layer: Layer, T: int, scratch) -> dict:
                 idx=arr(v.idx, T * k, np.int32).reshape(T, k), gates=arr(v.gates, T * k, np.float32).reshape(T, k),
                 offsets=arr(v.offsets, E + 1, np.int32), perm=arr(v.perm, T * k, np.int32),
                 pos=arr(v.pos, T * k, np.int32), used=arr(v.used, max(min(n_used, E), 0), np.int32),
-                n_used=n_used, fallbacks=int(arr(v.fallbacks, 1, np.uint64)[0]))
+                n_used=n_used, fallbacks=int(arr(v.fallbacks, 1, np.uint64)[0]),
+                mismatches=int(arr(v.mismatches, 1, np.uint64)[0]))
 
 
 NOALLOC_SCRATCH_BYTES = 32 << 20  # EMBER_MOE_NOALLOC_SCRATCH_BYTES

@@ -75,9 +75,13 @@ size_t ember_moe_scratch_bytes(const ember_moe_layer* w, int T);
  *                          blocks that stopped waiting for another block's router logit and computed it
  *                          themselves (results are identical either way; a diagnostic that only grows,
  *                          from whatever the buffer held, and is never reset by the library).
+ *   mismatches u64         one-token calls with a softmax router: the number of calls whose exact
+ *                          routing differed from the pick set the expert launch proved from its fast
+ *                          logits (never expected: a nonzero count means a wrong result; it only
+ *                          grows, from whatever the buffer held).
  * The same layout holds for every call with this descriptor and T. */
 typedef struct ember_moe_routing_view {
-  size_t logits, idx, gates, offsets, perm, pos, used, n_used, fallbacks;
+  size_t logits, idx, gates, offsets, perm, pos, used, n_used, fallbacks, mismatches;
 } ember_moe_routing_view;
 int ember_moe_scratch_routing(const ember_moe_layer* w, int T, ember_moe_routing_view* view);
 

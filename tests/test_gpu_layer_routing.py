@@ -42,6 +42,9 @@ def _check_routing(hl, x, r):
     assert np.array_equal(r["pos"], want_pos)
     used = np.flatnonzero(np.diff(offsets) > 0).astype(np.int32)
     assert r["n_used"] == used.size and np.array_equal(r["used"], used)
+    # one token, softmax router: the pick set the expert launch proved from its fast logits equalled the
+    # exact routing's (the scratch starts zeroed)
+    assert r["mismatches"] == 0
 
 
 def _run(dl, x):
@@ -95,18 +98,48 @@ def _edge_layer(T, kind):
         R[6] = -1e37 * s
     elif kind == "nan":
         x[0, 7] = np.nan  # token 0: every logit NaN
+    elif kind == "near":
+        # logits closer than the fast logits' bound: expert 2 differs from expert 1 in one weight's last
+        # bits, expert 4 by a relative 1e-6, expert 7 by 1e-3 (far enough to be proven apart)
+        R[2] = R[1]
+        R[2, 0] = np.nextafter(np.nextafter(R[1, 0], np.float32(np.inf)), np.float32(np.inf))
+        R[4] = R[1] * np.float32(1 + 1e-6)
+        R[7] = R[1] * np.float32(1 + 1e-3)
     hl.router = np.ascontiguousarray(R.reshape(-1))
     return hl, x
 
 
-@pytest.mark.parametrize("kind", ["ties", "inf", "nan"])
+@pytest.mark.parametrize("kind", ["ties", "inf", "nan", "near"])
 @pytest.mark.parametrize("T", [1, 2, 5, 8])
 def test_layer_routing_edges(gpu, kind, T):
     hl, x = _edge_layer(T, kind)
     dl = em.DeviceLayer.upload(hl)
     print(f"layer routing edge {kind} T={T}", flush=True)
-    _, r = _run(dl, x)
+    y, r = _run(dl, x)
     _check_routing(hl, x, r)
+    if kind in ("ties", "near"):
+        assert rel_l2(y, run_oracle(hl, x)) < 1e-5
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_one_token_near_ties(gpu, seed):
+    """One token whose k-th and (k+1)-th logits are nearly equal, at gaps from far below to far above
+    what the fast logits can resolve: the exact routing decides wherever the proof cannot."""
+    spec = em.LayerSpec(d=512, d_ff=256, E=8, k=2, wtype=em.F32, seed=200 + seed)
+    hl = em.make_host_layer(spec)
+    x = em.make_input(spec, 1, seed=300 + seed)
+    R = hl.router.reshape(spec.E, spec.d)
+    lg = O.router_logits(x, hl.router)[0]
+    order = np.argsort(-lg, kind="stable")
+    a, b = order[1], order[2]  # the second pick and the best unpicked expert
+    gap = [0.0, 1e-9, 1e-7, 1e-5, 1e-4, 1e-3][seed % 6] * (1 if seed % 12 < 6 else -1)
+    R[b] = R[a] * np.float32(1 + gap)  # expert b's logit ~ (1 + gap) times expert a's
+    hl.router = np.ascontiguousarray(R.reshape(-1))
+    dl = em.DeviceLayer.upload(hl)
+    print(f"near tie seed={seed} gap={gap}", flush=True)
+    y, r = _run(dl, x)
+    _check_routing(hl, x, r)
+    assert rel_l2(y, run_oracle(hl, x)) < 1e-5
 
 
 FULL = {
