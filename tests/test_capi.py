@@ -136,3 +136,25 @@ def test_prefill_pack_sizes_and_validation():
     assert em.scratch_bytes(_layer(prefill_pack=0x100000), 1) > 0
     assert em.scratch_bytes(_layer(prefill_pack=0x100010), 1) == 0
     assert em.scratch_bytes(_layer(prefill_pack=0x100000, down_type=em.BF16), 1) == 0
+
+
+@pytest.mark.parametrize("E,k,T", [(8, 2, 1), (8, 2, 9), (128, 8, 1), (64, 6, 4)])
+def test_scratch_routing_view_layout(E, k, T):
+    """ember_moe_scratch_routing (host arithmetic only): every section of the routing record lies inside
+    the scratch, 4-byte aligned and disjoint from the others; the two u64 counters are adjacent words at
+    the start of the flag area, whose 2E + 2 words (the counters, then one-token routing's exact and fast
+    logit words) end before the logits."""
+    L = _layer(E=E, k=k, d=512, d_ff=512)
+    need = em.scratch_bytes(L, T)
+    assert need > 0
+    v = em.RoutingView()
+    assert em.lib().ember_moe_scratch_routing(ctypes.byref(L), T, ctypes.byref(v)) == 0
+    assert v.mismatches == v.fallbacks + 8 and v.fallbacks % 8 == 0
+    assert v.fallbacks + 8 * (2 * E + 2) <= v.logits
+    spans = [(v.fallbacks, 8 * (2 * E + 2)), (v.logits, 4 * T * E), (v.idx, 4 * T * k), (v.gates, 4 * T * k),
+             (v.offsets, 4 * (E + 1)), (v.perm, 4 * T * k), (v.pos, 4 * T * k), (v.used, 4 * E), (v.n_used, 4)]
+    for off, n in spans:
+        assert off % 4 == 0 and off + n <= need, (off, n, need)
+    spans.sort()
+    for (o1, n1), (o2, _) in zip(spans, spans[1:]):
+        assert o1 + n1 <= o2, (o1, n1, o2)
