@@ -34,12 +34,12 @@ int path_mode(int type_in, int K_in, int type_out, int K_out, double avg_m, int 
     return s == "gemv" ? kGemv : s == "skinny" ? kSkinny : s == "gemm" ? kGemm : -1;
   }();
   if (forced >= 0) return forced;
-  // Q8_0 (its DMA tile kernels): the GEMV up to 1.5 tokens per expert (C2 T = 4: GEMV 255 vs 291 us;
-  // T = 8: 382 vs 342-359 us), then the 256-token-tile kernel, which skips the empty 32-row subtiles of
-  // a short segment and measured even with or ahead of the 64-token tiles from T = 8 on (C2 T = 32: 361
-  // vs 387 us with the prefill pack, 447 vs 483 without; T = 256: 498 vs 612)
+  // Q8_0 (its DMA tile kernels): the GEMV up to 1 token per expert, then the 256-token-tile kernel,
+  // which skips the empty 32-row subtiles of a short segment (C2, GEMV / 64-token / 256-token tiles:
+  // T = 4 253 / 288 / 261 us, T = 5 282 / 280 / 261, T = 6 347 / 335 / 305, T = 8 382 / 335 / 308,
+  // T = 12 531 / 341 / 311; T = 32 361 vs 387 us on the 64-token tiles with the prefill pack)
   const bool q8 = type_in == EMBER_TYPE_Q8_0 && type_out == EMBER_TYPE_Q8_0;
-  if (q8) return avg_m <= 1.5 ? kGemv : kGemm;
+  if (q8) return avg_m <= 1.0 ? kGemv : kGemm;
   // (packed BF16: row exponents for the fp16 MFMA path, which both tile kernels have; without them BF16 runs
   // the split bf16 MFMA, which only the 64-token-tile kernel implements)
   // packed Q4_K (the same DMA tile kernels): the GEMV up to 1.25 tokens per expert, the 64-token tiles up
