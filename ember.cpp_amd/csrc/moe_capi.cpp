@@ -23,7 +23,8 @@ constexpr int kMaxK = 64;   // picks live in a 64-entry LDS array per wave
 // Expert-product kernels by tokens per expert (M): the int16-dot GEMV while M is at most a few tokens,
 // the skinny MFMA GEMM (64-token tiles) for up to ~100, the 256-token-tile MFMA GEMM beyond.
 enum PathMode { kGemv = 0, kSkinny = 1, kGemm = 2 };
-int path_mode(int type_in, int K_in, int type_out, int K_out, double avg_m, int E, bool packed = false) {
+int path_mode(int type_in, int K_in, int type_out, int K_out, double avg_m, int E, bool packed = false,
+              bool with_shared = false) {
   if (!gemm_supported(type_in, K_in) || !gemm_supported(type_out, K_out)) return kGemv;
   // tuning override: gemv | skinny | gemm (read per call, so a test can select each kernel); the shared
   // expert (E = 1 here) reads EMBER_MOE_SHARED_PATH
@@ -42,22 +43,26 @@ int path_mode(int type_in, int K_in, int type_out, int K_out, double avg_m, int 
   if (q8) return avg_m <= 1.0 ? kGemv : kGemm;
   // (packed BF16: row exponents for the fp16 MFMA path, which both tile kernels have; without them BF16 runs
   // the split bf16 MFMA, which only the 64-token-tile kernel implements)
-  // packed Q4_K (the same DMA tile kernels): the GEMV up to 1.25 tokens per expert, the 64-token tiles up
-  // to 1.75, the 256-token tiles beyond (Mixtral-shaped: T = 4 GEMV 182 vs 258 (64), T = 6 280 vs 205
-  // (64), T = 8 345 (64) vs 278 (256); Qwen-shaped E = 128: T = 16 128 vs 140 (64), T = 24 167 vs 146
-  // (64), T = 32 159 either tiling)
+  // The expected tokens per expert HIT, T*k / (E (1 - (1 - 1/E)^(T*k))): the GEMV's cost follows the
+  // token passes over the hit experts and the MFMA tiles' the hit experts' weights.
+  const double slots = avg_m * E;
+  const double hit = slots > 0.0 ? E * (1.0 - std::pow(1.0 - 1.0 / E, slots)) : 0.0;
+  const double per_hit = hit > 0.0 ? slots / hit : 0.0;
+  // packed Q4_K (the same DMA tile kernels): the GEMV up to 1.55 tokens per hit expert, then the
+  // 256-token tiles (Qwen-shaped E = 128, GEMV / 64-token / 256-token tiles: T = 13 (1.47) 114 / 119 / 116
+  // us, T = 14 (1.51) 122 / 119 / 114, T = 16 (1.58) 128 / 118 / 115, T = 24 170 / 155 / 150, T = 48 255 /
+  // 160 / 159; Mixtral-shaped: T = 4 (1.52) GEMV 182 vs 258 on the 64-token tiles, T = 8 345 (64) vs 278
+  // (256))
   if (packed && type_in == EMBER_TYPE_Q4_K && type_out == EMBER_TYPE_Q4_K)
-    return avg_m <= 1.25 ? kGemv : avg_m <= 1.75 ? kSkinny : kGemm;
-  // BF16 / F16: by the expected tokens per expert HIT, T*k / (E (1 - (1 - 1/E)^(T*k))), since the GEMV's
-  // cost follows the token passes over the hit experts and the MFMA tiles' the hit experts' weights; the
-  // GEMV wins up to ~1.5 (C4-shaped routed experts: T = 8 183 vs 184 us, T = 12 254 vs 202; Qwen-shaped
-  // E = 128: T = 12 204 vs 206, T = 16 243 vs 210; Mixtral-shaped: T = 4 430 vs 671, T = 8 821 vs 691)
+    return per_hit <= 1.55 ? kGemv : kGemm;
+  // BF16 / F16: the GEMV up to ~1.55 tokens per hit expert (Qwen-shaped E = 128: T = 12 204 vs 206 us,
+  // T = 16 243 vs 210; Mixtral-shaped: T = 4 430 vs 671, T = 8 821 vs 691), up to 1.2 with a shared expert,
+  // whose dense MFMA launches then run beside the routed ones on a side stream (C4-shaped, GEMV / 64-token
+  // tiles: T = 4 (1.17) 102 / 131 us, T = 5 (1.21) 132 / 128, T = 6 (1.25) 139 / 131, T = 8 166 / 132)
   const bool half = (type_in == EMBER_TYPE_BF16 || type_in == EMBER_TYPE_F16) &&
                     (type_out == EMBER_TYPE_BF16 || type_out == EMBER_TYPE_F16);
   if (half && E > 1) {  // (one matrix, the shared expert: its T rows, the threshold below)
-    const double slots = avg_m * E;
-    const double hit = slots > 0.0 ? E * (1.0 - std::pow(1.0 - 1.0 / E, slots)) : 0.0;
-    if (hit <= 0.0 || slots / hit <= 1.55) return kGemv;
+    if (hit <= 0.0 || per_hit <= (with_shared ? 1.2 : 1.55)) return kGemv;
   } else if (avg_m <= 2.0) {
     return kGemv;
   }
@@ -203,7 +208,8 @@ Layout layout(const ember_moe_layer* w, int T) {
   l.y = o; o = align_up(o + slots * w->d * 4 * kMaxKSplit);
   l.hs = o; o = align_up(o + (size_t)T * w->d_ff_shared * 4);
   l.sg = o; o = align_up(o + (w->shared_gate ? (size_t)T * 4 : 0));
-  l.mode = path_mode(w->gate_type, w->d, w->down_type, w->d_ff, (double)T * w->k / w->E, w->E, w->prefill_pack != nullptr);
+  l.mode = path_mode(w->gate_type, w->d, w->down_type, w->d_ff, (double)T * w->k / w->E, w->E, w->prefill_pack != nullptr,
+                     w->d_ff_shared > 0);
   const bool pack_bf16 = w->prefill_pack && bf16_stacks(w);  // row exponents, also the shared expert's if BF16
   l.mode_shared = w->d_ff_shared > 0 ? path_mode(w->gate_shared_type, w->d, w->down_shared_type, w->d_ff_shared,
                                                  (double)T, 1, pack_bf16 && bf16_shared(w))
