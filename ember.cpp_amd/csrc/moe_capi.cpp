@@ -68,7 +68,11 @@ int path_mode(int type_in, int K_in, int type_out, int K_out, double avg_m, int 
   }
   // (one dense matrix, the shared expert: the 64-token tiles, split over K, up to 1024 rows; C4 shape
   // T = 512: 139 vs 201 us on the 256-token tiles, T = 2048: 234 vs 208)
-  if (avg_m <= (E == 1 ? 1024.0 : 96.0)) return kSkinny;
+  // packed BF16 routed experts: the 256-token tiles from ~32 tokens per expert (C4-shaped, 64-token /
+  // 256-token tiles: T = 256 (24 per expert) 184 / 213 us, T = 512 (48) 270 / 228, T = 1024 426 / 392,
+  // T = 2048 716 / 553)
+  const bool bf16_packed = packed && type_in == EMBER_TYPE_BF16 && type_out == EMBER_TYPE_BF16 && E > 1;
+  if (avg_m <= (E == 1 ? 1024.0 : bf16_packed ? 32.0 : 96.0)) return kSkinny;
   if (type_in == EMBER_TYPE_BF16 && type_out == EMBER_TYPE_BF16 && !packed) return kSkinny;
   return kGemm;
 }
