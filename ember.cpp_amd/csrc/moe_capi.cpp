@@ -35,12 +35,13 @@ int path_mode(int type_in, int K_in, int type_out, int K_out, double avg_m, int 
     return s == "gemv" ? kGemv : s == "skinny" ? kSkinny : s == "gemm" ? kGemm : -1;
   }();
   if (forced >= 0) return forced;
-  // Q8_0 (its DMA tile kernels): the GEMV up to 1 token per expert, then the 256-token-tile kernel,
-  // which skips the empty 32-row subtiles of a short segment (C2, GEMV / 64-token / 256-token tiles:
-  // T = 4 253 / 288 / 261 us, T = 5 282 / 280 / 261, T = 6 347 / 335 / 305, T = 8 382 / 335 / 308,
-  // T = 12 531 / 341 / 311; T = 32 361 vs 387 us on the 64-token tiles with the prefill pack)
+  // Q8_0 (its DMA tile kernels): the GEMV up to 1 token per expert with the prefill pack, 2 without,
+  // then the 256-token-tile kernel, which skips the empty 32-row subtiles of a short segment (C2 with the
+  // pack, GEMV / 64-token / 256-token tiles: T = 4 253 / 288 / 261 us, T = 5 282 / 280 / 261, T = 6 347
+  // / 335 / 305, T = 8 382 / 335 / 308, T = 12 531 / 341 / 311; T = 32 361 vs 387 us on the 64-token
+  // tiles. Without it, GEMV / 256-token tiles: T = 6 345 / 403, T = 8 386 / 404, T = 10 458 / 410)
   const bool q8 = type_in == EMBER_TYPE_Q8_0 && type_out == EMBER_TYPE_Q8_0;
-  if (q8) return avg_m <= 1.0 ? kGemv : kGemm;
+  if (q8) return avg_m <= (packed ? 1.0 : 2.0) ? kGemv : kGemm;
   // (packed BF16: row exponents for the fp16 MFMA path, which both tile kernels have; without them BF16 runs
   // the split bf16 MFMA, which only the 64-token-tile kernel implements)
   // The expected tokens per expert HIT, T*k / (E (1 - (1 - 1/E)^(T*k))): the GEMV's cost follows the
