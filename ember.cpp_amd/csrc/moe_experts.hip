@@ -867,7 +867,8 @@ int launch_proj_fmt(const ProjArgs& a, hipStream_t st) {
   if (row_lds == 0) return EMBER_OK;
   if (row_lds > kProjLdsBytes) return EMBER_ERR_SHAPE;
   // tokens per pass: up to 2 for gate/up (its 4-token variant runs out of registers), up to 4 for down
-  int MT = a.T <= 1 ? 1 : (a.T <= 2 || GATED ? 2 : 4);
+  // (F32 gate/up: four tokens per pass fit the registers; the quantizing formats' two-token limit stays)
+  int MT = a.T <= 1 ? 1 : (a.T <= 2 || (GATED && FMT != EMBER_TYPE_F32) ? 2 : 4);
   while (MT > 1 && MT * row_lds > kProjLdsBytes) MT >>= 1;
   const size_t lds = (size_t)MT * row_lds;
   if (a.route.flag) {  // routing fused into a one-token gate/up launch
