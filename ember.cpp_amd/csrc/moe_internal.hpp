@@ -109,10 +109,12 @@ struct ProjArgs {
   // one expert's router logit and publish it in a tagged word of the flag area (words 2..E+1); every
   // block collects them (a logit still missing after spin_limit polls it computes itself), computes the
   // same picks and gates and builds the one-token dispatch; block 0 also writes the routing and
-  // dispatch (idx, gates, pos, offsets, used, n_used, perm) for the later launches. A later launch of
-  // the same call (clear_flag) zeroes the E logit words, so stale words never carry a tag (a word of
-  // uninitialised scratch matches a 32-bit tag by chance with probability 2^-32). Word 0 counts the
-  // blocks that computed a missing logit themselves.
+  // dispatch (idx, gates, pos, offsets, used, n_used, perm) for the later launches. With the softmax
+  // router each router block also publishes a bounded fast logit (words E+2 .. 2E+1), from which the
+  // other blocks prove the pick set before the exact logits are summed. A later launch of the same call
+  // (clear_flag) zeroes both sets of words, so stale words never carry a tag (a word of uninitialised
+  // scratch matches a 32-bit tag by chance with probability 2^-32). Word 0 counts the blocks that
+  // computed a missing logit themselves, word 1 the calls whose exact picks contradicted the fast bounds.
   struct Route {
     unsigned long long* flag;  // 2 E + 2 words
     const float* x;       // the token [d]
