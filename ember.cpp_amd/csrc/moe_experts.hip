@@ -603,12 +603,15 @@ __device__ bool fast_route(const ProjArgs& a, uint8_t* ra, int32_t* s_off, int32
   const int t = threadIdx.x, E = r.E, kk = min(a.k, r.E);
   if (t == 0) s_ok = 1;
   __syncthreads();
+  // an eighth of the exact words' bound: the exact path follows a give-up (and waits for the same router
+  // block), and the fast words normally land a few microseconds into the launch
+  const unsigned spin = r.spin_limit >> 3;
   for (int e = t; e < E; e += NT) {
     unsigned long long w;
     unsigned n = 0;
     while (((w = __hip_atomic_load(r.flag + 2 + E + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) >> 32) !=
            kFastTag) {
-      if (++n > r.spin_limit) break;
+      if (++n > spin) break;
       __builtin_amdgcn_s_sleep(1);
     }
     const float v = __builtin_bit_cast(float, (uint32_t)w & 0xffffff00u);
