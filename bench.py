@@ -6,8 +6,9 @@ selects the other single-layer configs.
 One step = one ember_moe_ffn call over one batch of T tokens resident in HBM (the headline T is
 --tokens, default the config's first = decode). Prints ONE JSON line. Besides the contract fields it
 carries:
-  roofline      the dominant kernel (gate/up + SwiGLU, HBM-bound; at one token it also runs the router,
-                routing and dispatch before streaming): algorithmic bytes per launch over
+  roofline      the dominant kernel, HBM-bound (the gate/up + SwiGLU kernel; at one token with a prefill pack
+                the slice kernel, which runs the router and routing, then gate/up, SwiGLU and down per
+                64-column slice of d_ff): algorithmic bytes per launch over
                 its average duration, timed with HIP events that the launch records in the kernel's
                 own dispatch packet on the launch stream; `traffic` is the kernel's HBM bytes per launch from the
                 committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary of the same workload (profiles/)
@@ -15,6 +16,8 @@ carries:
                 when present; else the oracle's restatement) on the box's host cores, on a bounded
                 token sample of the same layer
   sweep         the other token counts of config 2 (µs/layer, tokens/s, roofline fractions)
+  c1, c3, c4    (default c2 run) the other single-layer configs' own sweeps, same fields
+  c5            (default c2 run) the end-to-end config 5 model: prefill + greedy decode tokens/s
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--config c2] [--tokens 1] [--sweep 1,8,128,2048]
 """
@@ -80,20 +83,75 @@ def realised_experts(em, dl, x, T):
     return int(np.unique(idx.cpu().numpy()).size)
 
 
-def algorithmic(spec, T, U):
-    """Algorithmic HBM bytes of the gate/up launch and of the whole layer (U = realised experts hit,
-    shared expert included), and the layer's flops (routed rows only)."""
+def algorithmic(spec, T, U, path_bits=0):
+    """Algorithmic HBM bytes of the dominant expert launch and of the whole layer (U = realised experts
+    hit, shared expert included, weights counted in their ggml encoding), and the layer's flops (routed
+    rows and the shared expert). The dominant launch is the gate/up + SwiGLU kernel, or, on the one-token
+    slice path (path_bits & PATH_SLICES), the slice kernel: gate/up, SwiGLU and down for every pick, plus
+    its partial output rows (k * d_ff / 64 rows of d floats written)."""
     import ember_moe as em
 
     d, dff, k, E = spec.d, spec.d_ff, spec.k, spec.E
     bpw = BPW[em.TYPE_NAMES[spec.wtype]]
     dsh = spec.d_ff_shared
-    gu = U * 2 * d * dff * bpw + T * k * d * 4 + T * k * dff * 4
-    if T == 1:
-        gu += E * d * 4  # one token: the router, routing and dispatch run inside the gate/up launch
+    if path_bits & em.PATH_SLICES:
+        gu = U * 3 * d * dff * bpw + k * (dff // 64) * d * 4 + d * 4 + E * d * 4
+    else:
+        gu = U * 2 * d * dff * bpw + T * k * d * 4 + T * k * dff * 4
+        if T == 1:
+            gu += E * d * 4  # one token: the router, routing and dispatch run inside the gate/up launch
     layer = (U * 3 * d * dff + 3 * d * dsh) * bpw + E * d * 4 + 2 * T * d * 4
     flops = 2.0 * T * (k * 3 * d * dff + 3 * d * dsh) + 2.0 * T * E * d
     return gu, layer, flops
+
+
+def run_sweep(em, spec, dl, sweep_T, steps, warmup, log_prefix="[bench]"):
+    """Per token count: eager and graph timing of the layer call, per-phase times and the roofline
+    fractions; returns {T: entry}."""
+    import torch
+
+    results = {}
+    for T in sweep_T:
+        x_host = em.make_input(spec, T)
+        x = torch.from_numpy(x_host).cuda()
+        U = realised_experts(em, dl, x, T)
+        bits = em.path(dl.desc, T)
+        eager_ms, graph_ms, phases, _ = time_layer(em, dl, x, T, steps, warmup)
+        best_ms = min(eager_ms, graph_ms) if graph_ms else eager_ms
+        gu_bytes, layer_bytes, flops = algorithmic(spec, T, U, bits)
+        gu_ms = phases["gate_up"]
+        results[T] = dict(T=T, experts_hit=U, path_bits=bits, us_per_layer=best_ms * 1e3, eager_us=eager_ms * 1e3,
+                          layer_mfma_frac=flops / (best_ms * 1e-3) / (MFMA_PEAK_TFLOPS * 1e12),
+                          graph_us=None if graph_ms is None else graph_ms * 1e3, tokens_per_s=T / (best_ms * 1e-3),
+                          layer_hbm_frac=layer_bytes / (best_ms * 1e-3) / (HBM_PEAK_GBS * 1e9),
+                          gate_up_us=gu_ms * 1e3, gate_up_gbs=gu_bytes / (gu_ms * 1e-3) / 1e9,
+                          gate_up_hbm_frac=gu_bytes / (gu_ms * 1e-3) / (HBM_PEAK_GBS * 1e9),
+                          layer_tflops=flops / (best_ms * 1e-3) / 1e12,
+                          phases_us={p: round(v * 1e3, 2) for p, v in phases.items()})
+        log(f"{log_prefix} T={T}: {json.dumps(results[T])}")
+    return results
+
+
+def nested_config(em, name, steps, warmup):
+    """Another BASELINE layer config's own sweep (its token counts), with the prefill pack where the layer
+    has one, for the default run's JSON line."""
+    import torch
+
+    spec = layer_spec(name)
+    t0 = time.time()
+    hl = em.make_host_layer(spec)
+    dl = em.DeviceLayer.upload(hl)
+    if em.prefill_pack_bytes(dl.desc) > 0:
+        dl.tensors["pack"] = torch.empty(em.prefill_pack_bytes(dl.desc), dtype=torch.uint8, device="cuda")
+        em.prefill_pack(dl.desc, dl.tensors["pack"])
+    torch.cuda.synchronize()
+    log(f"[bench {name}] layer ready in {time.time() - t0:.1f}s")
+    desc, _, tokens = CONFIGS[name]
+    res = run_sweep(em, spec, dl, tokens, steps, warmup, log_prefix=f"[bench {name}]")
+    out = {"workload": desc, "sweep": [res[T] for T in tokens]}
+    del dl
+    torch.cuda.empty_cache()
+    return out
 
 
 def time_layer(em, dl, x, T, steps, warmup):
@@ -271,6 +329,7 @@ def main():
     ap.add_argument("--sweep", type=str, default=None, help="comma-separated token counts (default: the config's)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-c5", action="store_true", help="skip the end-to-end config 5 run the default c2 run adds")
+    ap.add_argument("--no-nested", action="store_true", help="skip the config 1 / 3 / 4 sweeps the default c2 run adds")
     ap.add_argument("--no-pack", action="store_true",
                     help="run prefill without the prefill pack (Q8_0 / Q4_K tiles, BF16 row exponents)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -320,26 +379,9 @@ def main():
     torch.cuda.synchronize()
 
     sweep_T = sorted(set([args.tokens] + [int(t) for t in args.sweep.split(",") if t]))
-    results = {}
-    for T in sweep_T:
-        x_host = em.make_input(spec, T)
-        x = torch.from_numpy(x_host).cuda()
-        U = realised_experts(em, dl, x, T)
-        eager_ms, graph_ms, phases, _ = time_layer(em, dl, x, T, args.steps, args.warmup)
-        best_ms = min(eager_ms, graph_ms) if graph_ms else eager_ms
-        gu_bytes, layer_bytes, flops = algorithmic(spec, T, U)
-        gu_ms = phases["gate_up"]
-        results[T] = dict(T=T, experts_hit=U, us_per_layer=best_ms * 1e3, eager_us=eager_ms * 1e3,
-                          layer_mfma_frac=flops / (best_ms * 1e-3) / (MFMA_PEAK_TFLOPS * 1e12),
-                          graph_us=None if graph_ms is None else graph_ms * 1e3, tokens_per_s=T / (best_ms * 1e-3),
-                          layer_hbm_frac=layer_bytes / (best_ms * 1e-3) / (HBM_PEAK_GBS * 1e9),
-                          gate_up_us=gu_ms * 1e3, gate_up_gbs=gu_bytes / (gu_ms * 1e-3) / 1e9,
-                          layer_tflops=flops / (best_ms * 1e-3) / 1e12,
-                          phases_us={p: round(v * 1e3, 2) for p, v in phases.items()})
-        log(f"[bench] T={T}: {json.dumps(results[T])}")
+    results = run_sweep(em, spec, dl, sweep_T, args.steps, args.warmup)
 
     h = results[args.tokens]
-    gu_bytes, _, flops = algorithmic(spec, args.tokens, h["experts_hit"])
     line = {
         "metric": "MoE-FFN tokens/s (" + args.config + ")",
         "value": h["tokens_per_s"],
@@ -358,14 +400,26 @@ def main():
                    "tokens": args.tokens, "d": spec.d, "d_ff": spec.d_ff, "E": spec.E, "k": spec.k,
                    "mode": (f"hipgraph ({GRAPH_CALLS} calls per graph)" if h["graph_us"] is not None and h["graph_us"] <= h["eager_us"] else "eager"),
                    "prefill_pack": packed},
-        "roofline": {"kernel": f"gate/up + SwiGLU expert kernel ({em.TYPE_NAMES[spec.wtype]})"
-                               + (", router + routing fused in (one token)" if args.tokens == 1 else ""), "bound": "hbm",
-                     "achieved": h["gate_up_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        "roofline": {"kernel": (f"one-token slice kernel ({em.TYPE_NAMES[spec.wtype]}): router + routing, then per "
+                                f"64-column slice of d_ff its gate/up rows, SwiGLU and down columns"
+                                if h["path_bits"] & em.PATH_SLICES else
+                                f"gate/up + SwiGLU expert kernel ({em.TYPE_NAMES[spec.wtype]})"
+                                + (", router + routing fused in (one token)" if args.tokens == 1 else "")),
+                     "bound": "hbm", "achieved": h["gate_up_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": h["gate_up_gbs"] / HBM_PEAK_GBS, "traffic": profiled_traffic(args.config, args.tokens),
-                     "bytes_per_launch": gu_bytes, "avg_launch_us": h["gate_up_us"]},
+                     "bytes_per_launch": algorithmic(spec, args.tokens, h["experts_hit"], h["path_bits"])[0],
+                     "avg_launch_us": h["gate_up_us"]},
         "layer_hbm_frac": h["layer_hbm_frac"],
         "sweep": [results[T] for T in sweep_T],
     }
+    if args.config == "c2" and not args.no_nested:
+        # the other single-layer BASELINE configs (1, 3, 4) at their own token counts, nested so that the
+        # default run records them too
+        for name in ("c1", "c3", "c4"):
+            try:
+                line[name] = nested_config(em, name, max(5, args.steps // 2), args.warmup)
+            except Exception as exc:
+                line[name] = {"error": str(exc)}
     if args.config == "c2" and not args.no_c5:
         # BASELINE config 5 (the 32-layer Mixtral-architecture model, Q4_K experts) end to end, in the same
         # run: its own line's figures, nested here so the default run records them too

@@ -192,16 +192,26 @@ struct Layout {
   size_t logits, idx, gates, offsets, perm, h, y, hs, ys, sg;
   size_t x16, xexp, xb, h16, hexp, hs16, hsexp, tiles, n_tiles;  // MFMA paths
   size_t shpart;                          // the shared expert's partial gate / up dots (K split)
+  size_t part;                            // the one-token slice launch's partial outputs
   int mode, mode_shared;                  // PathMode of the routed experts and of the shared expert
   int ks_sh_gu, ks_sh_dn;                 // K split of the shared expert's 64-token-tile launches
   RouteLayout r;
   size_t end;
 };
+// Whether a call may take the one-token slice launch (SliceArgs): one token on the decode path, the
+// fused routing's limits, a Q8_0 or Q4_K prefill pack, no shared expert; unless any_size, also enough
+// slices to give every CU a block (the scratch layout reserves the section whenever the launch can run).
+bool slices_possible(const ember_moe_layer* w, int T, int mode, bool any_size) {
+  const int t = w->gate_type;
+  return T == 1 && mode == kGemv && w->prefill_pack && (t == EMBER_TYPE_Q8_0 || t == EMBER_TYPE_Q4_K) &&
+         packable(w) && w->d_ff_shared == 0 && slices_fit(t, w->d, w->d_ff, w->E, w->k, any_size);
+}
+
 Layout layout(const ember_moe_layer* w, int T) {
   Layout l;
   const size_t slots = (size_t)T * w->k;
   size_t o = 0;
-  l.flag = o; o = align_up(o + (size_t)8 * (2 * w->E + 2));
+  l.flag = o; o = align_up(o + (size_t)8 * (2 * w->E + 3));
   l.logits = o; o = align_up(o + (size_t)T * w->E * 4);
   l.idx = o; o = align_up(o + slots * 4);
   l.gates = o; o = align_up(o + slots * 4);
@@ -253,8 +263,36 @@ Layout layout(const ember_moe_layer* w, int T) {
   l.hsexp = o; o = align_up(o + (mfma_sh && !sp_sh ? (size_t)T * 4 : 0));
   l.tiles = o; o = align_up(o + tiles * 8);
   l.n_tiles = o; o = align_up(o + 4);
+  // the one-token slice launch's partial outputs [k][d_ff / 64][d]
+  l.part = o; o = align_up(o + (slices_possible(w, T, l.mode, true) ? (size_t)w->k * (w->d_ff / 64) * w->d * 4 : 0));
   l.end = o;
   return l;
+}
+
+// The launch plan of a call (which kernels run), shared by run_ffn and ember_moe_path.
+struct Plan {
+  bool fuse_route;  // one token: router, routing and dispatch inside the first expert launch
+  bool slices;      // one token: the whole layer in one launch over d_ff slices, plus an ordered reduce
+  bool down1;       // one token: the down projection with the combine fused in
+};
+Plan plan(const ember_moe_layer* w, const Layout& l, int T) {
+  static const bool fuse_ok = [] { const char* v = std::getenv("EMBER_FUSE_ROUTE"); return !(v && atoi(v) == 0); }();
+  static const bool down1_ok = [] { const char* v = std::getenv("EMBER_MOE_DOWN1"); return !(v && atoi(v) == 0); }();
+  // EMBER_MOE_SLICES (read per call): 0 never takes the slice launch, 1 takes it whenever it can run
+  const char* sv = std::getenv("EMBER_MOE_SLICES");
+  const bool slices_ok = !(sv && atoi(sv) == 0), slices_any = sv && atoi(sv) == 1;
+  const int d = w->d, d_ff = w->d_ff, E = w->E, k = w->k;
+  Plan p{};
+  // (the router blocks are one per expert and must fit the device's CUs: fewer CUs than experts take the
+  // unfused launches)
+  p.fuse_route = fuse_ok && l.mode == kGemv && T == 1 && fused_route_fits(w->gate_type, d, E, k) && E <= device_cus();
+  p.slices = slices_ok && p.fuse_route && slices_possible(w, T, l.mode, slices_any);
+  // (measured on MI355X: C1-shaped layer 22.6 -> 20.4 us, Mixtral-shaped even; with many picks or a
+  // shared expert its row partition leaves blocks idle: Qwen-shaped top-8 32 -> 40 us, DeepSeek-shaped
+  // top-6 + shared 50 -> 54 us, so those keep the down launch + combine)
+  p.down1 = !p.slices && down1_ok && l.mode == kGemv && T == 1 && k <= 2 && w->d_ff_shared == 0 &&
+            down1_fits(w->down_type, d, d_ff, k, 0);
+  return p;
 }
 
 template <class P>
@@ -404,10 +442,8 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
   const int sigmoid = w->scoring == EMBER_SCORE_SIGMOID ? 1 : 0;
   // one token on the decode path: the router, the routing and the dispatch run inside the gate/up launch
   // (its block 0 publishes them; the other blocks wait), saving two launches on the latency path
-  static const bool fuse_ok = [] { const char* v = std::getenv("EMBER_FUSE_ROUTE"); return !(v && atoi(v) == 0); }();
-  // (the router blocks are one per expert and must fit the device's CUs: fewer CUs than experts take the
-  // unfused launches)
-  const bool fuse_route = fuse_ok && l.mode == kGemv && T == 1 && fused_route_fits(w->gate_type, d, E, k) && E <= device_cus();
+  const Plan pl = plan(w, l, T);
+  const bool fuse_route = pl.fuse_route;
   const bool shared = w->d_ff_shared > 0;
   const bool shared_mfma = shared && l.mode_shared != kGemv;
   const float out_scale = w->out_scale == 0.0f ? 1.0f : w->out_scale;
@@ -452,12 +488,7 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
   float* ys = shared ? at<float>(scratch, l.ys) : nullptr;
   float* hs = at<float>(scratch, l.hs);
   // one token on the decode path: the down launch also forms the output rows (combine fused in)
-  static const bool down1_ok = [] { const char* v = std::getenv("EMBER_MOE_DOWN1"); return !(v && atoi(v) == 0); }();
-  // (measured on MI355X: C1-shaped layer 22.6 -> 20.4 us, Mixtral-shaped even; with many picks or a
-  // shared expert its row partition leaves blocks idle: Qwen-shaped top-8 32 -> 40 us, DeepSeek-shaped
-  // top-6 + shared 50 -> 54 us, so those keep the down launch + combine)
-  const bool down1 = down1_ok && l.mode == kGemv && T == 1 && k <= 2 && !shared &&
-                     down1_fits(w->down_type, d, d_ff, k, 0);
+  const bool down1 = pl.down1;
   // qwen2moe's shared-expert gate logit per token: a one-row router (the same FP64 fixed-order dot)
   float* sg = w->shared_gate ? at<float>(scratch, l.sg) : nullptr;
   if (sg && (s = launch_router_logits(x, T, d, 1, w->shared_gate, sg, st))) return s;
@@ -518,11 +549,24 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     return s;
   };
   SideStream* side = shared_mfma && fork_ok ? side_stream() : nullptr;
+  // Once forked, every return joins the side stream back into `st` (on an error return too), so that a
+  // capture on `st` never ends with an unjoined fork.
+  struct JoinGuard {
+    SideStream* side = nullptr;
+    hipStream_t st = nullptr;
+    ~JoinGuard() {
+      if (side) {
+        (void)hipEventRecord(side->join, side->s);
+        (void)hipStreamWaitEvent(st, side->join, 0);
+      }
+    }
+  } join_guard;
   if (side) {
     if (hipEventRecord(side->fork, st) != hipSuccess || hipStreamWaitEvent(side->s, side->fork, 0) != hipSuccess)
       return EMBER_ERR_LAUNCH;
+    join_guard.side = side;
+    join_guard.st = st;
     if ((s = run_shared(side->s))) return s;
-    if (hipEventRecord(side->join, side->s) != hipSuccess) return EMBER_ERR_LAUNCH;
   }
 
   if (l.mode != kGemv) {
@@ -651,6 +695,40 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
       const bool test_nopub = tv && atoi(tv) != 0;
       r.no_publish = test_nopub ? 1 : 0;
       r.spin_limit = test_nopub ? 4u : 4096u;
+      // test hook: the router blocks publish wrong fast values (negated) under tight bounds, a pick-set
+      // conflict that block 0 must catch (the output rows are then NaN)
+      const char* tc = std::getenv("EMBER_MOE_TEST_FAST_CORRUPT");
+      r.test_corrupt = tc && atoi(tc) != 0 ? 1 : 0;
+      // per-call tags (a word from an earlier call never matches; under graph capture the replays share
+      // the captured tags, and every call's last expert launch clears the words)
+      static std::atomic<uint32_t> calls{0};
+      const uint32_t c = calls.fetch_add(1, std::memory_order_relaxed) * 0x9e3779b1u;
+      r.logit_tag = (0x10617ed5u ^ c) | 1u;    // odd: never 0 (a cleared word)
+      r.fast_tag = (0x0fa57106u ^ c) & ~1u;    // even, and nonzero unless the mix cancels it
+      if (r.fast_tag == 0) r.fast_tag = 2u;
+    }
+    if (pl.slices) {
+      // one token: the whole layer in one launch over d_ff slices (the prefill pack's tiles), then the
+      // ordered reduce of the slices' partial outputs, which also clears the routing words
+      SliceArgs sa{};
+      sa.p = a;
+      const PackLayout pk = pack_layout(d, d_ff, E, w->gate_type);
+      const uint8_t* pack = static_cast<const uint8_t*>(w->prefill_pack);
+      sa.pack_gu = pack + pk.gu;
+      sa.pack_dn = pack + pk.dn;
+      sa.d = d;
+      sa.d_ff = d_ff;
+      sa.part = at<float>(scratch, l.part);
+      if (kev) *kev_used = 1;
+      if ((s = launch_slices(sa, st))) return s;
+      mark(ev, 4, st);
+      if ((s = launch_slice_reduce(sa.part, d_ff / 64, d, k, idx, gates, out_scale, routed ? nullptr : flag + 2 + 2 * E,
+                                   flag + 2, 2 * E, out, st)))
+        return s;
+      mark(ev, 5, st);
+      mark(ev, 6, st);
+      mark(ev, 7, st);
+      return EMBER_OK;
     }
     if (down1) {
       // one token: the down projection with the combine fused in (no y rows, no combine launch)
@@ -675,6 +753,7 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
       b.out = out;
       b.clear_flag = fuse_route ? flag + 2 : nullptr;
       b.clear_n = 2 * E;
+      b.conflict = fuse_route && !routed ? flag + 2 + 2 * E : nullptr;
       if ((s = launch_projection(a, st))) return s;
       mark(ev, 4, st);
       if (kev) {
@@ -742,11 +821,15 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     b.s_out = ys;
     if ((s = launch_projection(b, st))) return s;
   }
-  if (side && hipStreamWaitEvent(st, side->join, 0) != hipSuccess) return EMBER_ERR_LAUNCH;
+  if (side) {
+    join_guard.side = nullptr;
+    if (hipEventRecord(side->join, side->s) != hipSuccess || hipStreamWaitEvent(st, side->join, 0) != hipSuccess)
+      return EMBER_ERR_LAUNCH;
+  }
   mark(ev, 6, st);
   const int ys_parts = shared_mfma && l.mode_shared == kSkinny ? l.ks_sh_dn : 1;
   s = launch_combine(y, ksplit, (int64_t)T * k * d, gates, ds.pos, ys, ys_parts, (int64_t)T * d, sg, out_scale, T, k,
-                     d, out, st);
+                     d, out, st, fuse_route && !routed ? flag + 2 + 2 * E : nullptr);
   mark(ev, 7, st);
   return s;
 }
@@ -823,6 +906,21 @@ int ember_moe_ffn_timed(const ember_moe_layer* w, const float* x, int T, float* 
   return s;
 }
 
+int ember_moe_path(const ember_moe_layer* w, int T) {
+  const int s = validate(w);
+  if (s) return s;
+  if (T < 0) return EMBER_ERR_SHAPE;
+  if (T == 0) return 0;
+  const Layout l = layout(w, T);
+  const Plan p = plan(w, l, T);
+  int bits = l.mode == kGemv ? EMBER_PATH_GEMV : l.mode == kSkinny ? EMBER_PATH_TILES64 : EMBER_PATH_TILES256;
+  if (p.fuse_route) bits |= EMBER_PATH_FUSED_ROUTE;
+  if (p.slices) bits |= EMBER_PATH_SLICES;
+  if (p.down1) bits |= EMBER_PATH_DOWN1;
+  if (w->d_ff_shared > 0 && l.mode_shared != kGemv) bits |= EMBER_PATH_SHARED_MFMA;
+  return bits;
+}
+
 int ember_moe_scratch_routing(const ember_moe_layer* w, int T, ember_moe_routing_view* v) {
   const int s = validate(w);
   if (s) return s;
@@ -839,6 +937,7 @@ int ember_moe_scratch_routing(const ember_moe_layer* w, int T, ember_moe_routing
   v->n_used = l.r.n_used;
   v->fallbacks = l.flag;
   v->mismatches = l.flag + 8;
+  v->conflict = l.flag + 8 * (2 * (size_t)w->E + 2);
   return EMBER_OK;
 }
 

@@ -332,15 +332,33 @@ __device__ inline void proj_body(const ProjArgs& a, const Dispatch& dp, const Se
 
 // ---- routing fused into a one-token gate/up launch (ProjArgs::route)
 // Words of the flag area: [0] the count of blocks that computed a missing logit themselves, [1] the
-// count of calls whose exact picks differed from the fast ones; [2 + e] expert e's logit under
-// kLogitTag (the f32 bits in the low half). A word is read with one device-coherent load and carries its own data, so no
-// ordering between a payload and a flag is needed.
+// count of calls whose exact picks differed from the fast ones; [2 + e] expert e's logit under the
+// call's logit tag (Route::logit_tag in the high half, the f32 bits in the low half). A word is read
+// with one device-coherent load and carries its own data, so no ordering between a payload and a flag
+// is needed. The tags change from call to call (a per-process call counter mixed into two constants),
+// so a word left behind by an earlier call never matches.
 constexpr int kFusedMaxK = 8;
-constexpr uint32_t kLogitTag = 0x10617ed5u;
-// Words [2 + E + e]: expert e's fast logit under kFastTag — the same exact products summed as a tree (so
-// available ~4 us before the reference's eight chains are added), as binary32 with the low 8 mantissa
-// bits replaced by a bound: |fast - the reference's double logit| <= 2^(low byte - 160) (255: no bound).
-constexpr uint32_t kFastTag = 0x0fa57106u;
+// The launch's own tag: its AQL dispatch packet's address (distinct for consecutive dispatches on a
+// queue, graph replays included, whose packets take new queue slots) mixed with the call's host tag. A
+// word written by an earlier launch therefore never carries the current launch's tag, even when no later
+// launch of that call cleared it or a captured graph replays the same host tags.
+__device__ inline uint32_t launch_tag(uint32_t host) {
+  const uint64_t p = (uint64_t)__builtin_amdgcn_dispatch_ptr();
+  uint32_t t = ((uint32_t)(p >> 6) ^ ((uint32_t)(p >> 38) * 0x85ebca6bu)) ^ host;
+  t *= 0x9e3779b1u;
+  return t ^ (t >> 15);
+}
+__device__ inline uint32_t logit_tag(const ProjArgs::Route& r) { return launch_tag(r.logit_tag) | 1u; }
+__device__ inline uint32_t fast_tag(const ProjArgs::Route& r) {
+  const uint32_t t = launch_tag(r.fast_tag) & ~1u;
+  return t ? t : 2u;
+}
+// Words [2 + E + e]: expert e's fast logit under the call's fast tag — the same exact products summed as a
+// tree (so available ~4 us before the reference's eight chains are added), as binary32 with the low 8
+// mantissa bits replaced by a bound: |fast - the reference's double logit| <= 2^(low byte - 160) (255: no
+// bound). Word [2 + 2E]: this call's conflict status (block 0 sets it to 0 at the start of the launch and
+// to 1 if its exact picks contradict the fast words); the launch that writes the output rows reads it and
+// writes NaN rows when it is set, so a wrong pick set can never pass as a valid result.
 
 // The fast word of a logit whose exact products sum to s (tree order) with sum |p| = S, for a dot of
 // nq groups of eight. Bound (Higham, recursive sums): a sum of exact terms whose every term passes
@@ -349,7 +367,7 @@ constexpr uint32_t kFastTag = 0x0fa57106u;
 // reference's chains add nq terms, then 3 combining levels and the tail (an fma chain of at most 7
 // exact products, then one add): D <= nq + 11. 2 (nq + 64) u S covers both with room for the rounding
 // of S itself; truncating the binary32 value to 16 significant bits adds at most 2^-14 |s| + 2^-140.
-__device__ inline unsigned long long fast_word(double s, double S, int nq) {
+__device__ inline unsigned long long fast_word(double s, double S, int nq, uint32_t tag) {
   const float f = (float)s;
   uint32_t eb = 255;
   const double B = 2.0 * (double)(nq + 64) * 0x1p-53 * S + fabs(s) * 0x1p-14 + 0x1p-140;
@@ -358,7 +376,7 @@ __device__ inline unsigned long long fast_word(double s, double S, int nq) {
     const int ex = (int)((__builtin_bit_cast(unsigned long long, B) >> 52) & 0x7ff) - 1023 + 1;
     eb = ex + 160 < 0 ? 0u : ex + 160 > 254 ? 255u : (uint32_t)(ex + 160);
   }
-  return ((unsigned long long)kFastTag << 32) | (__builtin_bit_cast(uint32_t, f) & 0xffffff00u) | eb;
+  return ((unsigned long long)tag << 32) | (__builtin_bit_cast(uint32_t, f) & 0xffffff00u) | eb;
 }
 // LDS of a router block (the products, f64, chain-major) and, after it, every block's routing area
 // (logits, picks, gates, one routing wave's work area)
@@ -375,7 +393,7 @@ __host__ __device__ inline size_t fused_x_lds(int type, int d) {
 // eight lanes add their chain's products in order — the rounding sequence of acc += (double)r * (double)x.
 // Returns the logit in thread 0.
 template <int NT, bool FAST>
-__device__ float router_block_logit(const ProjArgs& a, int e, uint8_t* lds) {
+__device__ __attribute__((always_inline)) float router_block_logit(const ProjArgs& a, int e, uint8_t* lds) {
   const ProjArgs::Route& r = a.route;
   const int t = threadIdx.x, d = r.d, n8 = d - d % 8, nq = n8 / 8;
   // chain stride in doubles: even (16-byte pair reads stay aligned) and 2 mod 4 doubles past a multiple
@@ -445,7 +463,10 @@ __device__ float router_block_logit(const ProjArgs& a, int e, uint8_t* lds) {
       s = s + fpart[w];
       S = S + fpart[NW + w];
     }
-    __hip_atomic_store(r.flag + 2 + r.E + e, fast_word(s, S, nq), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // (test hook: a wrong value under a tight bound, the contradiction block 0 must catch)
+    if (r.test_corrupt) s = -s;
+    __hip_atomic_store(r.flag + 2 + r.E + e, fast_word(s, S, nq, fast_tag(r)), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
   }
   double acc = 0.0;
   if (t < 8) {
@@ -518,7 +539,7 @@ __device__ inline void fused_dispatch(const int* picks, int nv, int E, int32_t* 
 // Block 0's record of the routing for the later launches (logits, idx, gates, pos, used, perm, offsets,
 // n_used), from the routing area.
 template <int NT, bool ROUTED>
-__device__ void route_publish(const ProjArgs& a, uint8_t* ra) {
+__device__ __attribute__((always_inline)) void route_publish(const ProjArgs& a, uint8_t* ra) {
   const ProjArgs::Route& r = a.route;
   const int t = threadIdx.x;
   float* lg = reinterpret_cast<float*>(ra);
@@ -593,11 +614,11 @@ __device__ float router_logit_slow(const ProjArgs& a, int e, uint8_t* lds) {
 // when a word is missing after the wait's bound, carries no bound, or the margin is too small; the
 // caller then routes from the exact logits. On true the block's one-token dispatch is built.
 template <int NT>
-__device__ bool fast_route(const ProjArgs& a, uint8_t* ra, int32_t* s_off, int32_t* s_used, int32_t* s_n,
+__device__ __attribute__((always_inline)) bool fast_route(const ProjArgs& a, uint8_t* ra, int32_t* s_off, int32_t* s_used, int32_t* s_n,
                            int32_t* s_perm) {
   __shared__ float fv[kMaxRouteE];
   __shared__ uint8_t feb[kMaxRouteE];
-  __shared__ int s_ok;
+  __shared__ int s_ok, s_margin;  // every word present and bounded; the margin proves the set
   const ProjArgs::Route& r = a.route;
   int32_t* pidx = reinterpret_cast<int32_t*>(ra + 2048);
   const int t = threadIdx.x, E = r.E, kk = min(a.k, r.E);
@@ -606,16 +627,17 @@ __device__ bool fast_route(const ProjArgs& a, uint8_t* ra, int32_t* s_off, int32
   // an eighth of the exact words' bound: the exact path follows a give-up (and waits for the same router
   // block), and the fast words normally land a few microseconds into the launch
   const unsigned spin = r.spin_limit >> 3;
+  const uint32_t ftag = fast_tag(r);
   for (int e = t; e < E; e += NT) {
     unsigned long long w;
     unsigned n = 0;
     while (((w = __hip_atomic_load(r.flag + 2 + E + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) >> 32) !=
-           kFastTag) {
+           ftag) {
       if (++n > spin) break;
       __builtin_amdgcn_s_sleep(1);
     }
     const float v = __builtin_bit_cast(float, (uint32_t)w & 0xffffff00u);
-    if ((w >> 32) != kFastTag || (w & 0xff) == 0xff || v != v) s_ok = 0;
+    if ((w >> 32) != ftag || (w & 0xff) == 0xff || v != v) s_ok = 0;
     fv[e] = v;
     feb[e] = (uint8_t)(w & 0xff);
   }
@@ -639,29 +661,34 @@ __device__ bool fast_route(const ProjArgs& a, uint8_t* ra, int32_t* s_off, int32
       hi = fmax(hi, __shfl_xor(hi, off, 64));
     }
     const bool ok = n == kk && (kk == E || lo - hi > 0x1p-22 * fmax(fabs(lo), fabs(hi)) + 0x1p-140);
-    if (t == 0) s_ok = ok;
+    // (a word of its own: other waves may still be reading s_ok from the check above)
+    if (t == 0) s_margin = ok;
   }
   __syncthreads();
-  if (!s_ok) return false;
+  if (!s_margin) return false;
   fused_dispatch(pidx, kk, E, s_off, s_used, s_n, s_perm);
   __syncthreads();
   return true;
 }
 
-// Block 0's check of the other blocks' fast pick sets against its exact picks (used[0 .. n)). A set
-// proven from the fast words differs from the exact one only if some unpicked expert's lower bound
-// lies above some picked expert's upper bound: the exact logits would then break the bounds. Such a
-// contradiction (never expected) is counted in the flag area's word 1. Words not (yet) published are
-// skipped: the blocks that missed them routed from the exact logits.
+// The check of the fast pick sets against the exact picks (used[0 .. n)). A set proven from the fast words
+// differs from the exact one only if some unpicked expert's lower bound lies above some picked expert's
+// upper bound: the exact logits would then break the bounds. Returns (block-uniform) whether such a
+// contradiction (never expected) exists. Words not (yet) published are skipped: the blocks that missed
+// them routed from the exact logits. Block 0 counts a contradiction in the flag area's word 1 and stores
+// the call's conflict word (2 + 2E), which makes the output rows NaN (the launch that writes them reads it
+// or runs this check itself).
 template <int NT>
-__device__ void fast_check(const ProjArgs& a, const int32_t* used, int n) {
+__device__ __attribute__((always_inline)) bool fast_conflict(const ProjArgs& a, const int32_t* used, int n) {
+  __shared__ int s_bad;
   const ProjArgs::Route& r = a.route;
   const int t = threadIdx.x;
+  const uint32_t ftag = fast_tag(r);
   if (t < 64) {
     double lo_out = -__builtin_inf(), hi_in = __builtin_inf();  // bounds of the unpicked / picked
     for (int e = t; e < r.E; e += 64) {
       const unsigned long long w = __hip_atomic_load(r.flag + 2 + r.E + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if ((w >> 32) != kFastTag || (w & 0xff) == 0xff) continue;
+      if ((w >> 32) != ftag || (w & 0xff) == 0xff) continue;
       const double v = (double)__builtin_bit_cast(float, (uint32_t)w & 0xffffff00u);
       const double h = __builtin_bit_cast(double, (unsigned long long)((int)(w & 0xff) - 160 + 1023) << 52);
       bool picked = false;
@@ -676,13 +703,21 @@ __device__ void fast_check(const ProjArgs& a, const int32_t* used, int n) {
       hi_in = fmin(hi_in, __shfl_xor(hi_in, off, 64));
       lo_out = fmax(lo_out, __shfl_xor(lo_out, off, 64));
     }
-    if (t == 0 && lo_out > hi_in)
-      __hip_atomic_fetch_add(r.flag + 1, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (t == 0) {
+      s_bad = lo_out > hi_in;
+      if (blockIdx.x == 0) {
+        if (lo_out > hi_in) __hip_atomic_fetch_add(r.flag + 1, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(r.flag + 2 + 2 * r.E, lo_out > hi_in ? 1ull : 0ull, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
   }
+  __syncthreads();
+  return s_bad != 0;
 }
 
 template <int NT, bool ROUTED>
-__device__ void route_block(const ProjArgs& a, uint8_t* lds, uint8_t* ra, int32_t* s_off, int32_t* s_used,
+__device__ __attribute__((always_inline)) void route_block(const ProjArgs& a, uint8_t* lds, uint8_t* ra, int32_t* s_off, int32_t* s_used,
                             int32_t* s_n, int32_t* s_perm) {
   __shared__ uint8_t missing[kMaxRouteE];
   __shared__ int any_missing;
@@ -695,14 +730,15 @@ __device__ void route_block(const ProjArgs& a, uint8_t* lds, uint8_t* ra, int32_
   const int E = r.E, k = a.k;
   if (t == 0) any_missing = 0;
   __syncthreads();
+  const uint32_t ltag = logit_tag(r);
   for (int e = t; e < E; e += NT) {
     unsigned long long w;
     unsigned n = 0;
-    while (((w = __hip_atomic_load(r.flag + 2 + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) >> 32) != kLogitTag) {
+    while (((w = __hip_atomic_load(r.flag + 2 + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) >> 32) != ltag) {
       if (++n > r.spin_limit) break;
       __builtin_amdgcn_s_sleep(1);
     }
-    const bool got = (w >> 32) == kLogitTag;
+    const bool got = (w >> 32) == ltag;
     missing[e] = got ? 0 : 1;
     if (!got) any_missing = 1;
     lg[e] = __builtin_bit_cast(float, (uint32_t)w);
@@ -753,6 +789,57 @@ __device__ void route_block(const ProjArgs& a, uint8_t* lds, uint8_t* ra, int32_
 
 
 
+// The one-token launches' routing prologue (ROUTE 1: softmax router, 2: the DeepSeek-style options):
+// the token's activation row staged at the start of the dynamic LDS (xs), router blocks 0..E-1 publish
+// their expert's logit (and, softmax, a fast word), then every block obtains the pick set and builds
+// the one-token dispatch in s_off / s_used / s_n / s_perm; block 0 routes exactly and writes the record.
+// `prod` and `ra` are the router products' and routing area's LDS (after xs).
+// Returns whether this block's pick set came from the fast words (then not yet checked against the exact
+// routing, which block 0 always runs).
+template <int FMT, int NT, int ROUTE>
+__device__ inline bool fused_route_prologue(const ProjArgs& a, uint8_t* xs, uint8_t* prod, uint8_t* ra, int32_t* s_off,
+                                            int32_t* s_used, int32_t* s_n, int32_t* s_perm, int* zero_row) {
+  const int b = blockIdx.x;
+  EMBER_STAMP(0, 0);
+  if (threadIdx.x == 0) *zero_row = 0;
+  if (threadIdx.x < 64) route_stage_tables(ra + 2048 + 512);
+  if (b < a.route.E && !a.route.no_publish) {  // router block: its expert's logit, published tagged
+    const float v = router_block_logit<NT, ROUTE == 1>(a, b, prod);
+    EMBER_STAMP(0, 1);
+    if (threadIdx.x == 0) {
+      __hip_atomic_store(a.route.flag + 2 + b, ((unsigned long long)logit_tag(a.route) << 32) | __builtin_bit_cast(uint32_t, v),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  __syncthreads();
+  {  // then the activation row (router blocks after their logit, which is on the routing's critical path)
+    using F = Fmt<FMT>;
+    if constexpr (F::QX)
+      stage_rows_quant<F::PLANES>(a.route.x, a.route.d, zero_row, 1, xs, act_lds_bytes(true, a.route.d));
+    else
+      stage_rows_f32<F::NGL>(a.route.x, a.route.d, zero_row, 1, xs, act_lds_bytes(false, a.route.d));
+  }
+  // softmax router: the pick set from the fast words when they prove it (block 0 then writes the
+  // exact routing record after its rows); otherwise, and for the DeepSeek-style router, from the
+  // exact logits
+  bool fast = false;
+  if constexpr (ROUTE == 1) {
+    if (b != 0) fast = fast_route<NT>(a, ra, s_off, s_used, s_n, s_perm);
+  }
+  if (!fast) route_block<NT, ROUTE == 2>(a, prod, ra, s_off, s_used, s_n, s_perm);
+  if constexpr (ROUTE == 1) {
+    if (b == 0) {
+      // block 0 routes from the exact logits (and writes the record); the pick set the other blocks
+      // may have proven from the fast words must be the same: a difference (never expected) is
+      // counted in the flag area's word 1 and stored in the call's conflict word
+      (void)fast_conflict<NT>(a, s_used, *s_n);
+    }
+  }
+  EMBER_STAMP(0, 3);
+  __syncthreads();
+  return fast;
+}
+
 // ROUTE: 0 none; 1 the fused one-token routing with a softmax router; 2 with the DeepSeek-style options
 template <int FMT, int MT, bool GATED, int NB, int NT, int WPE, int ROUTE>
 __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) proj_kernel(ProjArgs a) {
@@ -770,43 +857,7 @@ __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) 
     uint8_t* xs = act_lds;
     uint8_t* prod = act_lds + fused_x_lds(FMT, a.route.d);
     uint8_t* ra = prod + fused_router_lds(a.route.d);
-    EMBER_STAMP(0, 0);
-    if (threadIdx.x == 0) zero_row = 0;
-    if (threadIdx.x < 64) route_stage_tables(ra + 2048 + 512);
-    if (b < a.route.E && !a.route.no_publish) {  // router block: its expert's logit, published tagged
-      const float v = router_block_logit<NT, ROUTE == 1>(a, b, prod);
-      EMBER_STAMP(0, 1);
-      if (threadIdx.x == 0) {
-        __hip_atomic_store(a.route.flag + 2 + b, ((unsigned long long)kLogitTag << 32) | __builtin_bit_cast(uint32_t, v),
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
-    __syncthreads();
-    {  // then the activation row (router blocks after their logit, which is on the routing's critical path)
-      using F = Fmt<FMT>;
-      if constexpr (F::QX)
-        stage_rows_quant<F::PLANES>(a.route.x, a.route.d, &zero_row, 1, xs, act_lds_bytes(true, a.route.d));
-      else
-        stage_rows_f32<F::NGL>(a.route.x, a.route.d, &zero_row, 1, xs, act_lds_bytes(false, a.route.d));
-    }
-    // softmax router: the pick set from the fast words when they prove it (block 0 then writes the
-    // exact routing record after its rows); otherwise, and for the DeepSeek-style router, from the
-    // exact logits
-    bool fast = false;
-    if constexpr (ROUTE == 1) {
-      if (b != 0) fast = fast_route<NT>(a, ra, s_off, s_used, &s_n, s_perm);
-    }
-    if (!fast) route_block<NT, ROUTE == 2>(a, prod, ra, s_off, s_used, &s_n, s_perm);
-    if constexpr (ROUTE == 1) {
-      if (b == 0) {
-        // block 0 routes from the exact logits (and writes the record); the pick set the other blocks
-        // may have proven from the fast words must be the same: a difference (never expected) is
-        // counted in the flag area's word 1, which the routing readback exposes
-        fast_check<NT>(a, s_used, s_n);
-      }
-    }
-    EMBER_STAMP(0, 3);
-    __syncthreads();
+    fused_route_prologue<FMT, NT, ROUTE>(a, xs, prod, ra, s_off, s_used, &s_n, s_perm, &zero_row);
     Dispatch dp{s_n, s_used, s_off, s_perm};
     SegView v;
     // softmax router: block 0 (the exact routing and its record) takes no rows; blocks 1 .. G-1 share them
@@ -901,6 +952,269 @@ int launch_proj_gated(const ProjArgs& a, hipStream_t st) {
 
 int launch_projection(const ProjArgs& a, hipStream_t st) {
   return a.gated ? launch_proj_gated<true>(a, st) : launch_proj_gated<false>(a, st);
+}
+
+// ---- one-token layer over d_ff slices (SliceArgs)
+// Pack rows (64 columns of one weight row, the prefill pack's layout) against one staged activation row:
+// chunk c of the row staged in LDS (act_lds_bytes layout; every lane of a wave reads the same chunk, an
+// LDS broadcast). A lane owns one pack row, so a wave's load of 64 consecutive rows is one contiguous
+// run of the tile, and each lane's dot is its row's whole 64-column share (no cross-lane reduction).
+template <int FMT>
+struct PackRow;
+template <>
+struct PackRow<EMBER_TYPE_Q8_0> {  // the two Q8_0 blocks as they are: Fmt<Q8_0>'s chunk
+  static constexpr int NW = 17, RB = kPackRowB;
+  __device__ static void load(const uint8_t* p, uint32_t* raw) { Fmt<EMBER_TYPE_Q8_0>::load(p, 0, 0, raw); }
+  __device__ static void dot(const uint32_t* raw, const uint8_t* x, int c, int K, float& acc) {
+    Fmt<EMBER_TYPE_Q8_0>::dot_tokens<1>(raw, x, 0, c, K, 1, &acc);
+  }
+};
+template <>
+struct PackRow<EMBER_TYPE_Q4_K> {  // {a0, m0, a1, m1} fp16, then 32 nibble bytes; weight = a q + m
+  static constexpr int NW = 10, RB = kPackRowQ4B;
+  __device__ static void load(const uint8_t* p, uint32_t* raw) {
+    const u32x4 q0 = *reinterpret_cast<const u32x4_a4*>(p);
+    const u32x4 q1 = *reinterpret_cast<const u32x4_a4*>(p + 16);
+    const uint2 q2 = *reinterpret_cast<const uint2*>(p + 32);
+    raw[0] = q0.x, raw[1] = q0.y, raw[2] = q0.z, raw[3] = q0.w;
+    raw[4] = q1.x, raw[5] = q1.y, raw[6] = q1.z, raw[7] = q1.w;
+    raw[8] = q2.x, raw[9] = q2.y;
+  }
+  // the activations as byte planes (Fmt<Q4_K>::PLANES): dot = 256 dot4(nibbles, high) + dot4(nibbles, low)
+  __device__ static void dot(const uint32_t* raw, const uint8_t* x, int c, int K, float& acc) {
+    int ha = 0, hb = 0;
+    uint32_t la = 0u, lb = 0u;
+#pragma unroll
+    for (int k2 = 0; k2 < 8; k2 += 2) {
+      const uint32_t w0 = raw[2 + k2], w1 = raw[3 + k2];
+      const uint32_t a0 = w0 & 0x0f0f0f0fu, a1 = w1 & 0x0f0f0f0fu;                // group 0, 8 elements
+      const uint32_t b0 = (w0 >> 4) & 0x0f0f0f0fu, b1 = (w1 >> 4) & 0x0f0f0f0fu;  // group 1
+      const u32x4 xa = *reinterpret_cast<const u32x4*>(lds_granule<3>(x, c, k2 >> 1));
+      const u32x4 xb = *reinterpret_cast<const u32x4*>(lds_granule<3>(x, c, 4 + (k2 >> 1)));
+      la = __builtin_amdgcn_udot4(a0, xa.x, la, false);
+      la = __builtin_amdgcn_udot4(a1, xa.y, la, false);
+      ha = __builtin_amdgcn_sdot4((int)a0, (int)xa.z, ha, false);
+      ha = __builtin_amdgcn_sdot4((int)a1, (int)xa.w, ha, false);
+      lb = __builtin_amdgcn_udot4(b0, xb.x, lb, false);
+      lb = __builtin_amdgcn_udot4(b1, xb.y, lb, false);
+      hb = __builtin_amdgcn_sdot4((int)b0, (int)xb.z, hb, false);
+      hb = __builtin_amdgcn_sdot4((int)b1, (int)xb.w, hb, false);
+    }
+    const int ia = 256 * ha + (int)la, ib = 256 * hb + (int)lb;
+    const float a0 = half_bits_to_float(raw[0] & 0xffff), m0 = half_bits_to_float(raw[0] >> 16);
+    const float a1 = half_bits_to_float(raw[1] & 0xffff), m1 = half_bits_to_float(raw[1] >> 16);
+    const float* sc = reinterpret_cast<const float*>(x + K * 2) + 2 * c;
+    const int* sm = reinterpret_cast<const int*>(x + K * 2 + (K / 32) * 4) + 2 * c;
+    acc += sc[0] * (a0 * (float)ia + m0 * (float)sm[0]) + sc[1] * (a1 * (float)ib + m1 * (float)sm[1]);
+  }
+};
+
+// Block 1 + item (softmax router; item = b for the DeepSeek-style router, whose block 0 also takes one),
+// item = j * ns + c: pick j (s_used[j], ascending), slice c. Each wave walks one sequence of pack-row
+// loads through a ring of NB register buffers: first its share of the gate/up K tiles (k-tile wave +
+// i * waves, gate then up, lane = slice row), then its share of the down rows (row group wave + i * waves
+// of 64 rows, lane = row, the slice's 64 columns). Between the two, at a block-uniform position of the
+// sequence (every wave has the same number of loads; surplus loads are clamped and their dots masked),
+// the waves' gate/up sums are added in wave order, SwiGLU'd and quantized as the GEMV quantizes h.
+template <int FMT, int NB, int NT, int ROUTE>
+__global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) slice_kernel(SliceArgs a) {
+  using P = PackRow<FMT>;
+  using F = Fmt<FMT>;
+  constexpr int NWV = NT / 64;
+  extern __shared__ __align__(16) uint8_t act_lds[];
+  __shared__ int32_t s_off[kMaxRouteE + 1], s_used[kFusedMaxK], s_perm[kFusedMaxK], s_n;
+  __shared__ int zero_row;
+  __shared__ float red[2][NWV][64];
+  __shared__ __align__(16) float hval[64];
+  __shared__ __align__(16) uint8_t hrow[2 * 64 + 2 * 8];  // act_lds_bytes(true, 64)
+  const ProjArgs& pa = a.p;
+  uint8_t* xs = act_lds;
+  uint8_t* prod = act_lds + fused_x_lds(FMT, a.d);
+  uint8_t* ra = prod + fused_router_lds(a.d);
+  fused_route_prologue<FMT, NT, ROUTE>(pa, xs, prod, ra, s_off, s_used, &s_n, s_perm, &zero_row);
+  constexpr int B0 = ROUTE == 1 ? 1 : 0;
+  const int ns = a.d_ff / 64;
+  const int item = (int)blockIdx.x - B0;
+  if (item < 0) return;  // block-uniform
+  const int j = item / ns, c = item - j * ns;
+  if (j >= s_n) return;  // an invalid pick (k > E): block-uniform
+  const int e = s_used[j];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int d = a.d, nkt = d / 64, nrg = d / 64;
+  const int64_t RB = P::RB, tile = 256 * RB;
+  // gate/up: tile (e, c / 2, kt), rows 64 (c % 2) + lane (gate) and 128 + the same (up)
+  const uint8_t* gbase = a.pack_gu + (int64_t)(e * ((a.d_ff + 127) / 128) + (c >> 1)) * nkt * tile +
+                         (64 * (c & 1) + lane) * RB;
+  // down: tile (e, rg / 4, c), row 64 (rg % 4) + lane
+  const int ntd = (d + 255) / 256;
+  const uint8_t* dbase = a.pack_dn + ((int64_t)e * ntd * ns + c) * tile + lane * RB;
+  const int ngu = (nkt + NWV - 1) / NWV, ndn = (nrg + NWV - 1) / NWV;
+  const int Q1 = 2 * ngu, Q = Q1 + ndn;
+  auto addr = [&](int q) __attribute__((always_inline)) -> const uint8_t* {
+    if (q < Q1) {
+      const int kt = min(wave + (q >> 1) * NWV, nkt - 1);
+      return gbase + (int64_t)kt * tile + (q & 1) * 128 * RB;
+    }
+    const int rg = min(wave + (q - Q1) * NWV, nrg - 1);
+    return dbase + (int64_t)(rg >> 2) * ns * tile + (rg & 3) * 64 * RB;
+  };
+  float ag = 0.0f, au = 0.0f;
+  float* part = a.part + (int64_t)item * d;
+  uint32_t buf[NB][P::NW];
+  auto use = [&](int q, const uint32_t (&b)[P::NW]) __attribute__((always_inline)) {
+    if (q < Q1) {
+      const int kt = wave + (q >> 1) * NWV;
+      if (kt < nkt) {
+        float t = 0.0f;
+        P::dot(b, xs, kt, d, t);
+        if (q & 1)
+          au += t;
+        else
+          ag += t;
+      }
+      return;
+    }
+    if (q == Q1) {  // block-uniform: every wave reaches load Q1 at the same ring position
+      red[0][wave][lane] = ag;
+      red[1][wave][lane] = au;
+      __syncthreads();
+      if (wave == 0) {
+        float g = 0.0f, u = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NWV; ++w) {
+          g = g + red[0][w][lane];
+          u = u + red[1][w][lane];
+        }
+        hval[lane] = swiglu(g, u);
+      }
+      __syncthreads();
+      if (threadIdx.x < 2) {  // the GEMV's activation quantization, one 32-element block per thread
+        uint32_t packed[16];
+        float sc;
+        int sm;
+        quant_block32(hval + 32 * threadIdx.x, packed, &sc, &sm);
+        store_block_quant<F::PLANES>(packed, sc, sm, threadIdx.x, 64, hrow);
+      }
+      __syncthreads();
+      EMBER_STAMP(0, 5);
+    }
+    if (q >= Q) return;
+    const int rg = wave + (q - Q1) * NWV;
+    if (rg < nrg) {
+      float t = 0.0f;
+      P::dot(b, hrow, 0, 64, t);
+      // streamed out past the L2 (read once, by the next launch): no dirty lines left to write back at the
+      // end of the launch
+      __builtin_nontemporal_store(t, part + rg * 64 + lane);
+    }
+  };
+  ring_for<NB - 1>([&](auto J) { P::load(addr(decltype(J)::value), buf[decltype(J)::value]); });
+  EMBER_STAMP(0, 4);
+#pragma unroll 1
+  for (int q0 = 0; q0 < Q; q0 += NB) {
+    ring_for<NB>([&](auto J) {
+      constexpr int jj = decltype(J)::value;
+      const int q = q0 + jj;
+      P::load(addr(min(q + NB - 1, Q - 1)), buf[(jj + NB - 1) % NB]);
+      use(q, buf[jj]);
+    });
+  }
+  EMBER_STAMP(0, 7);
+}
+
+// 32 outputs per block, the slices summed in 8 groups (group g: slices g, g + 8, ...) added in group order.
+// A thread issues its group's loads (up to 32 slices at a time) before adding them in slice order.
+__global__ void __launch_bounds__(256) slice_reduce_kernel(const float* __restrict__ part, int ns, int d, int k,
+                                                           const int32_t* __restrict__ idx,
+                                                           const float* __restrict__ gates, float scale,
+                                                           const unsigned long long* conflict,
+                                                           unsigned long long* clear_flag, int clear_n,
+                                                           float* __restrict__ out) {
+  __shared__ float red[8][32];
+  const int t = threadIdx.x, o = blockIdx.x * 32 + (t & 31), g = t >> 5;
+  if (clear_flag && blockIdx.x == 0)
+    for (int i = t; i < clear_n; i += 256)
+      __hip_atomic_store(clear_flag + i, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  float acc = 0.0f;
+  for (int j = 0; j < k; ++j) {
+    if (idx[j] < 0) break;  // the valid picks are a prefix (block-uniform)
+    const float* p = part + (int64_t)j * ns * d + o;
+    float s = 0.0f;
+    for (int c0 = g; c0 < ns; c0 += 8 * 32) {
+      float v[32];
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        const int c = c0 + 8 * i;
+        v[i] = c < ns ? p[(int64_t)c * d] : 0.0f;
+      }
+#pragma unroll
+      for (int i = 0; i < 32; ++i)
+        if (c0 + 8 * i < ns) s += v[i];
+    }
+    red[g][t & 31] = s;
+    __syncthreads();
+    if (g == 0) {
+      float y = red[0][t];
+#pragma unroll
+      for (int i = 1; i < 8; ++i) y = y + red[i][t];
+      acc = acc + gates[j] * y;  // combine_kernel's order: acc = acc + gate * y, picks ascending
+    }
+    __syncthreads();
+  }
+  if (g == 0) {
+    if (scale != 1.0f) acc = acc * scale + 0.0f;
+    out[o] = conflict && *conflict ? __builtin_nanf("") : acc;
+  }
+}
+
+template <int FMT, int ROUTE>
+int launch_slices_cfg(const SliceArgs& a, hipStream_t st) {
+  // three register buffers per wave, 512-thread blocks (two per CU): measured on MI355X against two buffers
+  // (even), four (spills; C2 97 vs 84 us) and 1024-thread blocks (90 vs 84 us)
+  constexpr int NB = 3, NT = 512;
+  const void* fn = reinterpret_cast<const void*>(&slice_kernel<FMT, NB, NT, ROUTE>);
+  const size_t lds = fused_x_lds(FMT, a.d) + fused_router_lds(a.d) + fused_route_lds(a.p.route.E);
+  if (blocks_per_cu(fn, NT, lds, kProjLdsBytes) <= 0) return EMBER_ERR_LAUNCH;
+  // every router block (0 .. E-1) must exist, whatever the number of slices
+  const int G = std::max((ROUTE == 1 ? 1 : 0) + a.p.k * (a.d_ff / 64), a.p.route.E);
+  if (a.p.ev_start)
+    hipExtLaunchKernelGGL(slice_kernel<FMT, NB, NT, ROUTE>, dim3(G), dim3(NT), lds, st, a.p.ev_start, a.p.ev_stop, 0,
+                          a);
+  else
+    slice_kernel<FMT, NB, NT, ROUTE><<<G, NT, lds, st>>>(a);
+  return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
+}
+
+// The slices pay off once they give every CU at least one block (Mixtral-shaped C2 / C5: 448 slices, 85 vs
+// 89 us and 55 vs 64 us against the GEMV path); with fewer (Qwen-shaped top-8 of 768-wide experts: 96
+// slices) the GEMV path is faster (30.1 vs 31.7 us).
+// (any_size: whenever the kernel can run, whatever the fill)
+bool slices_fit(int type, int d, int d_ff, int E, int k, bool any_size) {
+  return (type == EMBER_TYPE_Q8_0 || type == EMBER_TYPE_Q4_K) && d % 64 == 0 && d_ff % 64 == 0 &&
+         fused_route_fits(type, d, E, k) && (any_size || (int64_t)k * (d_ff / 64) >= device_cus()) &&
+         (int64_t)k * (d_ff / 64) < (1 << 30);
+}
+
+int launch_slices(const SliceArgs& a, hipStream_t st) {
+  if (!a.p.route.flag || !a.pack_gu || !a.pack_dn || !a.part ||
+      !slices_fit(a.p.type, a.d, a.d_ff, a.p.route.E, a.p.k, true))
+    return EMBER_ERR_SHAPE;
+  const bool routed = a.p.route.routed != 0;
+  switch (a.p.type) {
+    case EMBER_TYPE_Q8_0:
+      return routed ? launch_slices_cfg<EMBER_TYPE_Q8_0, 2>(a, st) : launch_slices_cfg<EMBER_TYPE_Q8_0, 1>(a, st);
+    case EMBER_TYPE_Q4_K:
+      return routed ? launch_slices_cfg<EMBER_TYPE_Q4_K, 2>(a, st) : launch_slices_cfg<EMBER_TYPE_Q4_K, 1>(a, st);
+    default: return EMBER_ERR_TYPE;
+  }
+}
+
+int launch_slice_reduce(const float* part, int ns, int d, int k, const int32_t* idx, const float* gates, float scale,
+                        const unsigned long long* conflict, unsigned long long* clear_flag, int clear_n, float* out,
+                        hipStream_t st) {
+  if (d % 32) return EMBER_ERR_SHAPE;
+  slice_reduce_kernel<<<d / 32, 256, 0, st>>>(part, ns, d, k, idx, gates, scale, conflict, clear_flag, clear_n, out);
+  return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
 }
 
 // 1 / (1 + expf(-s)) in binary32 with glibc's expf (graph_ir_ops.cpp:22 evaluates it on the host)
@@ -1111,8 +1425,10 @@ __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) 
                             a.sg_logit ? &sgc_s : nullptr, 0, [] {});
   }
   __syncthreads();
+  // a pick-set conflict of the fused routing (never expected): NaN rows instead of plausible numbers
+  const bool bad = a.conflict && __hip_atomic_load(a.conflict, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
   for (int sl = t; sl < a.nslots; sl += NT)
-    if (rowlist[sl] >= 0) a.out[rowlist[sl]] = obuf[sl];
+    if (rowlist[sl] >= 0) a.out[rowlist[sl]] = bad ? __builtin_nanf("") : obuf[sl];
   EMBER_STAMP(1, 7);
 }
 
@@ -1187,8 +1503,10 @@ extern "C" int ember_moe_probe_set(void* buf) {
 namespace ember_moe {
 #endif
 
-// The router blocks (0..E-1) must be resident together with block 0, which waits for them while they
-// wait for it: at least one block per CU is resident (MI355X: 256 CUs), so E <= 255 (ids fit a byte).
+// The fused routing's limits: E <= 255 (expert ids fit the fast words' byte arrays), k <= 8 and the
+// LDS of the staged row, the router products and the routing area. (A block that waits for a router
+// block's word longer than its bound computes that logit itself, so no block depends on another being
+// resident.)
 bool fused_route_fits(int type, int d, int E, int k) {
   return E <= 255 && k <= kFusedMaxK && d >= 8 && d <= 16 * 512 &&
          fused_x_lds(type, d) + fused_router_lds(d) + fused_route_lds(E) <= (size_t)kProjLdsBytes;
@@ -1211,7 +1529,7 @@ __global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ 
                                                       const float* __restrict__ gates, const int32_t* __restrict__ pos,
                                                       const float* __restrict__ y_shared, int s_parts, int64_t s_stride,
                                                       const float* __restrict__ sg_logit, float scale, int k, int d,
-                                                      float* __restrict__ out) {
+                                                      float* __restrict__ out, const unsigned long long* conflict) {
   const int t = blockIdx.y;
   const int o = blockIdx.x * blockDim.x + threadIdx.x;
   if (o >= d) return;
@@ -1227,7 +1545,7 @@ __global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ 
     const float v = y_at(y_shared, s_parts, s_stride, (size_t)t * d + o);
     acc = acc + (sg_logit ? v * c : v);
   }
-  out[(size_t)t * d + o] = acc;
+  out[(size_t)t * d + o] = conflict && *conflict ? __builtin_nanf("") : acc;
 }
 
 // The same with four consecutive outputs per thread (d % 4 == 0): 16-byte loads of y rows.
@@ -1235,7 +1553,7 @@ __global__ void __launch_bounds__(256) combine4_kernel(const float* __restrict__
                                                        const float* __restrict__ gates, const int32_t* __restrict__ pos,
                                                        const float* __restrict__ y_shared, int s_parts, int64_t s_stride,
                                                        const float* __restrict__ sg_logit, float scale, int k, int d,
-                                                       float* __restrict__ out) {
+                                                       float* __restrict__ out, const unsigned long long* conflict) {
   const int t = blockIdx.y;
   const int o = 4 * (blockIdx.x * blockDim.x + threadIdx.x);
   if (o >= d) return;
@@ -1294,22 +1612,23 @@ __global__ void __launch_bounds__(256) combine4_kernel(const float* __restrict__
     a2 = a2 + v.z;
     a3 = a3 + v.w;
   }
+  if (conflict && *conflict) a0 = a1 = a2 = a3 = __builtin_nanf("");  // a pick-set conflict (see Route)
   *reinterpret_cast<float4*>(out + (size_t)t * d + o) = make_float4(a0, a1, a2, a3);
 }
 
 int launch_combine(const float* y, int nparts, int64_t part_stride, const float* gates, const int32_t* pos,
                    const float* y_shared, int s_parts, int64_t s_stride, const float* sg, float scale, int T, int k,
-                   int d, float* out, hipStream_t st) {
+                   int d, float* out, hipStream_t st, const unsigned long long* conflict) {
   if (T <= 0) return EMBER_OK;
   if (d % 4 == 0) {
     dim3 grid((d / 4 + 255) / 256, T);
     combine4_kernel<<<grid, 256, 0, st>>>(y, nparts, part_stride, gates, pos, y_shared, s_parts, s_stride, sg, scale,
-                                          k, d, out);
+                                          k, d, out, conflict);
     return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
   }
   dim3 grid((d + 255) / 256, T);
   combine_kernel<<<grid, 256, 0, st>>>(y, nparts, part_stride, gates, pos, y_shared, s_parts, s_stride, sg, scale, k,
-                                       d, out);
+                                       d, out, conflict);
   return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
 }
 

@@ -1298,7 +1298,8 @@ int gemm_skinny_max_tiles(int T, int k, int E) { return (T * k + SBM - 1) / SBM 
 
 int gemm_ksplit(int type, bool packed, int T, int k, int E, int N, int K) {
   if (!dma_path(type, packed)) return 1;  // the split lives in the DMA kernels
-  if (const char* v = std::getenv("EMBER_KSPLIT")) return std::max(1, std::min(kMaxKSplit, atoi(v)));
+  // tuning override, clamped so that every part holds at least one K tile
+  if (const char* v = std::getenv("EMBER_KSPLIT")) return std::max(1, std::min(std::min(kMaxKSplit, K / GBK), atoi(v)));
   // expected 256-token tiles (segments average T k / E tokens) times n-tiles: aim for >= 4 rounds
   const int est_tiles = (T * k + GBM - 1) / GBM + E / 2;
   const int blocks = est_tiles * ((N + 255) / 256);
@@ -1310,7 +1311,8 @@ int gemm_ksplit(int type, bool packed, int T, int k, int E, int N, int K) {
 int gemm_skinny_ksplit(int type, bool packed, int max_mtiles, int N, int K) {
   (void)type;
   (void)packed;
-  if (const char* v = std::getenv("EMBER_KSPLIT")) return std::max(1, std::min(kMaxKSplit, atoi(v)));
+  // tuning override, clamped so that every part holds at least one K tile
+  if (const char* v = std::getenv("EMBER_KSPLIT")) return std::max(1, std::min(std::min(kMaxKSplit, K / GBK), atoi(v)));
   // up to 1024 blocks, with at least 5 K tiles per part (C4-shaped down projection, K = 1408: 22 K
   // tiles; split 1 / 2 / 4: T = 16 141 / 124 / 121 us, T = 64 152 / 134 / 131, T = 256 191 / 179 / 188)
   const int blocks = max_mtiles * ((N + 255) / 256);

@@ -112,11 +112,13 @@ struct ProjArgs {
   // dispatch (idx, gates, pos, offsets, used, n_used, perm) for the later launches. With the softmax
   // router each router block also publishes a bounded fast logit (words E+2 .. 2E+1), from which the
   // other blocks prove the pick set before the exact logits are summed. A later launch of the same call
-  // (clear_flag) zeroes both sets of words, so stale words never carry a tag (a word of uninitialised
-  // scratch matches a 32-bit tag by chance with probability 2^-32). Word 0 counts the blocks that
-  // computed a missing logit themselves, word 1 the calls whose exact picks contradicted the fast bounds.
+  // (clear_flag) zeroes both sets of words, and the tags change per call, so stale words never carry
+  // this call's tag (a word of uninitialised scratch matches a 32-bit tag by chance with probability
+  // 2^-32). Word 0 counts the blocks that computed a missing logit themselves, word 1 the calls whose
+  // exact picks contradicted the fast bounds; word 2 + 2E is this call's conflict status (0 / 1), read by
+  // the launch that writes the output (NaN rows when set).
   struct Route {
-    unsigned long long* flag;  // 2 E + 2 words
+    unsigned long long* flag;  // 2 E + 3 words
     const float* x;       // the token [d]
     const float* router;  // [E][d]
     int d, E, renorm, routed, sigmoid, groups_n, groups_top;
@@ -128,10 +130,33 @@ struct ProjArgs {
     int32_t *offsets, *used, *n_used, *perm;  // the dispatch (the launch's read-only views alias these)
     unsigned spin_limit;  // polls of a logit word before the block computes that logit itself
     int no_publish;       // test hook: router blocks do not publish (every block computes every logit)
+    int test_corrupt;     // test hook: the fast words carry wrong values under their bounds
+    uint32_t logit_tag, fast_tag;  // this call's tags of the exact and fast logit words (nonzero, distinct)
   } route;
   unsigned long long* clear_flag;  // non-null: block 0 of this launch zeroes clear_n words of the flag area
   int clear_n;
 };
+// One-token layer over d_ff slices (decode, T = 1, a prefill pack present): one launch in which block
+// 1 + j * ns + c (ns = d_ff / 64 slices) owns slice c of pick j — the slice's 64 gate and 64 up rows
+// (SwiGLU into LDS), then the matching 64 columns of the down projection, streamed as the pack's tiles —
+// and writes the slice's partial output part[j][c][0..d); the routing prologue is proj_kernel's fused
+// one (block 0: the exact routing record). A second launch sums the partials in fixed order and forms
+// the output as the combine does.
+struct SliceArgs {
+  ProjArgs p;              // route (the fused routing), k, type, ev_start / ev_stop
+  const uint8_t* pack_gu;  // the pack's gate/up section [E][ceil(d_ff / 128)][d / 64] tiles
+  const uint8_t* pack_dn;  // its down section [E][ceil(d / 256)][d_ff / 64] tiles
+  int d, d_ff;
+  float* part;             // [k][d_ff / 64][d]
+};
+bool slices_fit(int type, int d, int d_ff, int E, int k, bool any_size);
+int launch_slices(const SliceArgs& a, hipStream_t st);
+// out[o] = sum over valid picks j ascending of gates[j] * (sum over slices of part[j][c][o]), then
+// (x * scale) + 0; NaN rows when *conflict is set.
+// (clear_flag: clear_n words this launch zeroes, the fused routing's logit words, for the next call)
+int launch_slice_reduce(const float* part, int ns, int d, int k, const int32_t* idx, const float* gates, float scale,
+                        const unsigned long long* conflict, unsigned long long* clear_flag, int clear_n, float* out,
+                        hipStream_t st);
 // the fused routing's shape limits (the router blocks' and block 0's LDS)
 bool fused_route_fits(int type, int d, int E, int k);
 constexpr unsigned long long kRouteReady = 0x5e11a7ed0ddba11full;
@@ -161,6 +186,7 @@ struct Down1Args {
   int nslots;              // set by the launcher
   unsigned long long* clear_flag;
   int clear_n;
+  const unsigned long long* conflict;  // the fused routing's conflict word, or null (NaN rows when set)
   hipEvent_t ev_start, ev_stop;
 };
 bool down1_fits(int type, int d, int K, int k, int s_K);
@@ -299,6 +325,6 @@ bool dma_path(int type, bool packed);
 
 int launch_combine(const float* y, int nparts, int64_t part_stride, const float* gates, const int32_t* pos,
                    const float* y_shared, int s_parts, int64_t s_stride, const float* shared_gate_logit, float scale, int T,
-                   int k, int d, float* out, hipStream_t st);
+                   int k, int d, float* out, hipStream_t st, const unsigned long long* conflict = nullptr);
 
 }  // namespace ember_moe

@@ -136,7 +136,7 @@ __host__ __device__ inline size_t route_wave_lds(int E) {
 // value with ties to the lower index — the result of the reference's serial strict-> scans. Experts
 // with cand[e] == 0 are skipped (cand may be null); a pass that finds nothing ends the search. Lane 0
 // writes the picks in pick order; returns their number (uniform across the wave).
-__device__ inline int wave_topk_passes(const float* val, const char* cand, int E, int k, int* picks);
+__device__ __attribute__((always_inline)) inline int wave_topk_passes(const float* val, const char* cand, int E, int k, int* picks);
 
 // The same selection by ranks, for larger k: expert e is picked iff it is a candidate and fewer than k
 // candidates are strictly better (larger value, ties to the lower index) — exactly the experts the k
@@ -296,7 +296,7 @@ __device__ __attribute__((always_inline)) inline int wave_topk(const float* val,
   return k >= 4 ? wave_topk_rank(val, cand, E, k, picks) : wave_topk_passes(val, cand, E, k, picks);
 }
 
-__device__ inline int wave_topk_passes(const float* val, const char* cand, int E, int k, int* picks) {
+__device__ __attribute__((always_inline)) inline int wave_topk_passes(const float* val, const char* cand, int E, int k, int* picks) {
   const int lane = threadIdx.x & 63;
   uint32_t mine_taken = 0;  // bit q: expert lane + 64q taken (E <= 2048)
   int n = 0;

@@ -64,7 +64,7 @@ class RoutingView(ctypes.Structure):
 
     _fields_ = [(n, ctypes.c_size_t) for n in
                 ("logits", "idx", "gates", "offsets", "perm", "pos", "used", "n_used", "fallbacks",
-                 "mismatches")]
+                 "mismatches", "conflict")]
 
 
 _lib = None
@@ -126,6 +126,8 @@ def lib() -> ctypes.CDLL:
         L.ember_moe_prefill_pack_bytes.restype = sz
         L.ember_moe_prefill_pack.argtypes = [ctypes.POINTER(Layer), vp, sz, vp]
         L.ember_moe_prefill_pack.restype = i
+        L.ember_moe_path.argtypes = [ctypes.POINTER(Layer), i]
+        L.ember_moe_path.restype = i
         L.ember_moe_scratch_routing.argtypes = [ctypes.POINTER(Layer), i, ctypes.POINTER(RoutingView)]
         L.ember_moe_scratch_routing.restype = i
         L.ember_moe_strerror.argtypes = [i]
@@ -277,9 +279,22 @@ def moe_ffn(layer: Layer, x, T: int, out, scratch, scratch_nbytes: Optional[int]
     return int(lib().ember_moe_ffn(ctypes.byref(layer), _ptr(x), T, _ptr(out), _ptr(scratch), n, _stream(stream)))
 
 
+# ember_moe_path bits (include/ember_moe.h)
+PATH_GEMV, PATH_TILES64, PATH_TILES256 = 1, 2, 4
+PATH_FUSED_ROUTE, PATH_SLICES, PATH_DOWN1, PATH_SHARED_MFMA = 8, 16, 32, 64
+
+
+def path(layer: Layer, T: int) -> int:
+    """The EMBER_PATH_* bits of the kernels a call with T tokens runs (ember_moe_path)."""
+    st = lib().ember_moe_path(ctypes.byref(layer), T)
+    if st < 0:
+        raise EmberError(st, "ember_moe_path")
+    return st
+
+
 def scratch_routing(layer: Layer, T: int, scratch) -> dict:
     """The routing a completed ember_moe_ffn call left in `scratch` (a uint8 device tensor), copied to the
-    host: logits [T][E], idx / gates [T][k], offsets [E+1], perm / pos [T*k], used [n_used], fallbacks, mismatches."""
+    host: logits [T][E], idx / gates [T][k], offsets [E+1], perm / pos [T*k], used [n_used], fallbacks, mismatches, conflict."""
     v = RoutingView()
     st = lib().ember_moe_scratch_routing(ctypes.byref(layer), T, ctypes.byref(v))
     if st:
@@ -296,7 +311,8 @@ def scratch_routing(layer: Layer, T: int, scratch) -> dict:
                 offsets=arr(v.offsets, E + 1, np.int32), perm=arr(v.perm, T * k, np.int32),
                 pos=arr(v.pos, T * k, np.int32), used=arr(v.used, max(min(n_used, E), 0), np.int32),
                 n_used=n_used, fallbacks=int(arr(v.fallbacks, 1, np.uint64)[0]),
-                mismatches=int(arr(v.mismatches, 1, np.uint64)[0]))
+                mismatches=int(arr(v.mismatches, 1, np.uint64)[0]),
+                conflict=int(arr(v.conflict, 1, np.uint64)[0]))
 
 
 NOALLOC_SCRATCH_BYTES = 32 << 20  # EMBER_MOE_NOALLOC_SCRATCH_BYTES

@@ -145,7 +145,8 @@ class Mixtral:
     def _ensure_scratch(self, T):
         import torch
 
-        need = max(scratch_bytes(L, T) for L in self.layers[:1])
+        # (decode steps run T = 1 calls in the same buffer, whose one-token path has sections of its own)
+        need = max(scratch_bytes(L, n) for L in self.layers[:1] for n in (T, 1))
         if need == 0:
             raise EmberError(-1, "ember_moe_scratch_bytes")
         if self.scratch is None or self.scratch.numel() < need:

@@ -77,13 +77,34 @@ size_t ember_moe_scratch_bytes(const ember_moe_layer* w, int T);
  *                          from whatever the buffer held, and is never reset by the library).
  *   mismatches u64         one-token calls with a softmax router: the number of calls whose exact
  *                          routing differed from the pick set the expert launch proved from its fast
- *                          logits (never expected: a nonzero count means a wrong result; it only
- *                          grows, from whatever the buffer held).
+ *                          logits (never expected; it only grows, from whatever the buffer held).
+ *   conflict  u64          the same event for this call alone: set to 0 by every such call and to 1
+ *                          when it happens, in which case that call's output rows are all NaN (a
+ *                          pick-set conflict never yields plausible numbers). Meaningful after
+ *                          one-token calls with a softmax router; other calls leave it untouched.
  * The same layout holds for every call with this descriptor and T. */
 typedef struct ember_moe_routing_view {
-  size_t logits, idx, gates, offsets, perm, pos, used, n_used, fallbacks, mismatches;
+  size_t logits, idx, gates, offsets, perm, pos, used, n_used, fallbacks, mismatches, conflict;
 } ember_moe_routing_view;
 int ember_moe_scratch_routing(const ember_moe_layer* w, int T, ember_moe_routing_view* view);
+
+/* Which kernels a call of this descriptor with T tokens runs (a diagnostic for tests and integrators; no
+ * reference counterpart): a bit set of EMBER_PATH_*, or a negative ember_status. Exactly one of GEMV /
+ * TILES64 / TILES256 names the routed experts' path; the others add the one-token fusions:
+ *   FUSED_ROUTE  router, routing and dispatch run inside the first expert launch;
+ *   SLICES       the whole layer in one launch over 64-column slices of d_ff (prefill pack required), plus an
+ *                ordered reduce of the slices' partial outputs;
+ *   DOWN1        the down projection forms the output rows itself (the combine fused in);
+ *   SHARED_MFMA  the shared expert's rows take the MFMA tiles (on a side stream for ember_moe_ffn).
+ * The answer can depend on the current device (its CU count) and on the EMBER_* tuning variables. */
+#define EMBER_PATH_GEMV 1
+#define EMBER_PATH_TILES64 2
+#define EMBER_PATH_TILES256 4
+#define EMBER_PATH_FUSED_ROUTE 8
+#define EMBER_PATH_SLICES 16
+#define EMBER_PATH_DOWN1 32
+#define EMBER_PATH_SHARED_MFMA 64
+int ember_moe_path(const ember_moe_layer* w, int T);
 
 /* Prefill weight packing (no counterpart in the reference, which dequantizes every stack to F32 at
  * load, weight_management.cpp:486-511): a one-time preparation of a layer's routed stacks for the

@@ -142,16 +142,17 @@ def test_prefill_pack_sizes_and_validation():
 def test_scratch_routing_view_layout(E, k, T):
     """ember_moe_scratch_routing (host arithmetic only): every section of the routing record lies inside
     the scratch, 4-byte aligned and disjoint from the others; the two u64 counters are adjacent words at
-    the start of the flag area, whose 2E + 2 words (the counters, then one-token routing's exact and fast
-    logit words) end before the logits."""
+    the start of the flag area, whose 2E + 3 words (the counters, then one-token routing's exact and fast
+    logit words, then the per-call conflict word) end before the logits."""
     L = _layer(E=E, k=k, d=512, d_ff=512)
     need = em.scratch_bytes(L, T)
     assert need > 0
     v = em.RoutingView()
     assert em.lib().ember_moe_scratch_routing(ctypes.byref(L), T, ctypes.byref(v)) == 0
     assert v.mismatches == v.fallbacks + 8 and v.fallbacks % 8 == 0
-    assert v.fallbacks + 8 * (2 * E + 2) <= v.logits
-    spans = [(v.fallbacks, 8 * (2 * E + 2)), (v.logits, 4 * T * E), (v.idx, 4 * T * k), (v.gates, 4 * T * k),
+    assert v.conflict == v.fallbacks + 8 * (2 * E + 2)
+    assert v.fallbacks + 8 * (2 * E + 3) <= v.logits
+    spans = [(v.fallbacks, 8 * (2 * E + 3)), (v.logits, 4 * T * E), (v.idx, 4 * T * k), (v.gates, 4 * T * k),
              (v.offsets, 4 * (E + 1)), (v.perm, 4 * T * k), (v.pos, 4 * T * k), (v.used, 4 * E), (v.n_used, 4)]
     for off, n in spans:
         assert off % 4 == 0 and off + n <= need, (off, n, need)

@@ -5,8 +5,10 @@ layers checked against the CPU oracle inside the run:
     call's scratch, bit-exact against the oracle on the same inputs;
   * the FFN output of a seeded sample of tokens at the 2e-3 rel-L2 bar against the oracle's
     dequantize-then-F32 layer (the reference's path, utils.cpp:704-748);
-then greedy decode steps replayed from the captured HIP graph, which must give the same tokens as eager
-steps for a few steps (graph replay runs the same C ABI calls)."""
+then greedy decode steps: eager steps whose one-token MoE calls of the same layers (the decode branch,
+model.cpp:757-762 / 1318-1321: the slice launch over the prefill pack) are checked the same way (routing
+bit-exact, output at 2e-3 against the oracle on the decoded token's hidden state), and steps replayed from
+the captured HIP graph, which must give the same tokens as the eager steps."""
 import numpy as np
 import pytest
 
@@ -42,6 +44,20 @@ def test_c5_per_layer_parity(gpu):
     torch.cuda.synchronize()
     model.probe = None
     assert sorted(seen) == sorted(LAYERS)
+    # decode: eager steps, with the one-token calls of the same layers captured at every step
+    dec = {l: [] for l in LAYERS}
+
+    def probe_dec(l, h, f, scratch, L):
+        if l in LAYERS and h.shape[0] == 1:
+            dec[l].append((h.cpu().numpy(), f.cpu().numpy(), em.scratch_routing(L, 1, scratch)))
+
+    bits = em.path(model.layers[0], 1)
+    assert bits & em.PATH_SLICES and bits & em.PATH_FUSED_ROUTE, bits
+    model.probe = probe_dec
+    print("c5 eager decode", flush=True)
+    f_eager, toks_eager, _, _ = model.generate(prompt[:64], 4, use_graph=False)
+    model.probe = None
+    runs = [(int(f_eager[0]), toks_eager.cpu().numpy())]
     for l in LAYERS:
         h, f_rows, rows, r = seen[l]
         router = model.routers[l].cpu().numpy().reshape(-1)
@@ -59,11 +75,19 @@ def test_c5_per_layer_parity(gpu):
         print(f"c5 layer {l}: routing of {T} tokens bit-exact, rel-L2 {err:.2e} over tokens {rows.tolist()}",
               flush=True)
         assert err < 2e-3
+        assert len(dec[l]) == 4, len(dec[l])  # one call per decode step
+        for step, (hd, fd, rd) in enumerate(dec[l]):
+            lg = O.router_logits(hd, router)
+            assert same_bits(rd["logits"], lg), (l, step)
+            idx, gates = O.route(lg, spec.k)
+            assert np.array_equal(rd["idx"], idx) and same_bits(rd["gates"], gates), (l, step)
+            assert rd["conflict"] == 0
+            err = rel_l2(fd, O.moe_layer(hd, router, G, U, D, spec.d_ff, spec.E, spec.k))
+            print(f"c5 layer {l} decode step {step}: experts {idx[0].tolist()}, rel-L2 {err:.2e}", flush=True)
+            assert err < 2e-3
         del G, U, D
-    # decode: graph replay and eager steps give the same greedy tokens
-    runs = []
-    for use_graph in (False, True):
-        f0, toks, _, _ = model.generate(prompt[:64], 4, use_graph=use_graph)
-        runs.append((int(f0[0]), toks.cpu().numpy()))
+    # graph replay of the decode steps gives the eager steps' tokens
+    f0, toks, _, _ = model.generate(prompt[:64], 4, use_graph=True)
+    runs.append((int(f0[0]), toks.cpu().numpy()))
     assert runs[0][0] == runs[1][0] and np.array_equal(runs[0][1], runs[1][1])
     assert int(first[0]) >= 0

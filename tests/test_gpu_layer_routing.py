@@ -182,3 +182,49 @@ def test_fused_routing_fallback(gpu, monkeypatch):
     y2, r2 = _run(dl, x)
     assert r2["fallbacks"] == 0 and same_bits(y2, y0)
 
+
+
+@pytest.mark.parametrize("E,k", [(8, 2), (16, 4)])
+def test_fast_proof_conflict_poisons_output(gpu, monkeypatch, E, k):
+    """A pick set proven from wrong fast logits must never yield plausible numbers. With
+    EMBER_MOE_TEST_FAST_CORRUPT=1 the router blocks publish negated fast values under their tight bounds,
+    so the other blocks prove the bottom k (the wrong experts) and stream them; block 0's exact routing
+    (utils.cpp:708-733) contradicts the bounds. The call must then write NaN in every output row and set
+    the per-call conflict word, while the routing record stays the exact one. (E, k) = (8, 2) takes the
+    one-token down launch with the combine fused in, (16, 4) the down launch plus the combine. The scratch
+    starts as 0xff bytes: the conflict word is reset by every call, not accumulated."""
+    import torch
+
+    spec = em.LayerSpec(d=1024, d_ff=512, E=E, k=k, wtype=em.Q8_0, seed=21)
+    hl = em.make_host_layer(spec)
+    dl = em.DeviceLayer.upload(hl)
+    x = em.make_input(spec, 1, seed=22)
+    xd = torch.from_numpy(x).cuda()
+
+    def run():
+        scratch = torch.full((em.scratch_bytes(dl.desc, 1),), 0xFF, dtype=torch.uint8, device="cuda")
+        out, scratch = dl.forward(xd, scratch=scratch)
+        torch.cuda.synchronize()
+        return out.cpu().numpy(), em.scratch_routing(dl.desc, 1, scratch)
+
+    y0, r0 = run()
+    assert r0["conflict"] == 0 and np.isfinite(y0).all()
+    print(f"fast-proof conflict E={E} k={k}", flush=True)
+    monkeypatch.setenv("EMBER_MOE_TEST_FAST_CORRUPT", "1")
+    y1, r1 = run()
+    monkeypatch.delenv("EMBER_MOE_TEST_FAST_CORRUPT")
+    assert r1["conflict"] == 1, r1["conflict"]
+    assert np.isnan(y1).all(), "a pick-set conflict produced finite output"
+    assert r1["mismatches"] == (r0["mismatches"] + 1) % 2**64  # it grows from whatever the buffer held
+    _check_exact_record(hl, x, r1)
+    # the next call is clean again
+    y2, r2 = run()
+    assert r2["conflict"] == 0 and same_bits(y2, y0)
+
+
+def _check_exact_record(hl, x, r):
+    s = hl.spec
+    lg = O.router_logits(x, hl.router)
+    assert same_bits(r["logits"], lg)
+    idx, gates = O.route(lg, s.k, renorm=s.renorm)
+    assert np.array_equal(r["idx"], idx) and same_bits(r["gates"], gates)
