@@ -319,6 +319,39 @@ def em_input(spec, T):
     return em.make_input(spec, T)
 
 
+def bench_vendor_gemm(args):
+    """Times torch.matmul in fp16 with random operands (hipBLASLt / rocBLAS underneath) on the dense GEMMs a
+    config's prefill layer reduces to: all T k routed rows against one expert's gate+up (N = 2 d_ff, K = d)
+    and down (N = d, K = d_ff) matrices, and the per-expert share T k / E rows, plus 8192^3. A measured
+    reference for what the matrix cores sustain on this box, beside the datasheet peak."""
+    import torch
+
+    desc, _, tokens = CONFIGS[args.config]
+    spec = layer_spec(args.config)
+    T = args.tokens or max(tokens)
+    rows = T * spec.k
+    shapes = [(rows, 2 * spec.d_ff, spec.d), (rows, spec.d, spec.d_ff),
+              (max(1, rows // spec.E), 2 * spec.d_ff, spec.d), (max(1, rows // spec.E), spec.d, spec.d_ff),
+              (8192, 8192, 8192)]
+    out = []
+    for M, N, K in shapes:
+        a = torch.randn(M, K, device="cuda", dtype=torch.float16)
+        b = torch.randn(K, N, device="cuda", dtype=torch.float16)
+        for _ in range(3):
+            a @ b
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            a @ b
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / args.steps * 1e3
+        out.append({"M": M, "N": N, "K": K, "us": round(us, 1), "tflops": round(2 * M * N * K / us / 1e6, 1)})
+        log(f"[vendor-gemm] M={M} N={N} K={K}: {us:.1f} us, {out[-1]['tflops']} TFLOP/s")
+    print(json.dumps({"vendor_gemm_fp16": out, "config": args.config, "tokens": T}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -335,6 +368,9 @@ def main():
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device-to-device copies of MIB MiB (the reference kernel that scales "
                          "rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes), then exit")
+    ap.add_argument("--vendor-gemm", action="store_true",
+                    help="only time torch's fp16 matmul (the vendor GEMM library) on the dense shapes of the config's "
+                         "prefill expert GEMMs at the headline token count, as a measured ceiling, then exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for {args.gpus}): the multi-GPU layout (tensor parallel "
@@ -352,6 +388,9 @@ def main():
         torch.cuda.synchronize()
         log(f"[bench] copied {args.calibrate_copy} MiB x 5")
         return
+
+    if args.vendor_gemm:
+        return bench_vendor_gemm(args)
 
     import ember_moe as em
 

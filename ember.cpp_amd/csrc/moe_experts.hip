@@ -1103,9 +1103,7 @@ __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) sl
     if (rg < nrg) {
       float t = 0.0f;
       P::dot(b, hrow, 0, 64, t);
-      // streamed out past the L2 (read once, by the next launch): no dirty lines left to write back at the
-      // end of the launch
-      __builtin_nontemporal_store(t, part + rg * 64 + lane);
+      part[rg * 64 + lane] = t;
     }
   };
   ring_for<NB - 1>([&](auto J) { P::load(addr(decltype(J)::value), buf[decltype(J)::value]); });
