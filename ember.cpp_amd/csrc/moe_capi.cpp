@@ -193,6 +193,8 @@ struct Layout {
   size_t x16, xexp, xb, h16, hexp, hs16, hsexp, tiles, n_tiles;  // MFMA paths
   size_t shpart;                          // the shared expert's partial gate / up dots (K split)
   size_t part;                            // the one-token slice launch's partial outputs
+  size_t tailpart;                        // the 256-token gate/up launch's tail partials
+  int tail_parts;                         // their parts (0: no tail split)
   int mode, mode_shared;                  // PathMode of the routed experts and of the shared expert
   int ks_sh_gu, ks_sh_dn;                 // K split of the shared expert's 64-token-tile launches
   RouteLayout r;
@@ -262,6 +264,11 @@ Layout layout(const ember_moe_layer* w, int T) {
   l.hs16 = o; o = align_up(o + (mfma_sh ? (size_t)T * w->d_ff_shared * (sp_sh ? 4 : 2) : 0));
   l.hsexp = o; o = align_up(o + (mfma_sh && !sp_sh ? (size_t)T * 4 : 0));
   l.tiles = o; o = align_up(o + tiles * 8);
+  // the routed gate/up's tail split (256-token tiles): raw partial gate / up dots [parts][T k][2 d_ff]
+  l.tail_parts = l.mode == kGemm ? gemm_tail_parts(w->gate_type, w->prefill_pack != nullptr && !pack_bf16,
+                                                   (int)slots, w->d_ff, w->d)
+                                 : 0;
+  l.tailpart = o; o = align_up(o + (size_t)l.tail_parts * slots * 2 * w->d_ff * 4);
   l.n_tiles = o; o = align_up(o + 4);
   // the one-token slice launch's partial outputs [k][d_ff / 64][d]
   l.part = o; o = align_up(o + (slices_possible(w, T, l.mode, true) ? (size_t)w->k * (w->d_ff / 64) * w->d * 4 : 0));
@@ -609,7 +616,15 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
       g.w_hexp = wexp(bx.hmax);
     }
     const int mt = skinny ? gemm_skinny_max_tiles(T, k, E) : gemm_max_tiles(T, k, E);
+    if (!skinny && l.tail_parts > 1) {  // the tail round's tiles split over K
+      g.part_h = at<float>(scratch, l.tailpart);
+      g.part_rows = T * k;
+      g.tail_parts = l.tail_parts;
+      g.slots = gemm_slots();
+    }
     if ((s = gemm(g, true, mt))) return s;
+    g.part_h = nullptr;
+    g.tail_parts = 0;
     mark(ev, 4, st);
     g.A = h16;
     g.perm = nullptr;

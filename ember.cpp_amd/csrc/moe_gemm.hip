@@ -263,6 +263,48 @@ __device__ inline bool xcd_item(int M, int NT, int KS, int& mt, int& rem) {
   return true;
 }
 
+// The gated DMA kernels' work item of block b: the W = M x NT items, or with a tail split
+// (GemmArgs::tail_parts) the first R x slots items (R whole rounds) XCD-balanced as xcd_item takes them, then
+// for blocks R slots + i part i % S of tail item R slots + i / S, S = min(tail_parts, slots / tail) (S = 1: no
+// split; slots is a multiple of 8). Returns false for a block without an item; part / parts: this block's
+// K part.
+// The tail split of a gated launch of W = M x NT items: S parts per tail item (1: no split), capped at the
+// K tiles so that every part holds at least one; `full` = the items of the whole rounds (W without a split).
+__device__ inline int tail_split(const GemmArgs& g, int W, int& full) {
+  full = W;
+  if (g.tail_parts <= 1 || g.slots <= 0) return 1;
+  const int R = W / g.slots, tail = W - R * g.slots;
+  if (tail == 0) return 1;
+  const int S = min(min(g.tail_parts, g.slots / tail), g.K / GBK);
+  if (S <= 1) return 1;
+  full = R * g.slots;
+  return S;
+}
+__device__ inline bool gated_item(const GemmArgs& g, int NT, int& mt, int& nt, int& part, int& parts) {
+  const int W = launch_mtiles(g, GBM) * NT;
+  int full;
+  const int S = tail_split(g, W, full);
+  // the whole rounds' items take blocks 0 .. 8 C - 1 (xcd_item's mapping, C = ceil(full / 8)), the tail
+  // parts the blocks after them
+  const int b = blockIdx.x, C = (full + 7) / 8;
+  part = 0;
+  parts = 1;
+  if (b < 8 * C) {
+    const int j = b / 8, w = (b % 8) * C + j;
+    if (w >= full) return false;
+    mt = w / NT;
+    nt = w % NT;
+    return true;
+  }
+  const int i = b - 8 * C, w = full + i / S;
+  if (S == 1 || w >= W) return false;
+  mt = w / NT;
+  nt = w % NT;
+  part = i % S;
+  parts = S;
+  return true;
+}
+
 // Blocks take their tiles XCD-balanced (xcd_item).
 //
 // 512 threads = 8 waves in a 4 (M) x 2 (N) arrangement (two waves per SIMD, so one wave's waits and
@@ -528,10 +570,16 @@ __global__ void __launch_bounds__(kDmaThreads) gemm_dma_q8_kernel(GemmArgs g, in
   extern __shared__ __align__(16) uint8_t dsm[];
 
   // block -> (m-tile, n-tile, K split part), XCD-balanced
-  const int KS = GATED ? 1 : g.ksplit;
-  int mt, rem;
-  if (!xcd_item(launch_mtiles(g, GBM), NT, KS, mt, rem)) return;
-  const int nt = rem / KS, ks = rem % KS;
+  int KS, mt, nt, ks;
+  if constexpr (GATED) {
+    if (!gated_item(g, NT, mt, nt, ks, KS)) return;
+  } else {
+    KS = g.ksplit;
+    int rem;
+    if (!xcd_item(launch_mtiles(g, GBM), NT, KS, mt, rem)) return;
+    nt = rem / KS;
+    ks = rem % KS;
+  }
   int e = 0, p0 = 0, rows = 0;
   if (g.tiles) {
     e = g.tiles[2 * mt];
@@ -733,7 +781,13 @@ __global__ void __launch_bounds__(kDmaThreads) gemm_dma_q8_kernel(GemmArgs g, in
           const size_t o = (size_t)(p0 + m) * N + n;
           const int ex = s_rexp[m];
           if constexpr (GATED) {
-            store_h(g, o, p0 + m, ex, acc[i][0][4 * ii + jj], acc[i][1][4 * ii + jj], n == n0);
+            if (KS > 1) {  // a tail item's K part: raw partial dots, gemm_tail_fixup_kernel finishes the tile
+              float* part = g.part_h + ((size_t)ks * g.part_rows + p0 + m) * 2 * N + n;
+              part[0] = acc[i][0][4 * ii + jj];
+              part[N] = acc[i][1][4 * ii + jj];
+            } else {
+              store_h(g, o, p0 + m, ex, acc[i][0][4 * ii + jj], acc[i][1][4 * ii + jj], n == n0);
+            }
           } else {
             g.out_y[ks * g.part_stride + o] = unscale_y(acc[i][jn][4 * ii + jj], ex);
           }
@@ -1156,6 +1210,33 @@ __global__ void __launch_bounds__(256) swiglu_parts_kernel(GemmArgs g, int rows,
   store_h(g, (size_t)p * N + n, p, row_exp(g, p), __builtin_ldexpf(ga, we0), __builtin_ldexpf(ua, we1), n == 0, weh);
 }
 
+// The tail items of a split gated launch (gated_item): block i finishes tail item i — for each of its rows
+// and 128 columns the parts' raw gate and up dots summed in ascending part order, then the epilogue of the
+// DMA kernel (store_h with the row's exponent). Blocks without a tail item (no split this call) exit.
+__global__ void __launch_bounds__(256) gemm_tail_fixup_kernel(GemmArgs g, int NT) {
+  constexpr int BN = 128;
+  const int W = launch_mtiles(g, GBM) * NT;
+  int full;
+  const int S = tail_split(g, W, full);
+  if (S <= 1 || (int)blockIdx.x >= W - full) return;
+  const int w = full + blockIdx.x, mt = w / NT, nt = w % NT;
+  const int e = g.tiles[2 * mt], m0 = g.tiles[2 * mt + 1];
+  const int p0 = g.offsets[e] + m0, rows = min(GBM, g.offsets[e + 1] - p0);
+  const int N = g.N, n0 = nt * BN;
+  const size_t stride = (size_t)g.part_rows * 2 * N;
+  for (int i = threadIdx.x; i < rows * BN; i += 256) {
+    const int m = i / BN, c = i % BN, n = n0 + c;
+    if (n >= N) continue;
+    const float* part = g.part_h + (size_t)(p0 + m) * 2 * N + n;
+    float ga = part[0], ua = part[N];
+    for (int s = 1; s < S; ++s) {
+      ga = ga + part[s * stride];
+      ua = ua + part[s * stride + N];
+    }
+    store_h(g, (size_t)(p0 + m) * N + n, p0 + m, row_exp(g, p0 + m), ga, ua, c == 0);
+  }
+}
+
 // EMBER_GEMM_DMA=0 routes Q8_0 to the register-staged kernels (a debugging switch); they have no K split
 static bool dma_enabled() {
   static const bool on = [] { const char* v = std::getenv("EMBER_GEMM_DMA"); return !(v && atoi(v) == 0); }();
@@ -1173,6 +1254,21 @@ bool gemm_supported(int type, int K) {
 }
 
 int gemm_max_tiles(int T, int k, int E) { return (T * k + GBM - 1) / GBM + std::min(E, T * k); }
+
+// One 256-token-tile DMA block per CU (its LDS ring takes more than half a CU's LDS).
+int gemm_slots() { return device_cus() / 8 * 8; }
+
+// Up to 8 parts and K / 64 (a K tile per part), while the partials (parts x rows x 2N floats) stay within
+// 16 MiB (the scratch of a small batch stays well inside the no-allocation entry point's buffer).
+// EMBER_TAIL_PARTS (read per call) caps the parts; 1 turns the split off.
+int gemm_tail_parts(int type, bool packed, int rows, int N, int K) {
+  const char* e = std::getenv("EMBER_TAIL_PARTS");
+  const int cap = e ? atoi(e) : 8;
+  if (!dma_path(type, packed) || rows <= 0 || N <= 0) return 0;
+  const int64_t per = (int64_t)rows * 2 * N * 4;
+  const int p = (int)std::min<int64_t>(std::min(cap, K / GBK), ((int64_t)16 << 20) / per);
+  return p >= 2 ? p : 0;
+}
 
 template <int FMT, bool GATED>
 int launch_gemm_fmt(const GemmArgs& g, int max_mtiles, hipStream_t st) {
@@ -1196,14 +1292,23 @@ int launch_gemm_fmt(const GemmArgs& g, int max_mtiles, hipStream_t st) {
     if (!dma_ok) return EMBER_ERR_LAUNCH;
     GemmArgs gk = g;
     if (GATED || gk.ksplit < 1) gk.ksplit = 1;
-    const unsigned nb = blocks * (unsigned)gk.ksplit;
+    const bool tail = GATED && gk.tail_parts > 1 && gk.slots > 0 && gk.part_h && gk.tiles;
+    if (!tail) gk.tail_parts = 1;
+    unsigned nb = blocks * (unsigned)gk.ksplit;
+    // with a tail split: every whole round plus one round of tail parts, whatever the device-side tile count
+    if (tail) nb = std::max(nb, (unsigned)((max_mtiles * NT / gk.slots + 1) * gk.slots));
     if (FMT == EMBER_TYPE_Q4_K)
       gemm_dma_q8_kernel<GATED, kWfQ4Pack><<<nb, kDmaThreads, kDmaLds, st>>>(gk, NT);
     else if (gk.Wp)
       gemm_dma_q8_kernel<GATED, kWfQ8Pack><<<nb, kDmaThreads, kDmaLds, st>>>(gk, NT);
     else
       gemm_dma_q8_kernel<GATED, kWfQ8Rows><<<nb, kDmaThreads, kDmaLds, st>>>(gk, NT);
-    return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
+    if (hipGetLastError() != hipSuccess) return EMBER_ERR_LAUNCH;
+    if (tail) {
+      gemm_tail_fixup_kernel<<<(unsigned)(gk.slots / 2), 256, 0, st>>>(gk, NT);
+      if (hipGetLastError() != hipSuccess) return EMBER_ERR_LAUNCH;
+    }
+    return EMBER_OK;
   }
   if (g.split_bf16) return EMBER_ERR_TYPE;  // the split path runs in the 64-token-tile kernel only
   gemm_kernel<FMT, GATED><<<blocks, kGemmThreads, kGemmLds, st>>>(g, NT);

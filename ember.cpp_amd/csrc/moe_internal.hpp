@@ -237,7 +237,16 @@ struct GemmArgs {
   // part_h + (s * part_rows + p) * 2N (+ N for up), finished by a SwiGLU pass
   float* part_h;
   int part_rows;
+  // 256-token-tile gate/up (DMA kernels): the work items past the last whole round of `slots` blocks (the
+  // tail) split over K into up to tail_parts parts, raw partials at part_h as above (part_rows = T k),
+  // finished by gemm_tail_fixup_kernel. tail_parts <= 1: no split.
+  int tail_parts, slots;
 };
+// Parts of the tail split (GemmArgs::tail_parts) for a gated 256-token-tile launch of T k rows against
+// N = d_ff columns over K = d: 0 when it does not apply (the partials' size bound); and the resident blocks
+// per round (a multiple of 8).
+int gemm_tail_parts(int type, bool packed, int rows, int N, int K);
+int gemm_slots();
 // The prefill pack of a BF16 layer: per weight row the exponent e (int16) that puts the row's largest
 // finite magnitude in [0.5, 1) (clamped to [-120, 120]; 0 for a row of zeros), for the routed gate [E][d_ff],
 // up [E][d_ff], down [E][d], then per expert the largest gate + up exponent of its rows [E]; then, when the

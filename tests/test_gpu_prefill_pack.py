@@ -62,16 +62,20 @@ def test_pack_deepseek_style_with_shared_expert(gpu):
                                           (512, 768, 8, 2, 40)])
 def test_q4_k_pack_same_bits_as_register_staged(gpu, monkeypatch, d, d_ff, E, k, T):
     """Both runs forced onto the 256-token tiles (EMBER_MOE_PATH=gemm): the packed DMA kernel and the
-    register-staged one form the same fp16 operands and pair the same K elements in each MFMA."""
+    register-staged one form the same fp16 operands and pair the same K elements in each MFMA. (The DMA
+    kernel's tail split, which sums the K parts of the last round's tiles separately, is off for the
+    comparison: EMBER_TAIL_PARTS=1.)"""
     spec = em.LayerSpec(d=d, d_ff=d_ff, E=E, k=k, wtype=em.Q4_K, seed=24)
     hl = em.make_host_layer(spec)
     x = em.make_input(spec, T)
     print(f"prefill pack q4_k d={d} d_ff={d_ff} E={E} T={T}", flush=True)
     y_default = _run(hl, x, pack=True)
     monkeypatch.setenv("EMBER_MOE_PATH", "gemm")
+    monkeypatch.setenv("EMBER_TAIL_PARTS", "1")
     y_rows = _run(hl, x, pack=False)
     y_pack = _run(hl, x, pack=True)
     monkeypatch.delenv("EMBER_MOE_PATH")
+    monkeypatch.delenv("EMBER_TAIL_PARTS")
     assert same_bits(y_pack, y_rows)
     assert rel_l2(y_default, run_oracle(hl, x)) < 2e-3
 
