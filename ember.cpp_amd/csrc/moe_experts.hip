@@ -568,6 +568,37 @@ __device__ __attribute__((always_inline)) void route_publish(const ProjArgs& a, 
   }
 }
 
+// Router logits of a few tokens (the launch before the expert GEMMs of a small batch): block (e, t) computes
+// logit [t][e] with router_block_logit (the one-token launch's exact FP64 chains: products formed in
+// parallel, each chain added in order), so a batch of T tokens costs one such block per pair.
+__global__ void __launch_bounds__(512) router_logits_blocks(const float* __restrict__ x, const float* __restrict__ R,
+                                                            float* __restrict__ logits, int T, int d, int E) {
+  extern __shared__ __align__(16) uint8_t rb_lds[];
+  ProjArgs a{};
+  a.route.x = x + (size_t)blockIdx.y * d;
+  a.route.router = R;
+  a.route.d = d;
+  a.route.E = E;
+  const float v = router_block_logit<512, false>(a, blockIdx.x, rb_lds);
+  if (threadIdx.x == 0) logits[(size_t)blockIdx.y * E + blockIdx.x] = v;
+}
+
+bool router_blocks_fit(int T, int d, int E) {
+  return d % 4 == 0 && d <= 16 * 512 && (int64_t)T * E <= 1024 && T <= 65535;
+}
+
+int launch_router_logits_blocks(const float* x, int T, int d, int E, const float* R, float* logits, hipStream_t st) {
+  if (!router_blocks_fit(T, d, E)) return EMBER_ERR_SHAPE;
+  const size_t lds = fused_router_lds(d);
+  if (lds > kProjLdsBytes) return EMBER_ERR_SHAPE;
+  static const bool lds_ok = hipFuncSetAttribute(reinterpret_cast<const void*>(&router_logits_blocks),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (int)kProjLdsBytes) == hipSuccess;
+  if (!lds_ok) return EMBER_ERR_LAUNCH;
+  router_logits_blocks<<<dim3(E, T), 512, lds, st>>>(x, R, logits, T, d, E);
+  return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
+}
+
 // Every block (router blocks after their own logit): collects every expert's tagged logit (bounded
 // wait), runs route_token (exp tables staged at the start of the launch; every block computes the same
 // routing, so no second hop through one block is needed) and fills its dispatch arrays; block 0 also

@@ -268,6 +268,7 @@ __device__ inline bool xcd_item(int M, int NT, int KS, int& mt, int& rem) {
 // for blocks R slots + i part i % S of tail item R slots + i / S, S = min(tail_parts, slots / tail) (S = 1: no
 // split; slots is a multiple of 8). Returns false for a block without an item; part / parts: this block's
 // K part.
+constexpr int kMaxTailParts = 8;
 // The tail split of a gated launch of W = M x NT items: S parts per tail item (1: no split), capped at the
 // K tiles so that every part holds at least one; `full` = the items of the whole rounds (W without a split).
 __device__ inline int tail_split(const GemmArgs& g, int W, int& full) {
@@ -275,7 +276,7 @@ __device__ inline int tail_split(const GemmArgs& g, int W, int& full) {
   if (g.tail_parts <= 1 || g.slots <= 0) return 1;
   const int R = W / g.slots, tail = W - R * g.slots;
   if (tail == 0) return 1;
-  const int S = min(min(g.tail_parts, g.slots / tail), g.K / GBK);
+  const int S = min(min(min(g.tail_parts, kMaxTailParts), g.slots / tail), g.K / GBK);
   if (S <= 1) return 1;
   full = R * g.slots;
   return S;
@@ -1228,10 +1229,20 @@ __global__ void __launch_bounds__(256) gemm_tail_fixup_kernel(GemmArgs g, int NT
     const int m = i / BN, c = i % BN, n = n0 + c;
     if (n >= N) continue;
     const float* part = g.part_h + (size_t)(p0 + m) * 2 * N + n;
-    float ga = part[0], ua = part[N];
-    for (int s = 1; s < S; ++s) {
-      ga = ga + part[s * stride];
-      ua = ua + part[s * stride + N];
+    // every part's loads issued before the ordered sum
+    float pg[kMaxTailParts], pu[kMaxTailParts];
+#pragma unroll
+    for (int s = 0; s < kMaxTailParts; ++s) {
+      pg[s] = s < S ? part[s * stride] : 0.0f;
+      pu[s] = s < S ? part[s * stride + N] : 0.0f;
+    }
+    float ga = pg[0], ua = pu[0];
+#pragma unroll
+    for (int s = 1; s < kMaxTailParts; ++s) {
+      if (s < S) {
+        ga = ga + pg[s];
+        ua = ua + pu[s];
+      }
     }
     store_h(g, (size_t)(p0 + m) * N + n, p0 + m, row_exp(g, p0 + m), ga, ua, c == 0);
   }
@@ -1263,7 +1274,7 @@ int gemm_slots() { return device_cus() / 8 * 8; }
 // EMBER_TAIL_PARTS (read per call) caps the parts; 1 turns the split off.
 int gemm_tail_parts(int type, bool packed, int rows, int N, int K) {
   const char* e = std::getenv("EMBER_TAIL_PARTS");
-  const int cap = e ? atoi(e) : 8;
+  const int cap = std::min(e ? atoi(e) : kMaxTailParts, kMaxTailParts);
   if (!dma_path(type, packed) || rows <= 0 || N <= 0) return 0;
   const int64_t per = (int64_t)rows * 2 * N * 4;
   const int p = (int)std::min<int64_t>(std::min(cap, K / GBK), ((int64_t)16 << 20) / per);

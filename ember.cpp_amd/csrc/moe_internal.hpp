@@ -57,6 +57,10 @@ struct DispatchScratch {
 };
 
 int launch_router_logits(const float* x, int T, int d, int E, const float* R, float* logits, hipStream_t st);
+// Router logits of a small batch, one block per (expert, token) pair (router_block_logit's exact chains):
+// for T E <= 1024, d % 4 == 0, d <= 8192.
+bool router_blocks_fit(int T, int d, int E);
+int launch_router_logits_blocks(const float* x, int T, int d, int E, const float* R, float* logits, hipStream_t st);
 // conv (nullable): activation conversion run by extra blocks of the same launch
 int launch_route(const float* logits, int T, int E, int k, int renorm, int routed, int sigmoid, const float* bias,
                  int groups_n, int groups_top, int32_t* idx, float* gates, const ActConv* conv, hipStream_t st);

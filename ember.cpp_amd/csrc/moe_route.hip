@@ -654,6 +654,9 @@ int launch_router_logits(const float* x, int T, int d, int E, const float* R, fl
     } else {
       router_logits_chains<4, 8, 4, 4, 128><<<dim3((T + 15) / 16, (E + 31) / 32), 256, 0, st>>>(x, R, logits, T, d, E);
     }
+  } else if (router_blocks_fit(T, d, E)) {
+    // a few pairs: one block each, its products formed in parallel (the one-token launch's router blocks)
+    return launch_router_logits_blocks(x, T, d, E, R, logits, st);
   } else if (2 * (d + 8) <= kRouterLdsFloats && (lds_blocks <= 1024 || d % 4)) {
     // few blocks: each stages whole rows once and runs its chains from LDS (one memory latency)
     static const bool lds_ok =
