@@ -561,7 +561,9 @@ __device__ inline half8 b_frag(const uint8_t* row, int h) {
   }
 }
 
-template <bool GATED, int WF>
+// TAIL (gated only): the launch carries a tail split (gated_item); the other instantiation is the plain
+// XCD-balanced mapping.
+template <bool GATED, int WF, bool TAIL = false>
 __global__ void __launch_bounds__(kDmaThreads) gemm_dma_q8_kernel(GemmArgs g, int NT) {
   constexpr int BN = GATED ? 128 : 256;
   constexpr int kRowB = DmaW<WF>::kRowB;       // LDS bytes per weight row
@@ -572,10 +574,10 @@ __global__ void __launch_bounds__(kDmaThreads) gemm_dma_q8_kernel(GemmArgs g, in
 
   // block -> (m-tile, n-tile, K split part), XCD-balanced
   int KS, mt, nt, ks;
-  if constexpr (GATED) {
+  if constexpr (GATED && TAIL) {
     if (!gated_item(g, NT, mt, nt, ks, KS)) return;
   } else {
-    KS = g.ksplit;
+    KS = GATED ? 1 : g.ksplit;
     int rem;
     if (!xcd_item(launch_mtiles(g, GBM), NT, KS, mt, rem)) return;
     nt = rem / KS;
@@ -782,7 +784,7 @@ __global__ void __launch_bounds__(kDmaThreads) gemm_dma_q8_kernel(GemmArgs g, in
           const size_t o = (size_t)(p0 + m) * N + n;
           const int ex = s_rexp[m];
           if constexpr (GATED) {
-            if (KS > 1) {  // a tail item's K part: raw partial dots, gemm_tail_fixup_kernel finishes the tile
+            if (TAIL && KS > 1) {  // a tail item's K part: raw partial dots, gemm_tail_fixup_kernel finishes the tile
               float* part = g.part_h + ((size_t)ks * g.part_rows + p0 + m) * 2 * N + n;
               part[0] = acc[i][0][4 * ii + jj];
               part[N] = acc[i][1][4 * ii + jj];
@@ -1308,12 +1310,30 @@ int launch_gemm_fmt(const GemmArgs& g, int max_mtiles, hipStream_t st) {
     unsigned nb = blocks * (unsigned)gk.ksplit;
     // with a tail split: every whole round plus one round of tail parts, whatever the device-side tile count
     if (tail) nb = std::max(nb, (unsigned)((max_mtiles * NT / gk.slots + 1) * gk.slots));
-    if (FMT == EMBER_TYPE_Q4_K)
+    if (tail) {
+      if constexpr (GATED) {
+        static const bool tail_ok =
+            hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma_q8_kernel<true, kWfQ8Rows, true>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDmaLds) == hipSuccess &&
+            hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma_q8_kernel<true, kWfQ8Pack, true>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDmaLds) == hipSuccess &&
+            hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma_q8_kernel<true, kWfQ4Pack, true>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDmaLds) == hipSuccess;
+        if (!tail_ok) return EMBER_ERR_LAUNCH;
+        if (FMT == EMBER_TYPE_Q4_K)
+          gemm_dma_q8_kernel<true, kWfQ4Pack, true><<<nb, kDmaThreads, kDmaLds, st>>>(gk, NT);
+        else if (gk.Wp)
+          gemm_dma_q8_kernel<true, kWfQ8Pack, true><<<nb, kDmaThreads, kDmaLds, st>>>(gk, NT);
+        else
+          gemm_dma_q8_kernel<true, kWfQ8Rows, true><<<nb, kDmaThreads, kDmaLds, st>>>(gk, NT);
+      }
+    } else if (FMT == EMBER_TYPE_Q4_K) {
       gemm_dma_q8_kernel<GATED, kWfQ4Pack><<<nb, kDmaThreads, kDmaLds, st>>>(gk, NT);
-    else if (gk.Wp)
+    } else if (gk.Wp) {
       gemm_dma_q8_kernel<GATED, kWfQ8Pack><<<nb, kDmaThreads, kDmaLds, st>>>(gk, NT);
-    else
+    } else {
       gemm_dma_q8_kernel<GATED, kWfQ8Rows><<<nb, kDmaThreads, kDmaLds, st>>>(gk, NT);
+    }
     if (hipGetLastError() != hipSuccess) return EMBER_ERR_LAUNCH;
     if (tail) {
       gemm_tail_fixup_kernel<<<(unsigned)(gk.slots / 2), 256, 0, st>>>(gk, NT);
