@@ -487,6 +487,11 @@ constexpr int kDmaB = 256 * kDmaRowB;            // weight bytes per stage (20 K
 constexpr int kDmaStage = kDmaA + kDmaB;
 constexpr size_t kDmaLds = (size_t)kDmaStages * kDmaStage;
 constexpr int kDmaInstA = kDmaA / 1024 / 8;      // 16-byte DMA instructions per wave per tile: activations (4)
+// launches of at most 64 tokens (every segment, hence every tile, holds at most 64 rows: a token picks an
+// expert once): 64 activation rows per stage (8 KiB) and five stages, four tiles in flight
+constexpr int kDmaStagesShort = 5, kShortRows = 64;
+constexpr int kDmaAShort = kShortRows * GBK * 2;
+constexpr size_t kDmaLdsShort = (size_t)kDmaStagesShort * (kDmaAShort + kDmaB);
 
 __device__ inline void lds_dma16(const void* g, uint8_t* lds) {
   __builtin_amdgcn_global_load_lds(g, (lds_void_t*)lds, 16, 0, 0);
@@ -562,14 +567,19 @@ __device__ inline half8 b_frag(const uint8_t* row, int h) {
 }
 
 // TAIL (gated only): the launch carries a tail split (gated_item); the other instantiation is the plain
-// XCD-balanced mapping.
-template <bool GATED, int WF, bool TAIL = false>
+// XCD-balanced mapping. SHORT: the launch has at most 64 tokens (kDmaStagesShort).
+template <bool GATED, int WF, bool TAIL = false, bool SHORT = false>
 __global__ void __launch_bounds__(kDmaThreads) gemm_dma_q8_kernel(GemmArgs g, int NT) {
   constexpr int BN = GATED ? 128 : 256;
   constexpr int kRowB = DmaW<WF>::kRowB;       // LDS bytes per weight row
   constexpr int kLastB = DmaW<WF>::kInst - 1;  // last weight DMA instruction
   constexpr int kDmaInstB = (DmaW<WF>::kInst + 7) / 8;  // weight DMA instructions per wave (the last shared)
-  constexpr int kDmaInst = kDmaInstA + kDmaInstB;
+  constexpr int NS = SHORT ? kDmaStagesShort : kDmaStages;  // LDS stages
+  constexpr int kAB = SHORT ? kDmaAShort : kDmaA;           // activation bytes per stage
+  constexpr int kStage = kAB + kDmaB;
+  constexpr int kInstA = kAB / 1024 / 8;                    // activation DMA instructions per wave (1 or 4)
+  constexpr int kInstMax = kInstA > kDmaInstB ? kInstA : kDmaInstB;
+  constexpr int kDmaInst = kInstA + kDmaInstB;
   extern __shared__ __align__(16) uint8_t dsm[];
 
   // block -> (m-tile, n-tile, K split part), XCD-balanced
@@ -604,20 +614,20 @@ __global__ void __launch_bounds__(kDmaThreads) gemm_dma_q8_kernel(GemmArgs g, in
   // wave w runs on SIMD w % 4, so each SIMD holds one wave of each M half: a tile whose rows end
   // inside the first half leaves no SIMD with double work
   const int wm = wave >> 2, wn = wave & 3;
-  // 32-row subtiles of this wave's M half that hold tokens (0..4); the others are skipped
-  const int msub = min(4, max(0, (rows - 128 * wm + 31) >> 5));
+  // 32-row subtiles of this wave's M half that hold tokens (0..4; SHORT: 0..2); the others are skipped
+  const int msub = min(SHORT ? kShortRows / 32 : 4, max(0, (rows - 128 * wm + 31) >> 5));
 
   // DMA sources, the same code in every wave (no branches in the K loop): DMA instruction j of a
-  // tile fills 16-byte granules 64 j + lane. Activations: instructions 4 w + i (i < 4); granule gi is
-  // row gi / 8, slot gi % 8 holding K granule slot ^ ((row / 2) % 8); rows past the tile repeat its last
-  // row.
+  // tile fills 16-byte granules 64 j + lane. Activations: instructions 4 w + i (i < 4; SHORT: w, rows
+  // 8 w .. 8 w + 7); granule gi is row gi / 8, slot gi % 8 holding K granule slot ^ ((row / 2) % 8); rows
+  // past the tile repeat its last row.
   // Weights: instructions min(3 w + i, 19) (i < 3; waves 6 and 7 repeat instruction 19, which rewrites
   // identical bytes); granule gb is row gb / 5, part gb % 5 = bytes 16 part (parts 0-3) or 52.
-  const uint8_t* srcA[kDmaInstA];
+  const uint8_t* srcA[kInstA];
   const uint8_t* srcB[kDmaInstB];
 #pragma unroll
-  for (int i = 0; i < kDmaInstA; ++i) {
-    const int gi = 64 * (kDmaInstA * wave + i) + lane;
+  for (int i = 0; i < kInstA; ++i) {
+    const int gi = 64 * (kInstA * wave + i) + lane;
     const int r = gi >> 3, kg = (gi & 7) ^ ((r >> 1) & 7);
     const int p = p0 + min(r, rows - 1);
     srcA[i] = reinterpret_cast<const uint8_t*>(g.A + (size_t)(g.perm ? g.perm[p] / g.k : p) * K + 8 * kg);
@@ -641,14 +651,18 @@ __global__ void __launch_bounds__(kDmaThreads) gemm_dma_q8_kernel(GemmArgs g, in
   // per-tile DMA count, and the waits that count it, are the weights' alone
   auto issue = [&](int kt, int j, auto NOAc) {
     const int kc = kt0 + min(kt, nk - 1);
-    uint8_t* st = dsm + (kt % kDmaStages) * kDmaStage;
-    if constexpr (!decltype(NOAc)::value) lds_dma16(srcA[j] + (size_t)kc * GBK * 2, st + 1024 * (kDmaInstA * wave + j));
+    uint8_t* st = dsm + (kt % NS) * kStage;
+    if constexpr (!decltype(NOAc)::value) {
+      if (j < kInstA)
+        lds_dma16(srcA[j < kInstA ? j : 0] + (size_t)kc * GBK * 2, st + 1024 * (kInstA * wave + j));
+    }
     if (j < kDmaInstB)
-      lds_dma16(srcB[j] + (size_t)kc * DmaW<WF>::kStride, st + kDmaA + 1024 * min(kDmaInstB * wave + j, kLastB));
+      lds_dma16(srcB[j < kDmaInstB ? j : 0] + (size_t)kc * DmaW<WF>::kStride,
+                st + kAB + 1024 * min(kDmaInstB * wave + j, kLastB));
   };
   auto issue_all = [&](int kt, auto NOAc) {
 #pragma unroll
-    for (int j = 0; j < kDmaInstA; ++j) issue(kt, j, NOAc);
+    for (int j = 0; j < kInstMax; ++j) issue(kt, j, NOAc);
   };
 
   floatx16 acc[4][2];
@@ -680,7 +694,7 @@ __global__ void __launch_bounds__(kDmaThreads) gemm_dma_q8_kernel(GemmArgs g, in
       const int r = wm * 128 + 32 * i + (lane & 31);
       f.a[i] = *reinterpret_cast<const half8*>(st + 16 * (8 * r + (gk ^ ((r >> 1) & 7))));
     }
-    const uint8_t* Bs = st + kDmaA;
+    const uint8_t* Bs = st + kAB;
 #pragma unroll
     for (int jn = 0; jn < 2; ++jn) f.b[jn] = b_frag<WF, ks>(Bs + kRowB * brow_of(jn), h);
   };
@@ -704,62 +718,66 @@ __global__ void __launch_bounds__(kDmaThreads) gemm_dma_q8_kernel(GemmArgs g, in
   // kt % 3 may be refilled next iteration), and reads and decodes K step 0 of tile kt + 1 while the
   // MFMAs of K step 3 of tile kt run. (The last iteration reads tile nk, a clamped reload, unused.)
   // A wave whose M half holds no tokens (MS = 0) only loads and keeps the barriers.
-  static_assert(kDmaStages == 3, "the waits below assume one tile in flight beyond the current one");
+  // (NS stages: tiles kt + 1 .. kt + NS - 2 are in flight while tile kt is multiplied; the iteration
+  // issues tile kt + NS - 1 and then waits for tile kt + 1, leaving NS - 2 tiles' DMA outstanding)
   auto k_loop = [&](auto MSc, auto NOAc) {
     constexpr int kInst = decltype(NOAc)::value ? kDmaInstB : kDmaInst;  // this wave's DMA per tile
     using K0 = std::integral_constant<int, 0>;
     using K1 = std::integral_constant<int, 1>;
     using K2 = std::integral_constant<int, 2>;
     using K3 = std::integral_constant<int, 3>;
-    issue_all(0, NOAc);
-    issue_all(1, NOAc);
-    wait_vmcnt<kInst>();
+#pragma unroll
+    for (int t = 0; t < NS - 1; ++t) issue_all(t, NOAc);
+    wait_vmcnt<(NS - 2) * kInst>();
     barrier();
     Frags f0, f1;
     if constexpr (decltype(MSc)::value > 0) load_frags(dsm, K0{}, MSc, f0);
     for (int kt = 0; kt < nk; ++kt) {
       if constexpr (decltype(MSc)::value == 0) {
-        issue_all(kt + 2, NOAc);
-        wait_vmcnt<kInst>();
+        issue_all(kt + NS - 1, NOAc);
+        wait_vmcnt<(NS - 2) * kInst>();
         barrier();
       } else {
-        const uint8_t* st = dsm + (kt % kDmaStages) * kDmaStage;
+        const uint8_t* st = dsm + (kt % NS) * kStage;
         load_frags(st, K1{}, MSc, f1);
-        issue(kt + 2, 0, NOAc);
+        issue(kt + NS - 1, 0, NOAc);
         mfmas(f0, MSc);
         load_frags(st, K2{}, MSc, f0);
-        issue(kt + 2, 1, NOAc);
+        issue(kt + NS - 1, 1, NOAc);
         mfmas(f1, MSc);
         load_frags(st, K3{}, MSc, f1);
-        issue(kt + 2, 2, NOAc);
+        issue(kt + NS - 1, 2, NOAc);
         mfmas(f0, MSc);
-        issue(kt + 2, 3, NOAc);
-        wait_vmcnt<kInst>();
+        issue(kt + NS - 1, 3, NOAc);
+        wait_vmcnt<(NS - 2) * kInst>();
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of tile kt are complete
         barrier();
-        load_frags(dsm + ((kt + 1) % kDmaStages) * kDmaStage, K0{}, MSc, f0);
+        load_frags(dsm + ((kt + 1) % NS) * kStage, K0{}, MSc, f0);
         mfmas(f1, MSc);
       }
     }
   };
   __shared__ int s_rexp[GBM];
   load_row_exps(g, p0, rows, s_rexp);
-  // waves whose activation rows (32 w .. 32 w + 31) lie past the tile's tokens load none: a short tile's
-  // DMA is then its weights and only the activation rows it holds (wave-uniform)
+  // waves whose activation rows (32 w .. 32 w + 31; SHORT: 8 w .. 8 w + 7) lie past the tile's tokens load
+  // none: a short tile's DMA is then its weights and only the activation rows it holds (wave-uniform)
   using A1 = std::integral_constant<bool, false>;
   using A0 = std::integral_constant<bool, true>;
-  if (32 * wave >= rows) {
+  // (SHORT: msub <= 2, so the 3- and 4-subtile loops are not built)
+  using M4 = std::integral_constant<int, SHORT ? 2 : 4>;
+  using M3 = std::integral_constant<int, SHORT ? 2 : 3>;
+  if (8 * kInstA * wave >= rows) {
     switch (msub) {
-      case 4: k_loop(std::integral_constant<int, 4>{}, A0{}); break;
-      case 3: k_loop(std::integral_constant<int, 3>{}, A0{}); break;
+      case 4: k_loop(M4{}, A0{}); break;
+      case 3: k_loop(M3{}, A0{}); break;
       case 2: k_loop(std::integral_constant<int, 2>{}, A0{}); break;
       case 1: k_loop(std::integral_constant<int, 1>{}, A0{}); break;
       default: k_loop(std::integral_constant<int, 0>{}, A0{}); break;
     }
   } else {
     switch (msub) {
-      case 4: k_loop(std::integral_constant<int, 4>{}, A1{}); break;
-      case 3: k_loop(std::integral_constant<int, 3>{}, A1{}); break;
+      case 4: k_loop(M4{}, A1{}); break;
+      case 3: k_loop(M3{}, A1{}); break;
       case 2: k_loop(std::integral_constant<int, 2>{}, A1{}); break;
       case 1: k_loop(std::integral_constant<int, 1>{}, A1{}); break;
       default: k_loop(std::integral_constant<int, 0>{}, A1{}); break;
@@ -1283,6 +1301,27 @@ int gemm_tail_parts(int type, bool packed, int rows, int N, int K) {
   return p >= 2 ? p : 0;
 }
 
+// One DMA tile launch: the weight format's instantiation (Q4_K pack, Q8_0 pack, Q8_0 rows), its LDS.
+template <bool GATED, bool TAIL, bool SHORT>
+int launch_dma(int type, const GemmArgs& gk, int NT, unsigned nb, hipStream_t st) {
+  constexpr size_t lds = SHORT ? kDmaLdsShort : kDmaLds;
+  static const bool ok =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma_q8_kernel<GATED, kWfQ8Rows, TAIL, SHORT>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) == hipSuccess &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma_q8_kernel<GATED, kWfQ8Pack, TAIL, SHORT>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) == hipSuccess &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma_q8_kernel<GATED, kWfQ4Pack, TAIL, SHORT>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) == hipSuccess;
+  if (!ok) return EMBER_ERR_LAUNCH;
+  if (type == EMBER_TYPE_Q4_K)
+    gemm_dma_q8_kernel<GATED, kWfQ4Pack, TAIL, SHORT><<<nb, kDmaThreads, lds, st>>>(gk, NT);
+  else if (gk.Wp)
+    gemm_dma_q8_kernel<GATED, kWfQ8Pack, TAIL, SHORT><<<nb, kDmaThreads, lds, st>>>(gk, NT);
+  else
+    gemm_dma_q8_kernel<GATED, kWfQ8Rows, TAIL, SHORT><<<nb, kDmaThreads, lds, st>>>(gk, NT);
+  return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ERR_LAUNCH;
+}
+
 template <int FMT, bool GATED>
 int launch_gemm_fmt(const GemmArgs& g, int max_mtiles, hipStream_t st) {
   constexpr int BN = GATED ? 128 : 256;
@@ -1295,14 +1334,6 @@ int launch_gemm_fmt(const GemmArgs& g, int max_mtiles, hipStream_t st) {
   const unsigned blocks = (unsigned)(8 * mgroups * NT);
   if (max_mtiles == 0 || NT == 0) return EMBER_OK;
   if (dma_path(FMT, g.Wp != nullptr)) {
-    static const bool dma_ok =
-        hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma_q8_kernel<GATED, kWfQ8Rows>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDmaLds) == hipSuccess &&
-        hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma_q8_kernel<GATED, kWfQ8Pack>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDmaLds) == hipSuccess &&
-        hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma_q8_kernel<GATED, kWfQ4Pack>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDmaLds) == hipSuccess;
-    if (!dma_ok) return EMBER_ERR_LAUNCH;
     GemmArgs gk = g;
     if (GATED || gk.ksplit < 1) gk.ksplit = 1;
     const bool tail = GATED && gk.tail_parts > 1 && gk.slots > 0 && gk.part_h && gk.tiles;
@@ -1310,31 +1341,20 @@ int launch_gemm_fmt(const GemmArgs& g, int max_mtiles, hipStream_t st) {
     unsigned nb = blocks * (unsigned)gk.ksplit;
     // with a tail split: every whole round plus one round of tail parts, whatever the device-side tile count
     if (tail) nb = std::max(nb, (unsigned)((max_mtiles * NT / gk.slots + 1) * gk.slots));
-    if (tail) {
-      if constexpr (GATED) {
-        static const bool tail_ok =
-            hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma_q8_kernel<true, kWfQ8Rows, true>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDmaLds) == hipSuccess &&
-            hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma_q8_kernel<true, kWfQ8Pack, true>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDmaLds) == hipSuccess &&
-            hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma_q8_kernel<true, kWfQ4Pack, true>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDmaLds) == hipSuccess;
-        if (!tail_ok) return EMBER_ERR_LAUNCH;
-        if (FMT == EMBER_TYPE_Q4_K)
-          gemm_dma_q8_kernel<true, kWfQ4Pack, true><<<nb, kDmaThreads, kDmaLds, st>>>(gk, NT);
-        else if (gk.Wp)
-          gemm_dma_q8_kernel<true, kWfQ8Pack, true><<<nb, kDmaThreads, kDmaLds, st>>>(gk, NT);
-        else
-          gemm_dma_q8_kernel<true, kWfQ8Rows, true><<<nb, kDmaThreads, kDmaLds, st>>>(gk, NT);
-      }
-    } else if (FMT == EMBER_TYPE_Q4_K) {
-      gemm_dma_q8_kernel<GATED, kWfQ4Pack><<<nb, kDmaThreads, kDmaLds, st>>>(gk, NT);
-    } else if (gk.Wp) {
-      gemm_dma_q8_kernel<GATED, kWfQ8Pack><<<nb, kDmaThreads, kDmaLds, st>>>(gk, NT);
+    // at most 64 tokens: no tile holds more than 64 rows (EMBER_GEMM_SHORT=0, read per call: the
+    // three-stage kernel anyway, whose outputs the short one matches bit for bit)
+    const char* sv = std::getenv("EMBER_GEMM_SHORT");
+    const bool shrt = g.T <= kShortRows && !(sv && atoi(sv) == 0);
+    int s = EMBER_OK;
+    if constexpr (GATED) {
+      if (tail)
+        s = shrt ? launch_dma<true, true, true>(FMT, gk, NT, nb, st) : launch_dma<true, true, false>(FMT, gk, NT, nb, st);
+      else
+        s = shrt ? launch_dma<true, false, true>(FMT, gk, NT, nb, st) : launch_dma<true, false, false>(FMT, gk, NT, nb, st);
     } else {
-      gemm_dma_q8_kernel<GATED, kWfQ8Rows><<<nb, kDmaThreads, kDmaLds, st>>>(gk, NT);
+      s = shrt ? launch_dma<false, false, true>(FMT, gk, NT, nb, st) : launch_dma<false, false, false>(FMT, gk, NT, nb, st);
     }
-    if (hipGetLastError() != hipSuccess) return EMBER_ERR_LAUNCH;
+    if (s) return s;
     if (tail) {
       gemm_tail_fixup_kernel<<<(unsigned)(gk.slots / 2), 256, 0, st>>>(gk, NT);
       if (hipGetLastError() != hipSuccess) return EMBER_ERR_LAUNCH;
