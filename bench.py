@@ -105,22 +105,53 @@ def algorithmic(spec, T, U, path_bits=0):
     return gu, layer, flops
 
 
+# Consecutive calls of one layer would find part of the previous call's weights in the device's 256 MB
+# last-level cache, which the layers of a model (each its own weights) do not: the timed calls cycle through
+# copies of the layer, enough that a copy's weights are read again only after twice the cache's bytes.
+LLC_BYTES = 256 << 20
+MAX_COPIES = 16
+
+
+def copies_needed(touched_bytes):
+    return max(1, min(MAX_COPIES, -(-2 * LLC_BYTES // max(1, int(touched_bytes)))))
+
+
+def layer_copies(dl, n, log_prefix):
+    """dl and n - 1 device copies of it (DeviceLayer.clone)."""
+    import torch
+
+    dls = [dl]
+    for _ in range(n - 1):
+        dls.append(dl.clone())
+    torch.cuda.synchronize()
+    if n > 1:
+        log(f"{log_prefix} timing over {n} copies of the layer")
+    return dls
+
+
 def run_sweep(em, spec, dl, sweep_T, steps, warmup, log_prefix="[bench]"):
-    """Per token count: eager and graph timing of the layer call, per-phase times and the roofline
-    fractions; returns {T: entry}."""
+    """Per token count: eager and graph timing of the layer call (cycling through copies of the layer, see
+    LLC_BYTES), per-phase times and the roofline fractions; returns {T: entry}."""
     import torch
 
     results = {}
+    xs, need = {}, 1
     for T in sweep_T:
-        x_host = em.make_input(spec, T)
-        x = torch.from_numpy(x_host).cuda()
+        xs[T] = torch.from_numpy(em.make_input(spec, T)).cuda()
+        U = realised_experts(em, dl, xs[T], T)
+        need = max(need, copies_needed(algorithmic(spec, T, U, em.path(dl.desc, T))[1]))
+    dls = layer_copies(dl, need, log_prefix)
+    for T in sweep_T:
+        x = xs[T]
         U = realised_experts(em, dl, x, T)
         bits = em.path(dl.desc, T)
-        eager_ms, graph_ms, phases, _ = time_layer(em, dl, x, T, steps, warmup)
-        best_ms = min(eager_ms, graph_ms) if graph_ms else eager_ms
         gu_bytes, layer_bytes, flops = algorithmic(spec, T, U, bits)
+        ncop = min(len(dls), copies_needed(layer_bytes))
+        eager_ms, graph_ms, phases, _ = time_layer(em, dls[:ncop], x, T, steps, warmup)
+        best_ms = min(eager_ms, graph_ms) if graph_ms else eager_ms
         gu_ms = phases["gate_up"]
-        results[T] = dict(T=T, experts_hit=U, path_bits=bits, us_per_layer=best_ms * 1e3, eager_us=eager_ms * 1e3,
+        results[T] = dict(T=T, experts_hit=U, path_bits=bits, layer_copies=ncop, us_per_layer=best_ms * 1e3,
+                          eager_us=eager_ms * 1e3,
                           layer_mfma_frac=flops / (best_ms * 1e-3) / (MFMA_PEAK_TFLOPS * 1e12),
                           graph_us=None if graph_ms is None else graph_ms * 1e3, tokens_per_s=T / (best_ms * 1e-3),
                           layer_hbm_frac=layer_bytes / (best_ms * 1e-3) / (HBM_PEAK_GBS * 1e9),
@@ -129,6 +160,8 @@ def run_sweep(em, spec, dl, sweep_T, steps, warmup, log_prefix="[bench]"):
                           layer_tflops=flops / (best_ms * 1e-3) / 1e12,
                           phases_us={p: round(v * 1e3, 2) for p, v in phases.items()})
         log(f"{log_prefix} T={T}: {json.dumps(results[T])}")
+    del dls
+    torch.cuda.empty_cache()
     return results
 
 
@@ -154,21 +187,24 @@ def nested_config(em, name, steps, warmup):
     return out
 
 
-def time_layer(em, dl, x, T, steps, warmup):
+def time_layer(em, dls, x, T, steps, warmup):
     """Eager timing of K steps bracketed by synchronisations and events on the launch stream, then HIP-graph
-    replays of the same call, GRAPH_CALLS calls per graph (each replay checked bit-identical to eager)."""
+    replays of the same calls, GRAPH_CALLS calls per graph (each replay checked bit-identical to eager).
+    Call i runs on copy i % len(dls) of the layer (the same weights)."""
     import torch
 
+    dl = dls[0]
+    R = len(dls)
     out = torch.empty_like(x)
     scratch = torch.empty(em.scratch_bytes(dl.desc, T), dtype=torch.uint8, device="cuda")
-    for _ in range(warmup):
-        dl.forward(x, out, scratch)
+    for i in range(max(warmup, R)):
+        dls[i % R].forward(x, out, scratch)
     torch.cuda.synchronize()
     st = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(st)
-    for _ in range(steps):
-        em.moe_ffn(dl.desc, x, T, out, scratch)
+    for i in range(steps):
+        em.moe_ffn(dls[i % R].desc, x, T, out, scratch)
     e1.record(st)
     torch.cuda.synchronize()
     eager_ms = e0.elapsed_time(e1) / steps
@@ -186,9 +222,10 @@ def time_layer(em, dl, x, T, steps, warmup):
             em.moe_ffn(dl.desc, x, T, out, scratch)  # warm on the capture stream
         st.wait_stream(s2)
         torch.cuda.synchronize()
+        ncalls = max(GRAPH_CALLS, R)
         with torch.cuda.graph(g):
-            for _ in range(GRAPH_CALLS):
-                status = em.moe_ffn(dl.desc, x, T, out, scratch)
+            for i in range(ncalls):
+                status = em.moe_ffn(dls[i % R].desc, x, T, out, scratch)
                 assert status == 0
         out.zero_()
         for _ in range(warmup):
@@ -196,13 +233,13 @@ def time_layer(em, dl, x, T, steps, warmup):
         torch.cuda.synchronize()
         if not torch.equal(out.view(torch.int32), ref_out.view(torch.int32)):
             raise RuntimeError("graph replay differs from eager output")
-        reps = max(1, steps // GRAPH_CALLS)
+        reps = max(1, steps // ncalls)
         e0.record(st)
         for _ in range(reps):
             g.replay()
         e1.record(st)
         torch.cuda.synchronize()
-        graph_ms = e0.elapsed_time(e1) / (reps * GRAPH_CALLS)
+        graph_ms = e0.elapsed_time(e1) / (reps * ncalls)
         if not torch.equal(out.view(torch.int32), ref_out.view(torch.int32)):
             raise RuntimeError("graph replay differs from eager output")
     except Exception as exc:  # the eager number stands alone
@@ -212,8 +249,8 @@ def time_layer(em, dl, x, T, steps, warmup):
     # their dispatch packets), i.e. what rocprofv3 --kernel-trace reports for them
     phases = {p: 0.0 for p in em.PHASES}
     n = max(3, min(steps, 20))
-    for _ in range(n):
-        for p, v in em.moe_ffn_timed(dl.desc, x, T, out, scratch).items():
+    for i in range(n):
+        for p, v in em.moe_ffn_timed(dls[i % R].desc, x, T, out, scratch).items():
             phases[p] += v / n
     return eager_ms, graph_ms, phases, out
 

@@ -481,6 +481,21 @@ class DeviceLayer:
             L.shared_gate = _ptr(t.get("shared_gate"))
         return dl
 
+    def clone(self) -> "DeviceLayer":
+        """A second device copy of the layer (every tensor, the prefill pack included) with its own
+        descriptor: the same weights at other addresses, e.g. to time calls that do not find the previous
+        call's weights in the device's last-level cache, as consecutive layers of a model do not."""
+        c = DeviceLayer(host=self.host)
+        ctypes.memmove(ctypes.byref(c.desc), ctypes.byref(self.desc), ctypes.sizeof(Layer))
+        fields = {"router": "router", "gate": "gate", "up": "up", "down": "down", "bias": "selection_bias",
+                  "gate_sh": "gate_shared", "up_sh": "up_shared", "down_sh": "down_shared",
+                  "shared_gate": "shared_gate", "pack": "prefill_pack"}
+        for name, t in self.tensors.items():
+            c.tensors[name] = t.clone()
+            if name in fields:
+                setattr(c.desc, fields[name], _ptr(c.tensors[name]))
+        return c
+
     def forward(self, x, out=None, scratch=None, stream=None):
         """Runs ember_moe_ffn on device tensor x [T][d]; returns (out, scratch)."""
         import torch

@@ -166,3 +166,23 @@ def test_qwen2moe_gated_shared_expert(gpu, wtype, T):
     routed decode launches; many: its own MFMA launches."""
     check(em.LayerSpec(d=512, d_ff=256, E=16, k=4, wtype=wtype, renorm=False, d_ff_shared=1024, shared_gated=True,
                        seed=41), T)
+
+
+def test_device_layer_clone(gpu):
+    """DeviceLayer.clone (the bench's copies of a layer, prefill pack included): the same output bits at
+    other addresses."""
+    import torch
+
+    spec = em.LayerSpec(d=512, d_ff=512, E=8, k=2, wtype=em.Q8_0, seed=71)
+    hl = em.make_host_layer(spec)
+    dl = em.DeviceLayer.upload(hl)
+    dl.tensors["pack"] = torch.empty(em.prefill_pack_bytes(dl.desc), dtype=torch.uint8, device="cuda")
+    em.prefill_pack(dl.desc, dl.tensors["pack"])
+    c = dl.clone()
+    assert c.desc.gate != dl.desc.gate and c.desc.prefill_pack not in (0, dl.desc.prefill_pack)
+    for T in (1, 8, 300):
+        x = torch.from_numpy(em.make_input(spec, T, seed=72)).cuda()
+        y0, _ = dl.forward(x)
+        y1, _ = c.forward(x)
+        torch.cuda.synchronize()
+        assert torch.equal(y0.view(torch.int32), y1.view(torch.int32)), T
