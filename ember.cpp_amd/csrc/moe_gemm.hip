@@ -12,11 +12,14 @@
 // of a layer is ~4e-4 (rel-L2), inside the 2e-3 bar for quantized stacks. F32 stacks never take this
 // path (their bar is 1e-5).
 //
-// Tiling: 256 threads = 4 waves in a 2x2 arrangement, BM = 128 tokens, K tiles of 64. gate/up:
-// BN = 128 columns of h (256 rows of W: 128 gate + 128 up), each wave 64x64 of both; down: BN = 256,
-// each wave 64x128. Tiles (expert, first token) come from a table the dispatch step writes, so
-// grid.x over-provisions m-tiles and extra blocks exit at once; grid.y covers N. Global loads of the
-// next K tile are issued before the MFMAs of the current one.
+// Kernels: gemm_dma_q8_kernel (Q8_0 rows or the prefill pack's Q8_0 / Q4_K tiles; 256-token tiles,
+// weights and activations loaded straight into LDS), gemm_dma64_q8_kernel (the same formats, 64-token
+// tiles), gemm_kernel and gemm_skinny_kernel (register-staged 256- / 64-token tiles for the other
+// formats). Tiles are (expert, first token) pairs from a table the dispatch step writes (dense rows:
+// consecutive token ranges); grids are sized for the most tiles a call can have, blocks take their work
+// items XCD-balanced from the device-side tile count, and blocks without one exit at once. The down
+// projection can split K over blocks (partial sums added in order by the combine); the 256-token gate/up
+// launch splits only the tiles of its partial last round (the tail split), which a fixup launch finishes.
 #include <cstdlib>
 #include <type_traits>
 
@@ -471,7 +474,8 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs g, int NT) 
 // ---------------------------------------------------------------------------------------------
 // Q8_0 grouped GEMM with direct global->LDS tile loads. Tiles of 256 tokens x 256 weight rows x 64 K
 // run through a ring of three LDS stages that global_load_lds fills without passing through
-// registers, so two tiles are in flight while one is multiplied. Every wave loads a share of both
+// registers, so two tiles are in flight while one is multiplied (launches of at most 64 tokens: 64-row
+// activation stages and five stages, four tiles in flight). Every wave loads a share of both
 // operands: the activation tile as 16-byte granules XOR-swizzled by row pair (the 16 rows that one
 // 16-lane pass of ds_read_b128 reads fall on distinct bank groups of the 64-bank LDS), the weight
 // tile in its Q8_0 bytes: the 68 bytes of a row's K tile as five 16-byte granules, the fifth
