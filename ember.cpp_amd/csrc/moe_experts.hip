@@ -9,16 +9,22 @@
 //  * F32 / F16 / BF16 weights: FP32 dots over the exactly-decoded weights and FP32 activations
 //    (F32 layers stay within 1e-4 max-abs / 1e-5 rel-L2 of the reference);
 //  * Q8_0 / Q4_K weights: the activations are quantized to int16 per 32-element block (scale
-//    amax/32767, relative error ~2e-5) and each block's integer dot runs on v_dot2_i32_i16 with
-//    the weights' quants zero-extended to 16 bits (Q8_0 offset by +128, corrected with the block's
-//    activation sum), then scaled in FP32. Relative error stays near 1e-5, far inside 2e-3.
+//    amax/32767, relative error ~2e-5) and each block's integer dot runs exactly in int32 (Q8_0: on
+//    v_dot2_i32_i16 with the quants zero-extended to 16 bits, offset by +128 and corrected with the
+//    block's activation sum; Q4_K: the nibbles straight into v_dot4 against the activations staged as
+//    byte planes), then scaled in FP32. Relative error stays near 1e-5, far inside 2e-3.
 //
-// Work layout: a lane owns a 32/64-element "chunk" of a row (fixed byte offset in the ggml row);
-// L lanes (a power of two <= 64) cover a row (looping when a row has more than L chunks), so a wave
-// covers 64/L rows. Each lane group walks row groups of RR rows (x2 for the gate/up pair) across
-// the whole segment (grid-stride), with the next step's weights loaded before the current step is
-// computed. grid.y enumerates expert segments (experts that received tokens, from the dispatch
-// step), so no host synchronisation is needed.
+// Work layout (proj_kernel): a lane owns a 32/64-element "chunk" of a row (fixed byte offset in the
+// ggml row); L lanes (a power of two <= 64) cover a row, so a wave covers 64/L rows; a ring of register
+// buffers keeps the next loads in flight. The launch is one resident wave of blocks that share the
+// expert segments (experts that received tokens, from the dispatch step, read on the device: no host
+// synchronisation) in proportion to their rows (seg_view).
+//
+// One-token calls fuse the router, the routing and the dispatch into the first launch (router blocks
+// publish tagged logits; the other blocks prove the pick set from bounded fast logits or wait for the
+// exact ones; block 0 writes the exact record and flags a contradiction), then run either the down
+// launch with the combine fused in (down1_kernel), or, with a Q8_0 / Q4_K prefill pack, the whole layer
+// as one launch over 64-column slices of d_ff (slice_kernel) plus an ordered reduce.
 #include <cstdlib>
 #include <type_traits>
 
