@@ -1,7 +1,9 @@
 // The C ABI of the MoE FFN (include/ember_moe.h): descriptor validation, the scratch layout and the
 // launch sequence router -> route -> dispatch -> gate/up(+SwiGLU) -> down -> [shared expert] ->
 // combine, all on the caller's stream with no host synchronisation (cuda_kernels.cu:3628-3684 has
-// the same shape: router GEMM, routing kernel, expert products, SwiGLU, combine).
+// the same shape: router GEMM, routing kernel, expert products, SwiGLU, combine). One-token calls fold
+// the first three into the gate/up launch, and with a prefill pack run the slice launch + reduce instead
+// (plan(): the launch plan, also reported by ember_moe_path).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>

@@ -7,7 +7,10 @@
 //    chains are kept strictly sequential.
 //  * top-k: k passes of argmax with strict > (ties to the lower index), picks sorted ascending.
 //  * gates: (float)(exp((double)(r - mx)) / z), z the ascending double sum, exp = glibc's algorithm
-//    (moe_math.hpp); the DeepSeek-style router runs the reference's float algorithm serially.
+//    (moe_math.hpp); the DeepSeek-style router runs the reference's float algorithm, as wave-parallel
+//    scans whose results equal its serial ones (a row with a NaN runs it serially on one lane).
+// (Small batches take their logits from router_logits_blocks in moe_experts.hip: the one-token
+// launch's per-expert blocks, one per (expert, token).)
 // The dispatch permutation has no reference counterpart: slots s = t*k + j are stably sorted by
 // expert id (offsets[E+1], perm[p] = s, pos[s] = p), built without atomics on global memory.
 #include "moe_conv.hpp"
