@@ -196,6 +196,7 @@ struct Layout {
   size_t shpart;                          // the shared expert's partial gate / up dots (K split)
   size_t part;                            // the one-token slice launch's partial outputs
   size_t tailpart;                        // the 256-token gate/up launch's tail partials
+  size_t rfast;                           // the proven-picks router's planes, row scales and bounds
   int tail_parts;                         // their parts (0: no tail split)
   int mode, mode_shared;                  // PathMode of the routed experts and of the shared expert
   int ks_sh_gu, ks_sh_dn;                 // K split of the shared expert's 64-token-tile launches
@@ -222,6 +223,9 @@ Layout layout(const ember_moe_layer* w, int T) {
   l.offsets = o; o = align_up(o + (size_t)(w->E + 1) * 4);
   l.perm = o; o = align_up(o + slots * 4);
   l.r = route_layout(T, w->E, w->k, o); o = l.r.end;
+  l.rfast = o;
+  o = align_up(o + (router_fast_fits(T, w->d, w->E, w->k, w->renorm ? 1 : 0, is_routed(w) ? 1 : 0)
+                        ? router_fast_work_bytes(T, w->d, w->E) : 0));
   l.h = o; o = align_up(o + slots * w->d_ff * 4);
   // y holds kMaxKSplit partial sums per row when an MFMA path splits the down projection's K
   l.y = o; o = align_up(o + slots * w->d * 4 * kMaxKSplit);
@@ -485,11 +489,21 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
   const bool need_conv = conv.y16 || conv.yb;
   auto* flag = at<unsigned long long>(scratch, l.flag);
   mark(ev, 0, st);
-  if (!fuse_route && (s = launch_router_logits(x, T, d, E, w->router, logits, st))) return s;
-  mark(ev, 1, st);
-  if (!fuse_route && (s = launch_route_dispatch(logits, T, E, k, renorm, routed, sigmoid, w->selection_bias, groups_n,
-                                                groups_top, idx, gates, ds, need_conv ? &conv : nullptr, st)))
-    return s;
+  if (!fuse_route && router_fast_fits(T, d, E, k, renorm, routed)) {
+    // picks proven from exact-integer fast logits; exact FP64 logits only where the bound leaves a doubt
+    if ((s = launch_router_fast(x, T, d, E, k, w->router, logits, idx, gates, at<void>(scratch, l.rfast),
+                                need_conv ? &conv : nullptr, st)))
+      return s;
+    mark(ev, 1, st);
+    if ((s = launch_dispatch(idx, T, k, E, ds, st))) return s;
+  } else {
+    if (!fuse_route && (s = launch_router_logits(x, T, d, E, w->router, logits, st))) return s;
+    mark(ev, 1, st);
+    if (!fuse_route && (s = launch_route_dispatch(logits, T, E, k, renorm, routed, sigmoid, w->selection_bias,
+                                                  groups_n, groups_top, idx, gates, ds, need_conv ? &conv : nullptr,
+                                                  st)))
+      return s;
+  }
   if (fuse_route && need_conv && (s = launch_act_conv(conv, st))) return s;
   mark(ev, 2, st);
   mark(ev, 3, st);

@@ -61,6 +61,13 @@ int launch_router_logits(const float* x, int T, int d, int E, const float* R, fl
 // for T E <= 1024, d % 4 == 0, d <= 8192.
 bool router_blocks_fit(int T, int d, int E);
 int launch_router_logits_blocks(const float* x, int T, int d, int E, const float* R, float* logits, hipStream_t st);
+// Proven-picks router for renormalised softmax routers (moe_router_fast.hip): router logits exact for
+// every expert the int8 fast logits' bound cannot rule out (the picks among them), a proven lower bound
+// elsewhere, then the routing (idx, gates) as launch_route gives it. work: router_fast_work_bytes.
+bool router_fast_fits(int T, int d, int E, int k, int renorm, int routed);
+size_t router_fast_work_bytes(int T, int d, int E);
+int launch_router_fast(const float* x, int T, int d, int E, int k, const float* R, float* logits, int32_t* idx,
+                       float* gates, void* work, const ActConv* conv, hipStream_t st);
 // conv (nullable): activation conversion run by extra blocks of the same launch
 int launch_route(const float* logits, int T, int E, int k, int renorm, int routed, int sigmoid, const float* bias,
                  int groups_n, int groups_top, int32_t* idx, float* gates, const ActConv* conv, hipStream_t st);

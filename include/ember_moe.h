@@ -66,7 +66,9 @@ size_t ember_moe_scratch_bytes(const ember_moe_layer* w, int T);
 /* Where ember_moe_ffn leaves its routing in the scratch buffer (byte offsets from its start), for
  * callers and tests that inspect a call's routing after it completes (no reference counterpart; it
  * plays the role of reading back moe_route_sel_kernel's outputs, cuda_kernels.cu:3565-3604):
- *   logits    f32 [T][E]   router logits
+ *   logits    f32 [T][E]   router logits (with the proven-picks router, EMBER_ROUTER_FAST=1: exact for every
+ *                          expert its bound could not rule out, the picks among them, and elsewhere a lower
+ *                          bound of the logit that lies strictly below every pick's)
  *   idx       i32 [T][k]   picks, ascending expert ids (-1: none); gates f32 [T][k] their weights
  *   offsets   i32 [E+1]    expert segment starts in the dispatch order; perm i32 [T*k] the slot t*k+j
  *                          at each dispatch position; pos i32 [T*k] slot -> position (-1: no pick)

@@ -45,3 +45,25 @@ def same_bits(a, b) -> bool:
     b = np.asarray(b, np.float32)
     both_nan = np.isnan(a) & np.isnan(b)
     return bool(np.all(both_nan | (a.view(np.uint32) == b.view(np.uint32))))
+
+
+def router_logits_match(got, want, idx) -> bool:
+    """The logits a layer call read back against the reference's (oracle) logits. Bit-equal, except where
+    the proven-picks router (renormalised softmax routers, batches of EMBER_ROUTER_FAST_T tokens and more)
+    ruled an expert out from its bounds: there it stores a lower bound of that expert's logit that lies
+    strictly below every pick's logit. A row with a NaN logit (a non-finite input) is exact throughout."""
+    got = np.asarray(got, np.float32)
+    want = np.asarray(want, np.float32)
+    idx = np.asarray(idx)
+    eq = (np.isnan(got) & np.isnan(want)) | (got.view(np.uint32) == want.view(np.uint32))
+    for t in np.nonzero(~eq.all(axis=1))[0]:
+        if np.isnan(want[t]).any():
+            return False
+        picks = idx[t][idx[t] >= 0]
+        floor = want[t, picks].min()
+        d = ~eq[t]
+        if np.isin(np.nonzero(d)[0], picks).any():
+            return False
+        if not (np.all(got[t, d] < floor) and np.all(got[t, d] <= want[t, d])):
+            return False
+    return True

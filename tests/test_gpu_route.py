@@ -35,7 +35,7 @@ def test_router_logits_bit_exact(gpu, T, d, E):
     assert same_bits(lg.cpu().numpy(), O.router_logits(x, R))
 
 
-def _route_gpu(logits, k, renorm=True, scoring=em.SCORE_SOFTMAX, bias=None, groups_n=1, groups_top=1):
+def _route_gpu(logits, k, renorm=True, scoring=em.SCORE_SOFTMAX, bias=None, groups_n=1, groups_top=1, scratch=None):
     import torch
 
     T, E = logits.shape
@@ -43,7 +43,8 @@ def _route_gpu(logits, k, renorm=True, scoring=em.SCORE_SOFTMAX, bias=None, grou
     gates = torch.empty((T, k), dtype=torch.float32, device="cuda")
     offsets = torch.empty(E + 1, dtype=torch.int32, device="cuda")
     perm = torch.full((T * k,), -1, dtype=torch.int32, device="cuda")
-    scratch = torch.empty(em.route_scratch_bytes(T, E, k), dtype=torch.uint8, device="cuda")
+    if scratch is None:
+        scratch = torch.empty(em.route_scratch_bytes(T, E, k), dtype=torch.uint8, device="cuda")
     s = em.route(_dev(logits), T, E, k, renorm, scoring, None if bias is None else _dev(bias), groups_n, groups_top,
                  idx, gates, offsets, perm, scratch)
     assert s == 0, em.strerror(s)
@@ -73,7 +74,8 @@ def _edge_logits(rng, T, E):
 
 @pytest.mark.parametrize("T,E,k", [(1, 8, 2), (8, 8, 2), (13, 64, 6), (128, 128, 8), (7, 200, 5), (9, 16, 16),
                                    (4096, 128, 8), (2048, 8, 2), (6, 4, 7), (3, 256, 8), (40, 256, 8), (5, 300, 10),
-                                   (2, 512, 4), (33, 512, 12), (1000, 256, 8), (1025, 64, 8), (700, 16, 17)])
+                                   (2, 512, 4), (33, 512, 12), (1000, 256, 8), (1025, 64, 8), (700, 16, 17),
+                                   (64, 8, 2), (64, 128, 8), (57, 32, 4), (16, 8, 2), (65, 128, 8)])
 @pytest.mark.parametrize("renorm", [True, False])
 def test_route_softmax_bit_exact(gpu, T, E, k, renorm):
     rng = np.random.default_rng(T * 131 + E * 7 + k)
@@ -106,6 +108,26 @@ def test_route_deepseek_bit_exact(gpu, sigmoid, use_bias, groups):
                                groups_top=groups[1])
         assert np.array_equal(idx, widx)
         assert same_bits(gates, wgates)
+        woff, wperm = O.dispatch(widx, E)
+        assert np.array_equal(offsets, woff)
+        assert np.array_equal(perm[:woff[-1]], wperm[:woff[-1]])
+
+
+def test_route_reuses_scratch(gpu):
+    """One scratch buffer, first filled with 0xff bytes, serves routing calls of several sizes in a row
+    (one-block fused routing + dispatch at 8 tokens or fewer, separate route and dispatch launches above):
+    each call's picks, gates and dispatch match the oracle, whatever an earlier call left in the scratch."""
+    import torch
+
+    rng = np.random.default_rng(5)
+    E, k = 64, 6
+    scratch = torch.full((em.route_scratch_bytes(64, E, k),), 0xFF, dtype=torch.uint8, device="cuda")
+    for T in (64, 17, 64, 9, 40, 8, 33):
+        lg = _edge_logits(rng, T, E)
+        print(f"route reuse T={T}", flush=True)
+        idx, gates, offsets, perm = _route_gpu(lg, k, True, scratch=scratch)
+        widx, wgates = O.route(lg, k, renorm=True)
+        assert np.array_equal(idx, widx) and same_bits(gates, wgates)
         woff, wperm = O.dispatch(widx, E)
         assert np.array_equal(offsets, woff)
         assert np.array_equal(perm[:woff[-1]], wperm[:woff[-1]])
