@@ -1460,11 +1460,13 @@ int gemm_ksplit(int type, bool packed, int T, int k, int E, int N, int K) {
   if (!dma_path(type, packed)) return 1;  // the split lives in the DMA kernels
   // tuning override, clamped so that every part holds at least one K tile
   if (const char* v = std::getenv("EMBER_KSPLIT")) return std::max(1, std::min(std::min(kMaxKSplit, K / GBK), atoi(v)));
-  // expected 256-token tiles (segments average T k / E tokens) times n-tiles: aim for >= 4 rounds
+  // expected 256-token tiles (segments average T k / E tokens) times n-tiles: aim for >= 4 rounds, with
+  // at least 64 K tiles per part (Mixtral-shaped down projection, K = 14336: split 2 / 4 measured, one box,
+  // C2 T = 8 278 / 282 us, T = 128 and 2048 even; Q4_K T = 8 / 128 / 512 265 / 271, 338 / 342, 604 / 618)
   const int est_tiles = (T * k + GBM - 1) / GBM + E / 2;
   const int blocks = est_tiles * ((N + 255) / 256);
   int ks = 1;
-  while (ks < kMaxKSplit && blocks * ks < 4 * 256 && K / GBK >= 32 * ks * 2) ks *= 2;
+  while (ks < kMaxKSplit && blocks * ks < 4 * 256 && K / GBK >= 64 * ks * 2) ks *= 2;
   return ks;
 }
 
