@@ -650,12 +650,18 @@ int launch_router_logits(const float* x, int T, int d, int E, const float* R, fl
   const int EG = max(1, min(router_lds_rows(d), (int)(((int64_t)T * E + 255) / 256)));
   const int64_t lds_blocks = (int64_t)T * ((E + EG - 1) / EG);
   if (d % 4 == 0 && ((E >= 16 && T >= 4) || (E >= 8 && T >= 64))) {
-    // one lane per chain; 4 x 8 pairs per block, or (E >= 32) 16 x 32 once that still gives 256 blocks
-    // (with 8 to 15 experts the staged-row kernels below stay ahead up to a few dozen tokens)
-    if (E < 32 || (int64_t)((T + 15) / 16) * ((E + 31) / 32) < 256) {
-      router_logits_chains<4, 8, 1, 1, 512><<<dim3((T + 3) / 4, (E + 7) / 8), 256, 0, st>>>(x, R, logits, T, d, E);
-    } else {
+    // one lane per chain; the largest tile that still gives >= 256 blocks: 16 x 32 pairs (E >= 32), 8 x 16
+    // (E >= 16), else 4 x 8 (with 8 to 15 experts the staged-row kernels below stay ahead up to a few
+    // dozen tokens). Measured router times, 4 x 8 / 8 x 16 / 16 x 32: C3-shaped (E = 128, d = 2048) T = 128
+    // 14.4 / 17.6 / 34.0 us, T = 256 21.1 / 18.9, T = 512 34.8 / 25.7 / 34.4, T = 1024 - / 40.6 / 36.5;
+    // C4-shaped (E = 64) T = 256 13.5 / 16.9, T = 512 20.4 / 18.0, T = 1024 32.4 / 24.7
+    const int64_t b16 = (int64_t)((T + 15) / 16) * ((E + 31) / 32), b8 = (int64_t)((T + 7) / 8) * ((E + 15) / 16);
+    if (E >= 32 && b16 >= 256) {
       router_logits_chains<4, 8, 4, 4, 128><<<dim3((T + 15) / 16, (E + 31) / 32), 256, 0, st>>>(x, R, logits, T, d, E);
+    } else if (E >= 16 && b8 >= 256) {
+      router_logits_chains<4, 8, 2, 2, 256><<<dim3((T + 7) / 8, (E + 15) / 16), 256, 0, st>>>(x, R, logits, T, d, E);
+    } else {
+      router_logits_chains<4, 8, 1, 1, 512><<<dim3((T + 3) / 4, (E + 7) / 8), 256, 0, st>>>(x, R, logits, T, d, E);
     }
   } else if (router_blocks_fit(T, d, E)) {
     // a few pairs: one block each, its products formed in parallel (the one-token launch's router blocks)

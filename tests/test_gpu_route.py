@@ -20,6 +20,7 @@ def _dev(a):
 
 
 @pytest.mark.parametrize("T,d,E", [(1, 4096, 8), (8, 4096, 8), (3, 100, 8), (64, 2048, 128), (257, 2048, 64), (2048, 4096, 8),
+                                   (512, 2048, 128), (300, 256, 100), (520, 2048, 64), (2050, 512, 16),
                                    (40, 256, 8), (31, 20, 5), (1500, 520, 200), (300, 2052, 24), (9, 100, 16), (100, 36, 12),
                                    (4, 64, 16)])
 def test_router_logits_bit_exact(gpu, T, d, E):
