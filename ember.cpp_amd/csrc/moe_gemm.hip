@@ -1460,14 +1460,27 @@ int gemm_ksplit(int type, bool packed, int T, int k, int E, int N, int K) {
   if (!dma_path(type, packed)) return 1;  // the split lives in the DMA kernels
   // tuning override, clamped so that every part holds at least one K tile
   if (const char* v = std::getenv("EMBER_KSPLIT")) return std::max(1, std::min(std::min(kMaxKSplit, K / GBK), atoi(v)));
-  // expected 256-token tiles (segments average T k / E tokens) times n-tiles: aim for >= 4 rounds, with
-  // at least 64 K tiles per part (Mixtral-shaped down projection, K = 14336: split 2 / 4 measured, one box,
-  // C2 T = 8 278 / 282 us, T = 128 and 2048 even; Q4_K T = 8 / 128 / 512 265 / 271, 338 / 342, 604 / 618)
-  const int est_tiles = (T * k + GBM - 1) / GBM + E / 2;
-  const int blocks = est_tiles * ((N + 255) / 256);
-  int ks = 1;
-  while (ks < kMaxKSplit && blocks * ks < 4 * 256 && K / GBK >= 64 * ks * 2) ks *= 2;
-  return ks;
+  // The launch runs tiles * ks blocks in rounds of `slots`; a part of a round costs a whole round, so ks
+  // minimises ceil(tiles * ks / slots) / ks (ties to fewer parts: each part is another y row the combine
+  // reads), among the splits that keep >= 32 K tiles per part and are reached while the blocks are fewer
+  // than four rounds. tiles: the expected 256-token tiles of uniform routing (an expert's rows n ~
+  // Binomial(T k, 1 / E) make E[ceil(n / 256)] tiles; normal approximation) times the n-tiles.
+  // Mixtral-shaped down projection (K = 14336), ks 1 / 2 / 4, one box: T = 768 814 / 748 / 769 us,
+  // T = 1024 1020 / 1047 / 1017 (about half the experts take a second, short tile), T = 8 - / 278 / 282.
+  const double m = (double)T * k / E, sd = std::sqrt(m * (1.0 - 1.0 / E));
+  double per_e = 1.0 - std::pow(1.0 - 1.0 / E, (double)T * k);  // P(n > 0)
+  for (int j = 1; j <= 64 && GBM * j < m + 8 * sd + GBM; ++j)
+    per_e += sd > 0 ? 0.5 * std::erfc((GBM * j + 0.5 - m) / (sd * std::sqrt(2.0))) : (m > GBM * j ? 1.0 : 0.0);
+  const double tiles = E * per_e * ((N + 255) / 256);
+  const double slots = std::max(1, gemm_slots());
+  auto rounds = [&](int ks) { return std::ceil(tiles * ks / slots - 1e-6); };  // (a whole count stays whole)
+  int best = 1;
+  double best_cost = rounds(1);
+  for (int ks = 2; ks <= kMaxKSplit && K / GBK >= 32 * ks && tiles * ks / 2 < 4 * slots; ks *= 2) {
+    const double cost = rounds(ks) / ks;
+    if (cost < best_cost - 1e-9) best = ks, best_cost = cost;
+  }
+  return best;
 }
 
 int gemm_skinny_ksplit(int type, bool packed, int max_mtiles, int N, int K) {
