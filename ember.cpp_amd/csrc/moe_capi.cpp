@@ -660,7 +660,7 @@ int run_ffn(const ember_moe_layer* w, const float* x, int T, float* out, void* s
     g.w_exp0 = pack_bf16 ? wexp(bx.down) : nullptr;
     g.w_exp1 = nullptr;
     g.w_hexp = nullptr;
-    g.ksplit = ksplit = skinny ? gemm_skinny_ksplit(g.type, pack != nullptr, mt, d, d_ff)
+    g.ksplit = ksplit = skinny ? gemm_skinny_ksplit(g.type, pack != nullptr, T, k, E, d, d_ff)
                                : gemm_ksplit(g.type, pack != nullptr, T, k, E, d, d_ff);
     g.part_stride = (int64_t)T * k * d;
     if ((s = gemm(g, false, mt))) return s;

@@ -490,7 +490,6 @@ constexpr int kDmaA = GBM * GBK * 2;             // activation bytes per stage (
 constexpr int kDmaB = 256 * kDmaRowB;            // weight bytes per stage (20 KiB)
 constexpr int kDmaStage = kDmaA + kDmaB;
 constexpr size_t kDmaLds = (size_t)kDmaStages * kDmaStage;
-constexpr int kDmaInstA = kDmaA / 1024 / 8;      // 16-byte DMA instructions per wave per tile: activations (4)
 // launches of at most 64 tokens (every segment, hence every tile, holds at most 64 rows: a token picks an
 // expert once): 64 activation rows per stage (8 KiB) and five stages, four tiles in flight
 constexpr int kDmaStagesShort = 5, kShortRows = 64;
@@ -1456,6 +1455,17 @@ int gemm_dense_ksplit(bool gated, int T, int N, int K, int64_t weight_bytes) {
 
 int gemm_skinny_max_tiles(int T, int k, int E) { return (T * k + SBM - 1) / SBM + std::min(E, T * k); }
 
+// Expected row tiles (of `bm` rows) of T tokens' k picks over E experts under uniform routing: an expert's
+// rows n ~ Binomial(T k, 1 / E) make E[ceil(n / bm)] = sum over j >= 0 of P(n > bm j) tiles (normal
+// approximation for j >= 1).
+static double expected_row_tiles(int T, int k, int E, int bm) {
+  const double m = (double)T * k / E, sd = std::sqrt(m * (1.0 - 1.0 / E));
+  double per_e = 1.0 - std::pow(1.0 - 1.0 / E, (double)T * k);  // P(n > 0)
+  for (int j = 1; j <= 4096 && bm * j < m + 8 * sd + bm; ++j)
+    per_e += sd > 0 ? 0.5 * std::erfc((bm * j + 0.5 - m) / (sd * std::sqrt(2.0))) : (m > bm * j ? 1.0 : 0.0);
+  return E * per_e;
+}
+
 int gemm_ksplit(int type, bool packed, int T, int k, int E, int N, int K) {
   if (!dma_path(type, packed)) return 1;  // the split lives in the DMA kernels
   // tuning override, clamped so that every part holds at least one K tile
@@ -1467,11 +1477,7 @@ int gemm_ksplit(int type, bool packed, int T, int k, int E, int N, int K) {
   // Binomial(T k, 1 / E) make E[ceil(n / 256)] tiles; normal approximation) times the n-tiles.
   // Mixtral-shaped down projection (K = 14336), ks 1 / 2 / 4, one box: T = 768 814 / 748 / 769 us,
   // T = 1024 1020 / 1047 / 1017 (about half the experts take a second, short tile), T = 8 - / 278 / 282.
-  const double m = (double)T * k / E, sd = std::sqrt(m * (1.0 - 1.0 / E));
-  double per_e = 1.0 - std::pow(1.0 - 1.0 / E, (double)T * k);  // P(n > 0)
-  for (int j = 1; j <= 64 && GBM * j < m + 8 * sd + GBM; ++j)
-    per_e += sd > 0 ? 0.5 * std::erfc((GBM * j + 0.5 - m) / (sd * std::sqrt(2.0))) : (m > GBM * j ? 1.0 : 0.0);
-  const double tiles = E * per_e * ((N + 255) / 256);
+  const double tiles = expected_row_tiles(T, k, E, GBM) * ((N + 255) / 256);
   const double slots = std::max(1, gemm_slots());
   auto rounds = [&](int ks) { return std::ceil(tiles * ks / slots - 1e-6); };  // (a whole count stays whole)
   int best = 1;
@@ -1483,16 +1489,18 @@ int gemm_ksplit(int type, bool packed, int T, int k, int E, int N, int K) {
   return best;
 }
 
-int gemm_skinny_ksplit(int type, bool packed, int max_mtiles, int N, int K) {
+int gemm_skinny_ksplit(int type, bool packed, int T, int k, int E, int N, int K) {
   (void)type;
   (void)packed;
   // tuning override, clamped so that every part holds at least one K tile
   if (const char* v = std::getenv("EMBER_KSPLIT")) return std::max(1, std::min(std::min(kMaxKSplit, K / GBK), atoi(v)));
-  // up to 1024 blocks, with at least 5 K tiles per part (C4-shaped down projection, K = 1408: 22 K
-  // tiles; split 1 / 2 / 4: T = 16 141 / 124 / 121 us, T = 64 152 / 134 / 131, T = 256 191 / 179 / 188)
-  const int blocks = max_mtiles * ((N + 255) / 256);
+  // up to 1024 blocks of the expected 64-token tiles (uniform routing; the worst-case tile count the grid
+  // is sized for stopped the split early at small T), with at least 5 K tiles per part. C4-shaped down
+  // projection (K = 1408: 22 K tiles), split 1 / 2 / 4: T = 16 151 / 132 / 127 us, T = 64 165 / 146 /
+  // 142, T = 128 166 / 150 / 149, T = 256 189 / 186 / 199 (it was the worst-case count: 2 at all four).
+  const double blocks = expected_row_tiles(T, k, E, 64) * ((N + 255) / 256);
   int ks = 1;
-  while (ks < kMaxKSplit && blocks * ks < 1024 && K / GBK >= 5 * ks * 2) ks *= 2;
+  while (ks < kMaxKSplit && blocks * ks <= 1023 && K / GBK >= 5 * ks * 2) ks *= 2;  // (a whole 1024 stays)
   return ks;
 }
 

@@ -332,7 +332,7 @@ int gemm_skinny_max_tiles(int T, int k, int E);
 // K split of the skinny path's plain (down) projection: 1..kMaxKSplit, so that the launch has enough
 // blocks for the chip when the output is narrow
 constexpr int kMaxKSplit = 4;
-int gemm_skinny_ksplit(int type, bool packed, int max_mtiles, int N, int K);
+int gemm_skinny_ksplit(int type, bool packed, int T, int k, int E, int N, int K);
 // ... and of a dense projection (the shared expert's T rows) on the 64-token tiles, gated or plain: up to
 // kMaxDenseKSplit parts, until the launch has 512 blocks, each part keeps >= 2 K tiles and the partial
 // sums (f32) stay within the weights' bytes
