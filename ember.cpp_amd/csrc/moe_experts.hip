@@ -924,7 +924,12 @@ int launch_proj_cfg(const ProjArgs& a_in, size_t act_lds, hipStream_t st) {
   const int cus = device_cus();
   if (cached_bpc <= 0 || cus <= 0) return EMBER_ERR_LAUNCH;
   static const int bpc_override = [] { const char* e = std::getenv("EMBER_PROJ_BPC"); return e ? atoi(e) : 0; }();
-  const int bpc = bpc_override > 0 ? std::min(bpc_override, cached_bpc) : cached_bpc;
+  int bpc = bpc_override > 0 ? std::min(bpc_override, cached_bpc) : cached_bpc;
+  // a launch of a few MB of routed weights and no shared expert runs best with one block per CU (measured
+  // one-token layers, default / one: C1 gate/up 1.4 MB 20.2 -> 18.5 us, C3 down 7 MB 30.9 -> 29.1 us per
+  // layer; C3 gate/up 14 MB even, C4 46-93 MB and the Mixtral-shaped GEMV slower)
+  const double wbytes = (double)(a.used ? a.max_segments : 0) * (double)a.expert_stride * (GATED ? 2 : 1);
+  if (bpc_override <= 0 && !a.s_w0 && wbytes > 0 && wbytes < 10e6) bpc = 1;
   const int segs = (a.used ? std::max(a.max_segments, 1) : 0) + (a.s_w0 ? 1 : 0);
   const int G = std::max(std::max(cus * bpc, segs), ROUTE ? a.route.E : 0);
   if (ROUTE && a.route.E > cus) return EMBER_ERR_SHAPE;  // the router blocks could not all be resident
