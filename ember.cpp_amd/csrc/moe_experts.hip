@@ -1500,7 +1500,11 @@ int launch_down1_cfg(const Down1Args& a_in, hipStream_t st) {
 
 template <int FMT>
 int launch_down1_fmt(const Down1Args& a, hipStream_t st) {
-  static const int nt = [] { const char* v = std::getenv("EMBER_DOWN1_NT"); return v ? atoi(v) : 1024; }();
+  // 1024-thread blocks, or 512 for a few MB of down weights (measured, 1024 / 512: C1-shaped 1.4 MB 17.9 /
+  // 16.8 us per layer; Mixtral-shaped Q8_0 125 MB 86.8 / 89.7, Q4_K 68.1 / 71.7); EMBER_DOWN1_NT overrides
+  static const int nt_env = [] { const char* v = std::getenv("EMBER_DOWN1_NT"); return v ? atoi(v) : 0; }();
+  const double bytes = (double)a.k * (double)a.expert_stride;
+  const int nt = nt_env ? nt_env : (bytes < 10e6 ? 512 : 1024);
   return nt == 1024 ? launch_down1_cfg<FMT, 1024>(a, st) : launch_down1_cfg<FMT, 512>(a, st);
 }
 
