@@ -14,7 +14,8 @@ CASES = {
     # name: (spec kwargs, T, environment, the EMBER_PATH bits the call must take)
     "slices_q8": (dict(d=1024, d_ff=512, E=8, k=2, wtype=em.Q8_0), 1, {"EMBER_MOE_SLICES": "1"}, em.PATH_SLICES),
     "gemv_q4": (dict(d=1024, d_ff=512, E=8, k=2, wtype=em.Q4_K), 1, {"EMBER_MOE_SLICES": "0"}, em.PATH_GEMV),
-    "tiles_tail_q8": (dict(d=512, d_ff=1024, E=8, k=2, wtype=em.Q8_0), 8, {"EMBER_MOE_PATH": "gemm"}, em.PATH_TILES256),
+    "tiles_tail_q8": (dict(d=512, d_ff=1024, E=8, k=2, wtype=em.Q8_0), 8, {"EMBER_MOE_PATH": "gemm",
+                                                                           "EMBER_TAIL_PARTS": "8"}, em.PATH_TILES256),
     "tiles_q4_shared": (dict(d=512, d_ff=768, E=8, k=2, wtype=em.Q4_K, d_ff_shared=512), 24,
                         {"EMBER_MOE_PATH": "gemm"}, em.PATH_TILES256),
 }

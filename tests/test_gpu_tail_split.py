@@ -45,6 +45,7 @@ def test_tail_split(gpu, monkeypatch, name):
     dl.tensors["pack"] = buf
     x = em.make_input(spec, T, seed=52)
     monkeypatch.setenv("EMBER_MOE_PATH", "gemm")  # the 256-token tiles
+    monkeypatch.setenv("EMBER_TAIL_PARTS", "8")   # the split, also for these short K (by default K >= 64 tiles)
     assert em.path(dl.desc, T) & em.PATH_TILES256
     print(f"tail split {name} T={T}", flush=True)
     y = _run(dl, x)
