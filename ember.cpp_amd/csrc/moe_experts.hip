@@ -109,8 +109,10 @@ __device__ inline int uniform(int v) { return __builtin_amdgcn_readfirstlane(v);
 
 // ONE_TOKEN: every routed segment holds one token (a one-token launch, at most 64 picks), so each has the
 // same work w and the prefix sums are s w (integer-valued floats: the same values the scans give)
+// gr_fixed >= 0: the routed blocks are 0 .. gr_fixed - 1 whatever the number of segments (the one-token
+// launches fix the split before the routing is known, so that the shared segment's blocks need not wait)
 template <bool GATED, int MT, bool ONE_TOKEN = false>
-__device__ inline bool seg_view(const ProjArgs& a, const Dispatch& dp, int b, int G, SegView& v) {
+__device__ inline bool seg_view(const ProjArgs& a, const Dispatch& dp, int b, int G, SegView& v, int gr_fixed = -1) {
   const int nseg = a.used ? dp.n_used : 0;
   const int lane = threadIdx.x & 63;
   // routed work: total, then this block's segment from the prefix sums
@@ -132,8 +134,12 @@ __device__ inline bool seg_view(const ProjArgs& a, const Dispatch& dp, int b, in
   const float w_shared = a.s_w0 ? seg_work(a.s_rows, a.T, MT) : 0.0f;
   if (w_routed + w_shared == 0.0f) return false;
   int Gr = 0;
-  if (nseg > 0) Gr = w_shared ? uniform(max(nseg, min(G - 1, (int)(G * (w_routed / (w_routed + w_shared)))))) : G;
+  if (gr_fixed >= 0)
+    Gr = gr_fixed;
+  else if (nseg > 0)
+    Gr = w_shared ? uniform(max(nseg, min(G - 1, (int)(G * (w_routed / (w_routed + w_shared)))))) : G;
   if (b < Gr) {
+    if (nseg == 0) return false;  // (a fixed split whose token has no valid pick)
     // block start of segment s: s + floor((Gr - nseg) * W(<s) / W); the block's segment is the one
     // whose [start, next start) holds b
     const float spare = (float)(Gr - nseg);
@@ -835,7 +841,8 @@ __device__ __attribute__((always_inline)) void route_block(const ProjArgs& a, ui
 // routing, which block 0 always runs).
 template <int FMT, int NT, int ROUTE>
 __device__ inline bool fused_route_prologue(const ProjArgs& a, uint8_t* xs, uint8_t* prod, uint8_t* ra, int32_t* s_off,
-                                            int32_t* s_used, int32_t* s_n, int32_t* s_perm, int* zero_row) {
+                                            int32_t* s_used, int32_t* s_n, int32_t* s_perm, int* zero_row,
+                                            bool routing = true) {
   const int b = blockIdx.x;
   EMBER_STAMP(0, 0);
   if (threadIdx.x == 0) *zero_row = 0;
@@ -855,6 +862,10 @@ __device__ inline bool fused_route_prologue(const ProjArgs& a, uint8_t* xs, uint
       stage_rows_quant<F::PLANES>(a.route.x, a.route.d, zero_row, 1, xs, act_lds_bytes(true, a.route.d));
     else
       stage_rows_f32<F::NGL>(a.route.x, a.route.d, zero_row, 1, xs, act_lds_bytes(false, a.route.d));
+  }
+  if (!routing) {  // a shared-segment block: its rows do not depend on the picks
+    __syncthreads();
+    return false;
   }
   // softmax router: the pick set from the fast words when they prove it (block 0 then writes the
   // exact routing record after its rows); otherwise, and for the DeepSeek-style router, from the
@@ -894,12 +905,23 @@ __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) 
     uint8_t* xs = act_lds;
     uint8_t* prod = act_lds + fused_x_lds(FMT, a.route.d);
     uint8_t* ra = prod + fused_router_lds(a.route.d);
-    fused_route_prologue<FMT, NT, ROUTE>(a, xs, prod, ra, s_off, s_used, &s_n, s_perm, &zero_row);
-    Dispatch dp{s_n, s_used, s_off, s_perm};
-    SegView v;
     // softmax router: block 0 (the exact routing and its record) takes no rows; blocks 1 .. G-1 share them
     constexpr int B0 = ROUTE == 1 ? 1 : 0;
-    const bool act = b >= B0 && seg_view<GATED, MT, true>(a, dp, b - B0, gridDim.x - B0, v);
+    const int G1 = gridDim.x - B0;
+    // with a shared expert the routed / shared split of the blocks is fixed from k (the segments of a token
+    // whose picks are all valid, the split seg_view would compute), so the shared segment's blocks skip the
+    // routing and stream their rows while it runs (a token with fewer valid picks spreads its routed blocks
+    // over fewer segments)
+    int gr = -1;
+    if (a.s_w0 && a.used) {
+      const float w1 = seg_work(a.rows, 1, MT), ws = seg_work(a.s_rows, a.T, MT), wr = (float)a.k * w1;
+      gr = uniform(max(a.k, min(G1 - 1, (int)(G1 * (wr / (wr + ws))))));
+    }
+    const bool shared_blk = gr >= 0 && b >= B0 && b - B0 >= gr;
+    fused_route_prologue<FMT, NT, ROUTE>(a, xs, prod, ra, s_off, s_used, &s_n, s_perm, &zero_row, !shared_blk);
+    Dispatch dp{shared_blk ? 0 : s_n, s_used, s_off, s_perm};
+    SegView v;
+    const bool act = b >= B0 && seg_view<GATED, MT, true>(a, dp, b - B0, G1, v, gr);
     EMBER_STAMP(0, 4);
     if (act) proj_body<FMT, MT, GATED, NB, NT, false, true>(a, dp, v);
     EMBER_STAMP(0, 7);
