@@ -300,11 +300,14 @@ Plan plan(const ember_moe_layer* w, const Layout& l, int T) {
   // unfused launches)
   p.fuse_route = fuse_ok && l.mode == kGemv && T == 1 && fused_route_fits(w->gate_type, d, E, k) && E <= device_cus();
   p.slices = slices_ok && p.fuse_route && slices_possible(w, T, l.mode, slices_any);
-  // (measured on MI355X: C1-shaped layer 22.6 -> 20.4 us, Mixtral-shaped even; with many picks or a
-  // shared expert its row partition leaves blocks idle: Qwen-shaped top-8 32 -> 40 us, DeepSeek-shaped
-  // top-6 + shared 50 -> 54 us, so those keep the down launch + combine)
-  p.down1 = !p.slices && down1_ok && l.mode == kGemv && T == 1 && k <= 2 && w->d_ff_shared == 0 &&
-            down1_fits(w->down_type, d, d_ff, k, 0);
+  // (the picks of a row run side by side in down1_walk_picks; measured on MI355X against the down launch
+  // + combine: C1-shaped layer 17.1 -> 16.7 us, Qwen-shaped top-8 29.0 -> 26.8, DeepSeek-shaped top-6 +
+  // shared 54.2 -> 52.0, Mixtral-shaped without a pack even). A shared expert joins when it rides in the
+  // routed GEMV launches (same types), as run_ffn then passes it to the down launch.
+  const bool shared_gemv = w->d_ff_shared == 0 || (l.mode_shared == kGemv && w->gate_shared_type == w->gate_type &&
+                                                    w->down_shared_type == w->down_type);
+  p.down1 = !p.slices && down1_ok && l.mode == kGemv && T == 1 && k <= kDown1MaxPicks && shared_gemv &&
+            down1_fits(w->down_type, d, d_ff, k, w->d_ff_shared);
   return p;
 }
 

@@ -1291,24 +1291,22 @@ __device__ inline float shared_gate_sigmoid(float s) { return 1.0f / (1.0f + exp
 // activation quantization) and the sum in combine_kernel's order, so the output bits equal those of
 // the down launch followed by the combine launch.
 //
-// Row ownership follows proj_body's interleave for the routed matrices (the grid's waves read adjacent
-// rows at any time): with RPS rows per wave step, wave w of block b owns rows (b*nw + w)*RPS + i*W*RPS
-// + sub, W = all waves of the grid; slot (i*nw + w)*RPS + sub of the block's row list holds that row.
-// The shared expert's rows (another row length, so another lane partition) are the same rows, walked
-// through the slot list.
+// Row ownership: with RPS rows per wave step (the routed row length's lane partition), block b of G owns
+// the row groups b, b + G, ... (adjacent blocks read adjacent rows at any time), slot i*RPS + sub of its
+// row list holding row sub of its i-th group. Its waves share the (group, pick) pairs, so the picks of a
+// row are read side by side, into one LDS row of dots per pick that is then summed in pick order. The
+// shared expert's rows (another row length, so another lane partition) are the same rows, walked through
+// the slot list.
 
-// Walks npicks matrices (wbase[j]: rows of K elements, rb bytes apart) over the block's slots; the dot
-// of slot s's row with activation row j (act + j * row_lds) goes to obuf[s]: obuf = obuf + coef[j] * dot,
-// or (shared) obuf = obuf + dot * (*sgc) / obuf + dot.
-// before_loop() runs (on every thread of the block) after the first weight loads are issued and before
-// the first dot: the activation staging goes there, so that the weights travel while it runs.
-template <int FMT, int NB, int NT, class Before>
-__device__ __attribute__((always_inline)) inline void down1_walk(const uint8_t* w0, const int* exps, int64_t estride,
-                                                                 int npicks, int64_t rb, int K, const uint8_t* act,
-                                                                 int row_lds, const int* rowlist, int nslots,
-                                                                 float* obuf, const float* coef, bool shared,
-                                                                 const float* sgc, int rows_total,
-                                                                 Before&& before_loop) {
+// Walks the shared expert's down matrix (rows of K elements, rb bytes apart) over the block's slots: the
+// dot of slot s's row (rowlist[s]; holes load row 0 and store nothing) with the shared expert's activation
+// row `act` is added to obuf[s] (obuf = obuf + dot * (*sgc), or + dot). Its row length sets its own lane
+// partition (L lanes per row, RPS rows per wave step), the slot groups of RPS taken by the waves in turn.
+template <int FMT, int NB, int NT>
+__device__ __attribute__((always_inline)) inline void down1_walk_shared(const uint8_t* w0, int64_t rb, int K,
+                                                                        const uint8_t* act, int row_lds,
+                                                                        const int* rowlist, int nslots, float* obuf,
+                                                                        const float* sgc) {
   using F = Fmt<FMT>;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = NT / 64;
   const int C = (K + F::CE - 1) / F::CE;
@@ -1317,31 +1315,79 @@ __device__ __attribute__((always_inline)) inline void down1_walk(const uint8_t* 
   const int L = 1 << Lg, RPS = 64 >> Lg;
   const int sub = lane >> Lg, rl = lane & (L - 1);
   const int NC = (C + L - 1) / L;
-  // slot groups of this wave: for the routed walk (rows_total > 0) the groups holding rows, a prefix
-  // (proj_body's count); for the shared walk every group of the slot list (its holes load row 0 and
-  // store nothing)
-  int ngroups;
-  if (rows_total > 0) {
-    const int gt = (rows_total + RPS - 1) / RPS, wg = blockIdx.x * nwaves + wave, Wall = gridDim.x * nwaves;
-    ngroups = wg < gt ? (gt - wg + Wall - 1) / Wall : 0;
-  } else {
-    const int ngt = (nslots + RPS - 1) / RPS;
-    ngroups = wave < ngt ? (ngt - wave + nwaves - 1) / nwaves : 0;
-  }
-  const int nsteps = ngroups * NC;
-  const int nloads = npicks > 0 ? nsteps * npicks : 0;  // load q: pick q / nsteps, step q % nsteps
+  const int ngt = (nslots + RPS - 1) / RPS;
+  const int ngroups = wave < ngt ? (ngt - wave + nwaves - 1) / nwaves : 0;
+  const int nloads = ngroups * NC;  // load q: slot group q / NC of this wave, chunk step q % NC
   auto slot_of = [&](int st) { return ((st / NC) * nwaves + wave) * RPS + sub; };
-  // the routed walk's rows follow arithmetically from the slot (no LDS lookup on the load path)
-  const int wg = blockIdx.x * nwaves + wave, Wall = gridDim.x * nwaves;
-  auto row_of = [&](int st) {
-    return rows_total > 0 ? min((wg + (st / NC) * Wall) * RPS + sub, rows_total - 1)
-                          : max(rowlist[min(slot_of(st), nslots - 1)], 0);
-  };
   auto load_q = [&](int q, uint32_t (&buf)[F::NW]) {
-    const int j = min(q / nsteps, npicks - 1), st = q - (q / nsteps) * nsteps;
-    const int e = __builtin_amdgcn_readfirstlane(exps[j]);  // LDS, a wave-uniform index
+    const int st = min(q, nloads - 1);
     const int c = min(rl + (st % NC) * L, C - 1);
-    F::load(w0 + (int64_t)e * estride + (int64_t)row_of(st) * rb, c, K, buf);
+    F::load(w0 + (int64_t)max(rowlist[min(slot_of(st), nslots - 1)], 0) * rb, c, K, buf);
+  };
+  if (nloads == 0) return;
+  uint32_t buf[NB][F::NW];
+  ring_for<NB - 1>([&](auto J) { load_q(decltype(J)::value, buf[decltype(J)::value]); });
+  float acc = 0.0f;
+#pragma unroll 1
+  for (int q0 = 0; q0 < nloads; q0 += NB) {
+    ring_for<NB>([&](auto J) {
+      constexpr int jj = decltype(J)::value;
+      const int q = q0 + jj;
+      load_q(q + NB - 1, buf[(jj + NB - 1) % NB]);
+      const int sl = slot_of(q);
+      const int c = rl + (q % NC) * L;
+      const bool ok = q < nloads && c < C && sl < nslots;
+      float tk[1] = {0.0f};
+      F::template dot_tokens<1>(buf[jj % NB], act, row_lds, min(c, C - 1), K, 1, tk);
+      acc += ok ? tk[0] : 0.0f;
+      if (q < nloads && q % NC == NC - 1) {  // the row is complete
+        float v = acc;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1)
+          if (off < L) v += __shfl_xor(v, off, 64);
+        if (rl == 0 && sl < nslots && rowlist[sl] >= 0) {
+          float& o = obuf[sl];
+          o = o + (sgc ? v * *sgc : v);  // the shared expert's row (qwen2moe: times its gate)
+        }
+        acc = 0.0f;
+      }
+    });
+  }
+}
+
+// The routed picks' dots of the block's row groups (block b owns groups b, b + G, b + 2G, ... of RPS rows):
+// the (group, pick) units are spread over the block's waves, pick fastest, so the picks of one row run
+// side by side instead of one after another; unit (i, j)'s dot of row sub of group i goes to
+// pbuf[j][i * RPS + sub]. Each dot is formed as proj_body forms it (same lane partition, chunk order and
+// shuffle reduction); the caller adds them in pick order. before_loop() runs on every thread of the block
+// after the first weight loads are issued and before the first dot: the activation staging goes there, so
+// that the weights travel while it runs.
+template <int FMT, int NB, int NT, class Before>
+__device__ __attribute__((always_inline)) inline void down1_walk_picks(const uint8_t* w0, const int* exps,
+                                                                       int64_t estride, int npicks, int64_t rb, int K,
+                                                                       const uint8_t* act, int row_lds, int rows_total,
+                                                                       int nslots, float (*pbuf)[kDown1Slots],
+                                                                       Before&& before_loop) {
+  using F = Fmt<FMT>;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = NT / 64;
+  const int C = (K + F::CE - 1) / F::CE;
+  int Lg = 0;
+  while ((1 << Lg) < C && Lg < 6) ++Lg;
+  const int L = 1 << Lg, RPS = 64 >> Lg;
+  const int sub = lane >> Lg, rl = lane & (L - 1);
+  const int NC = (C + L - 1) / L;
+  const int gt = (rows_total + RPS - 1) / RPS, G = gridDim.x, b = blockIdx.x;
+  const int ngb = b < gt ? (gt - b + G - 1) / G : 0;
+  const int nunits = npicks > 0 ? ngb * npicks : 0;
+  const int nu_w = wave < nunits ? (nunits - wave + nwaves - 1) / nwaves : 0;
+  const int nloads = nu_w * NC;  // load q: this wave's unit q / NC, chunk step q % NC
+  auto unit_of = [&](int q) { return min(wave + (q / NC) * nwaves, nunits - 1); };
+  auto load_q = [&](int q, uint32_t (&buf)[F::NW]) {
+    const int u = unit_of(q), i = u / npicks, j = u - i * npicks;
+    const int e = __builtin_amdgcn_readfirstlane(exps[j]);  // LDS, a wave-uniform index
+    const int row = min((b + i * G) * RPS + sub, rows_total - 1);
+    const int c = min(rl + (q % NC) * L, C - 1);
+    F::load(w0 + (int64_t)e * estride + (int64_t)row * rb, c, K, buf);
   };
   uint32_t buf[NB][F::NW];
   if (nloads > 0) ring_for<NB - 1>([&](auto J) { load_q(decltype(J)::value, buf[decltype(J)::value]); });
@@ -1354,26 +1400,19 @@ __device__ __attribute__((always_inline)) inline void down1_walk(const uint8_t* 
       constexpr int jj = decltype(J)::value;
       const int q = q0 + jj;
       load_q(q + NB - 1, buf[(jj + NB - 1) % NB]);
-      const int j = min(q / nsteps, npicks - 1), st = q - (q / nsteps) * nsteps;
-      const int sl = slot_of(st);
-      const int c = rl + (st % NC) * L;
-      const bool ok = q < nloads && c < C && sl < nslots;
+      const int u = unit_of(q), i = u / npicks, j = u - i * npicks;
+      const int c = rl + (q % NC) * L;
+      const bool ok = q < nloads && c < C;
       float tk[1] = {0.0f};
       F::template dot_tokens<1>(buf[jj % NB], act + (size_t)j * row_lds, row_lds, min(c, C - 1), K, 1, tk);
       acc += ok ? tk[0] : 0.0f;
-      if (q == 0 && !shared) EMBER_STAMP(1, 6);
-      if (q < nloads && st % NC == NC - 1) {  // the row is complete for pick j
+      if (q < nloads && q % NC == NC - 1) {  // the row is complete for pick j
         float v = acc;
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1)
           if (off < L) v += __shfl_xor(v, off, 64);
-        if (rl == 0 && sl < nslots && rowlist[sl] >= 0) {
-          float& o = obuf[sl];
-          if (shared)
-            o = o + (sgc ? v * *sgc : v);  // the shared expert's row (qwen2moe: times its gate)
-          else
-            o = o + coef[j] * v;  // combine_kernel: acc = acc + gate * y
-        }
+        const int sl = i * RPS + sub;
+        if (rl == 0 && sl < nslots) pbuf[j][sl] = v;
         acc = 0.0f;
       }
     });
@@ -1383,9 +1422,9 @@ __device__ __attribute__((always_inline)) inline void down1_walk(const uint8_t* 
 template <int FMT, int NB, int NT, int WPE>
 __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) down1_kernel(Down1Args a) {
   using F = Fmt<FMT>;
-  constexpr int NW = NT / 64;
   extern __shared__ __align__(16) uint8_t act_lds[];
   __shared__ float obuf[kDown1Slots];
+  __shared__ float pbuf[kDown1MaxPicks][kDown1Slots];  // the routed picks' dots per slot
   __shared__ int rowlist[kDown1Slots];
   __shared__ float gate_s[kDown1MaxPicks], sgc_s;
   __shared__ int pos_s[kDown1MaxPicks], exp_s[kDown1MaxPicks], np_s, zero_row;
@@ -1426,17 +1465,16 @@ __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) 
       zero_row = 0;
     }
   }
-  // the block's rows: proj_body's interleave for the routed row length (see above)
+  // the block's rows: its row groups b, b + G, ... of RPS rows (the routed row length's lane partition),
+  // slot i * RPS + sub holding row sub of its i-th group
   {
     const int C = (a.K + F::CE - 1) / F::CE;
     int Lg = 0;
     while ((1 << Lg) < C && Lg < 6) ++Lg;
     const int RPS = 64 >> Lg;
-    const int Wall = gridDim.x * NW;
     for (int sl = t; sl < a.nslots; sl += NT) {
-      const int grp = sl / RPS, sub = sl - grp * RPS;
-      const int i = grp / NW, w = grp - i * NW;
-      const int r = ((blockIdx.x * NW + w) + i * Wall) * RPS + sub;
+      const int i = sl / RPS, sub = sl - i * RPS;
+      const int r = (blockIdx.x + i * (int)gridDim.x) * RPS + sub;
       rowlist[sl] = r < a.d ? r : -1;
       obuf[sl] = 0.0f;
     }
@@ -1474,17 +1512,25 @@ __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE))) 
     __syncthreads();
     EMBER_STAMP(1, 5);
   };
-  down1_walk<FMT, NB, NT>(static_cast<const uint8_t*>(a.w), exp_s, a.expert_stride, np, F::row_bytes(a.K), a.K, act_lds,
-                          row_lds, rowlist, a.nslots, obuf, gate_s, false, nullptr, a.d, stage);
+  down1_walk_picks<FMT, NB, NT>(static_cast<const uint8_t*>(a.w), exp_s, a.expert_stride, np, F::row_bytes(a.K), a.K,
+                                act_lds, row_lds, a.d, a.nslots, pbuf, stage);
+  __syncthreads();
+  // combine_kernel's sum on this block's rows: acc = acc + gate * y, picks ascending
+  for (int sl = t; sl < a.nslots; sl += NT)
+    if (rowlist[sl] >= 0) {
+      float o = 0.0f;
+      for (int j = 0; j < np; ++j) o = o + gate_s[j] * pbuf[j][sl];
+      obuf[sl] = o;
+    }
   __syncthreads();
   // the rest of combine_kernel's sequence on this block's rows: (acc * scale) + 0, then the shared row
   if (a.scale != 1.0f)
     for (int sl = t; sl < a.nslots; sl += NT) obuf[sl] = obuf[sl] * a.scale + 0.0f;
   if (a.s_w) {
     __syncthreads();
-    down1_walk<FMT, NB, NT>(static_cast<const uint8_t*>(a.s_w), exp_s, 0, 1, F::row_bytes(a.s_K), a.s_K,
-                            act_lds + (size_t)np * row_lds, srow_lds, rowlist, a.nslots, obuf, nullptr, true,
-                            a.sg_logit ? &sgc_s : nullptr, 0, [] {});
+    down1_walk_shared<FMT, NB, NT>(static_cast<const uint8_t*>(a.s_w), F::row_bytes(a.s_K), a.s_K,
+                                   act_lds + (size_t)np * row_lds, srow_lds, rowlist, a.nslots, obuf,
+                                   a.sg_logit ? &sgc_s : nullptr);
   }
   __syncthreads();
   // a pick-set conflict of the fused routing (never expected): NaN rows instead of plausible numbers
@@ -1508,10 +1554,10 @@ int launch_down1_cfg(const Down1Args& a_in, hipStream_t st) {
   const int C = (a_in.K + F::CE - 1) / F::CE;
   int Lg = 0;
   while ((1 << Lg) < C && Lg < 6) ++Lg;
-  const int RPS = 64 >> Lg, NW = NT / 64;
-  const int gt = (a_in.d + RPS - 1) / RPS, Wall = G * NW;
+  const int RPS = 64 >> Lg;
+  const int gt = (a_in.d + RPS - 1) / RPS;
   Down1Args a = a_in;
-  a.nslots = (gt + Wall - 1) / Wall * NW * RPS;  // every wave's groups, in slots
+  a.nslots = (gt + G - 1) / G * RPS;  // the block's row groups, in slots
   if (a.nslots > kDown1Slots) return EMBER_ERR_SHAPE;
   if (a.ev_start)
     hipExtLaunchKernelGGL(down1_kernel<FMT, NB, NT, WPE>, dim3(G), dim3(NT), lds, st, a.ev_start, a.ev_stop, 0, a);
@@ -1540,11 +1586,11 @@ bool down1_fits(int type, int d, int K, int k, int s_K) {
   int Lg = 0;
   while ((1 << Lg) < C && Lg < 6) ++Lg;
   const int RPS = 64 >> Lg;
-  // at least one block per CU of eight waves: the slot bound for the smallest grid
+  // at least one block per CU: the slot bound for the smallest grid
   const int cus = device_cus();
   if (cus <= 0) return false;
-  const int Wall = cus * 8, gt = (d + RPS - 1) / RPS;
-  return (gt + Wall - 1) / Wall * 8 * RPS <= kDown1Slots;
+  const int gt = (d + RPS - 1) / RPS;
+  return (gt + cus - 1) / cus * RPS <= kDown1Slots;
 }
 
 int launch_down1(const Down1Args& a, hipStream_t st) {
