@@ -1,8 +1,8 @@
-"""GPU tests of the one-token decode path (fused routing, expert GEMVs, combine): the output of a
-one-token call has the same bits as the same token's row of a two-token call (the per-token arithmetic
-of the expert kernels and of the combine does not depend on the batch), for plain, scaled,
-DeepSeek-style (sigmoid, bias, groups) and shared-expert layers, over repeated calls (the fused
-routing's flag words are re-armed every call)."""
+"""GPU tests of the one-token decode path (fused routing, expert GEMVs, the down launch with the combine
+fused in): the output of a one-token call has the same bits as the same token's row of a two-token call
+(the down launch then the combine launch: the per-token arithmetic does not depend on the batch), for
+plain, scaled, DeepSeek-style (sigmoid, bias, groups), top-8 and shared-expert layers, over repeated
+calls (the fused routing's flag words are re-armed every call)."""
 import numpy as np
 import pytest
 
@@ -17,6 +17,10 @@ CASES = {
     "deepseek_bf16_shared": dict(d=256, d_ff=512, E=16, k=4, wtype=em.BF16, scoring=em.SCORE_SIGMOID, renorm=True,
                                  bias_std=1.0, groups_n=4, groups_top=2, out_scale=2.5, d_ff_shared=512),
     "f32": dict(d=256, d_ff=256, E=4, k=2, wtype=em.F32),
+    # the fused down launch's limits: eight picks; six picks with a shared expert
+    "qwen_top8_q4k": dict(d=512, d_ff=768, E=32, k=8, wtype=em.Q4_K),
+    "top6_shared_bf16": dict(d=512, d_ff=384, E=32, k=6, wtype=em.BF16, scoring=em.SCORE_SIGMOID, renorm=True,
+                             bias_std=2.0, d_ff_shared=768),
 }
 
 
@@ -29,6 +33,7 @@ def test_one_token_matches_batch_row(gpu, monkeypatch, name):
     dl = em.DeviceLayer.upload(hl)
     x2 = em.make_input(spec, 2)
     print(f"decode combine {name}", flush=True)
+    assert em.path(dl.desc, 1) & em.PATH_DOWN1  # one token: the down launch with the combine fused in
     xd2 = torch.from_numpy(x2).cuda()
     # the two-token call on the expert GEMVs (the path one token takes; small layers with a shared expert
     # would pick the MFMA tiles at two tokens)
