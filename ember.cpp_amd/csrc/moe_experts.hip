@@ -1615,12 +1615,12 @@ extern "C" int ember_moe_probe_set(void* buf) {
 namespace ember_moe {
 #endif
 
-// The fused routing's limits: E <= 255 (expert ids fit the fast words' byte arrays), k <= 8 and the
-// LDS of the staged row, the router products and the routing area. (A block that waits for a router
+// The fused routing's limits: E <= kMaxRouteE (its per-expert LDS arrays), k <= 8 and the LDS of the
+// staged row, the router products and the routing area. (A block that waits for a router
 // block's word longer than its bound computes that logit itself, so no block depends on another being
 // resident.)
 bool fused_route_fits(int type, int d, int E, int k) {
-  return E <= 255 && k <= kFusedMaxK && d >= 8 && d <= 16 * 512 &&
+  return E <= kMaxRouteE && k <= kFusedMaxK && d >= 8 && d <= 16 * 512 &&
          fused_x_lds(type, d) + fused_router_lds(d) + fused_route_lds(E) <= (size_t)kProjLdsBytes;
 }
 

@@ -171,7 +171,7 @@ int launch_slice_reduce(const float* part, int ns, int d, int k, const int32_t* 
 // the fused routing's shape limits (the router blocks' and block 0's LDS)
 bool fused_route_fits(int type, int d, int E, int k);
 constexpr unsigned long long kRouteReady = 0x5e11a7ed0ddba11full;
-constexpr int kMaxRouteE = 256;  // experts a fused routing block handles (E <= 255)
+constexpr int kMaxRouteE = 256;  // experts a fused routing block handles
 
 int launch_projection(const ProjArgs& a, hipStream_t st);
 

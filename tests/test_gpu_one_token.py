@@ -86,6 +86,9 @@ CASES = {
     "q4_raw_gates": dict(d=1024, d_ff=512, E=8, k=2, wtype=em.Q4_K, renorm=False),
     "q8_deepseek": dict(d=1024, d_ff=512, E=16, k=4, wtype=em.Q8_0, scoring=em.SCORE_SIGMOID, bias_std=1.0,
                         groups_n=4, groups_top=2, out_scale=2.5),
+    "q8_e256_k8": dict(d=1024, d_ff=256, E=256, k=8, wtype=em.Q8_0),                 # the most experts fused
+    "q8_deepseek_e256": dict(d=1024, d_ff=256, E=256, k=8, wtype=em.Q8_0, scoring=em.SCORE_SIGMOID, bias_std=1.0,
+                             groups_n=8, groups_top=4, out_scale=2.5),
 }
 
 
