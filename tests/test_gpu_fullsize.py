@@ -3,7 +3,9 @@
 Tokens are independent in the reference (one moe_ffn_f32_cpu call per token), so at sizes where the
 oracle cannot finish every token in seconds it checks a seeded sample of tokens of the same batch:
 the sample's rows of the GPU output must match the oracle run on the sample alone. Routing (logits,
-experts, gates) is checked bit-exact on every token."""
+experts, gates) is checked bit-exact on every token. The largest batches (a 16384-token Mixtral-shaped
+prefill, 32768 tokens at the Qwen shape: 262144 routed rows) exercise the multi-block dispatch and every
+index of the scratch at sizes eight times the BASELINE configs'."""
 import numpy as np
 import pytest
 
@@ -35,7 +37,9 @@ def _layer(name):
 
 @pytest.mark.parametrize("name,T,sample", [("c2", 1, 1), ("c2", 8, 8), ("c2", 128, 12), ("c2", 2048, 12),
                                            ("c3", 1, 1), ("c3", 32, 32), ("c3", 4096, 24),
-                                           ("c4", 1, 1), ("c4", 2048, 24)])
+                                           ("c4", 1, 1), ("c4", 2048, 24),
+                                           # long prefills: 32768 and 262144 dispatch slots
+                                           ("c2", 16384, 8), ("c3", 32768, 16)])
 def test_full_size_layer(gpu, name, T, sample):
     import torch
 
