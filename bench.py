@@ -405,6 +405,12 @@ def main():
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device-to-device copies of MIB MiB (the reference kernel that scales "
                          "rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes), then exit")
+    ap.add_argument("--expert-type", type=str, default=None, choices=sorted(BPW),
+                    help="single-layer configs only: encode the experts in this type instead of the config's "
+                         "(e.g. a Mixtral-shaped Q4_K layer, config 5's FFN, for counter passes)")
+    ap.add_argument("--decode-steps", type=int, default=256,
+                    help="--config c5 only: greedy decode steps after the 512-token prefill (a shorter run for "
+                         "counter passes)")
     ap.add_argument("--vendor-gemm", action="store_true",
                     help="only time torch's fp16 matmul (the vendor GEMM library) on the dense shapes of the config's "
                          "prefill expert GEMMs at the headline token count, as a measured ceiling, then exit")
@@ -434,6 +440,10 @@ def main():
     em.lib()
     if args.config == "c5":
         return bench_e2e(args)
+    if args.expert_type:
+        d0, kw0, tk0 = CONFIGS[args.config]
+        CONFIGS[args.config] = (f"{d0.rsplit(',', 1)[0]}, experts re-encoded as {args.expert_type}",
+                                dict(kw0, wtype=args.expert_type), tk0)
     desc, _, tokens = CONFIGS[args.config]
     if args.tokens is None:
         args.tokens = tokens[0]
@@ -442,7 +452,7 @@ def main():
     spec = layer_spec(args.config)
     t0 = time.time()
     hl = em.make_host_layer(spec)
-    log(f"[bench] generated + quantized the Q8_0 layer in {time.time() - t0:.1f}s")
+    log(f"[bench] generated + quantized the layer in {time.time() - t0:.1f}s")
     dl = em.DeviceLayer.upload(hl)
     # the prefill pack (tile-contiguous copy of the Q8_0 stacks for the 256-token-tile GEMM), prepared
     # once at load as a model loader would; decode does not read it
@@ -458,6 +468,8 @@ def main():
     results = run_sweep(em, spec, dl, sweep_T, args.steps, args.warmup)
 
     h = results[args.tokens]
+    # the committed traffic summaries are keyed by workload: a re-encoded layer is not the config's own
+    traffic_key = args.config + (f":{args.expert_type}" if args.expert_type else "")
     line = {
         "metric": "MoE-FFN tokens/s (" + args.config + ")",
         "value": h["tokens_per_s"],
@@ -482,7 +494,7 @@ def main():
                                 f"gate/up + SwiGLU expert kernel ({em.TYPE_NAMES[spec.wtype]})"
                                 + (", router + routing fused in (one token)" if args.tokens == 1 else "")),
                      "bound": "hbm", "achieved": h["gate_up_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": h["gate_up_gbs"] / HBM_PEAK_GBS, "traffic": profiled_traffic(args.config, args.tokens),
+                     "frac": h["gate_up_gbs"] / HBM_PEAK_GBS, "traffic": profiled_traffic(traffic_key, args.tokens),
                      "bytes_per_launch": algorithmic(spec, args.tokens, h["experts_hit"], h["path_bits"])[0],
                      "avg_launch_us": h["gate_up_us"]},
         "layer_hbm_frac": h["layer_hbm_frac"],
@@ -555,7 +567,7 @@ def run_e2e(prompt_len=512, n_new=256, log_prefix="[bench]"):
 
 def bench_e2e(args):
     """bench.py --config c5: the end-to-end run alone, as its own JSON line."""
-    r = run_e2e()
+    r = run_e2e(n_new=args.decode_steps)
     line = {"metric": r["metric"], "value": r["value"], "unit": r["unit"], "n_gpus": 1, "steps": 1, "warmup": 1,
             "ms_per_step": (r["prefill_s"] + r["decode_s"]) * 1e3, "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None, "dtype": r["dtype"], "data": r["data"], "config": r["config"]}
