@@ -195,6 +195,9 @@ __device__ __attribute__((always_inline)) inline int wave_topk_regs(const float*
   // t stays 0 when there are fewer than k candidates: then every candidate is above it. Every trial is
   // >= 1, so the zero keys of non-candidates never count.
   uint32_t t = 0;
+  // kept rolled: unrolled, the 32 steps of each register-count variant added ~10 KB of code to every
+  // launch that routes inline (the one-token kernels: 58 -> 45 KB), for no measured gain
+#pragma unroll 1
   for (int bit = 31; bit >= 0; --bit) {
     const uint32_t trial = t | (1u << bit);
     int cnt = 0;
