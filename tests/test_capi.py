@@ -13,7 +13,8 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
 def declared(header: str):
-    text = open(os.path.join(ROOT, "include", header)).read()
+    with open(os.path.join(ROOT, "include", header)) as f:
+        text = f.read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"^\s*(?:[\w\s\*]+?)\b(ember_\w+)\s*\(", text, flags=re.M)))
 
