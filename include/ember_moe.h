@@ -110,8 +110,10 @@ int ember_moe_path(const ember_moe_layer* w, int T);
 
 /* Prefill weight packing (no counterpart in the reference, which dequantizes every stack to F32 at
  * load, weight_management.cpp:486-511): a one-time preparation of a layer's routed stacks for the
- * prefill MFMA GEMMs (more than ~1.5-2 tokens per expert), which never replaces the stacks (decode
- * streams the ggml rows).
+ * prefill MFMA GEMMs (more than ~1.5-2 tokens per expert), kept beside the stacks, which it never
+ * replaces: decode batches stream the ggml rows, except that a one-token call of a Q8_0 / Q4_K layer
+ * without a shared expert whose k * d_ff / 64 slices fill the device (EMBER_PATH_SLICES) reads the pack's
+ * tiles.
  *   All-Q8_0 layers: each 256-row x 64-column tile contiguous (gate/up: the tile's 128 gate and 128 up
  *     rows; rows past the end repeat the last), 68-byte rows, as large as the three stacks; the GEMM
  *     loads whole tiles and reads them at a bank-conflict-free stride. Same values, same arithmetic:
