@@ -101,7 +101,8 @@ class Mixtral:
         ang = torch.arange(max_ctx, device=device, dtype=torch.float64)[:, None] * inv[None, :]
         self.cos = torch.cat([ang.cos(), ang.cos()], -1).float()
         self.sin = torch.cat([ang.sin(), ang.sin()], -1).float()
-        self.cos_b, self.sin_b = self.cos.to(torch.bfloat16), self.sin.to(torch.bfloat16)  # decode: bf16 q / k
+        # decode: RoPE as one matmul by a per-position [D, D] matrix (rot_matrix), built once per step
+        self.rot_perm = self.rope_perm(s.head_dim, device)
         self.kcache = torch.zeros(s.n_layers, s.n_kv, max_ctx, s.head_dim, device=device, dtype=torch.bfloat16)
         self.vcache = torch.zeros_like(self.kcache)
         self.scratch = None
@@ -132,6 +133,25 @@ class Mixtral:
             rep = self.s.n_heads // self.s.n_kv
             return F.scaled_dot_product_attention(q, k.repeat_interleave(rep, 1), v.repeat_interleave(rep, 1),
                                                   attn_mask=mask, is_causal=causal)
+
+    @staticmethod
+    def rope_perm(D, device="cpu"):
+        """The signed rotate-half permutation: x @ P = rotate_half(x) = [-x[D/2:], x[:D/2]]."""
+        import torch
+
+        hd = D // 2
+        P = torch.zeros(D, D, device=device)
+        P[torch.arange(hd) + hd, torch.arange(hd)] = -1.0  # out[j] = -x[j + D/2], j < D/2
+        P[torch.arange(hd), torch.arange(hd) + hd] = 1.0   # out[j] = x[j - D/2], j >= D/2
+        return P
+
+    @staticmethod
+    def rot_matrix(cos, sin, perm):
+        """R with x @ R = x cos + rotate_half(x) sin for one position (cos, sin [D]; perm the signed
+        rotate-half permutation, perm[i][j] = -1 for i = j + D/2, 1 for j = i + D/2)."""
+        import torch
+
+        return torch.diag(cos) + perm * sin[None, :]
 
     @staticmethod
     def attend_decode(q, kc, vc, mbias):
@@ -202,13 +222,13 @@ class Mixtral:
         s = self.s
         qd, kvd = s.n_heads * s.head_dim, s.n_kv * s.head_dim
         x = self.emb[tok].float()
-        cos, sin = self.cos_b[pos], self.sin_b[pos]  # [1, head_dim]
+        rot = self.rot_matrix(self.cos[pos][0], self.sin[pos][0], self.rot_perm).to(torch.bfloat16)
         mbias = torch.zeros(self.max_ctx, device=self.dev, dtype=torch.bfloat16)
         mbias.masked_fill_(torch.arange(self.max_ctx, device=self.dev) > pos, float("-inf"))
         for l in range(s.n_layers):
             h = self._rms(x).to(torch.bfloat16)
             qkv = h @ self.wqkv[l].t()  # bf16: q, k, v and their rotation stay in the cache's dtype
-            qk = self._rot(qkv[:, :qd + kvd].view(1, s.n_heads + s.n_kv, s.head_dim), cos[:, None], sin[:, None])
+            qk = (qkv[:, :qd + kvd].view(s.n_heads + s.n_kv, s.head_dim) @ rot)[None]
             q, k = qk[:, :s.n_heads], qk[:, s.n_heads:]
             v = qkv[:, qd + kvd:].view(1, s.n_kv, s.head_dim)
             self.kcache[l].index_copy_(1, pos, k.transpose(0, 1))

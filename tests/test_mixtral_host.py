@@ -23,3 +23,16 @@ def test_attend_decode_matches_repeated_kv_sdpa(H, Hkv, C, D, n):
     assert got.shape == (H, D)
     assert torch.allclose(got, want, rtol=1e-5, atol=1e-5), (got - want).abs().max()
 
+
+
+def test_rope_matrix_equals_rotate_half():
+    D, hd = 16, 8
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(6, D, generator=g)
+    ang = torch.randn(hd, generator=g)
+    cos, sin = torch.cat([ang.cos(), ang.cos()]), torch.cat([ang.sin(), ang.sin()])
+    perm = Mixtral.rope_perm(D)
+    assert torch.equal(x @ perm, torch.cat([-x[:, hd:], x[:, :hd]], -1))
+    want = Mixtral._rot(x, cos, sin)
+    got = x @ Mixtral.rot_matrix(cos, sin, perm)
+    assert torch.allclose(got, want, rtol=1e-6, atol=1e-6)
