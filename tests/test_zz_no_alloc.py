@@ -1,6 +1,7 @@
 """ember_moe_ffn_noalloc (the entry point that allocates nothing and runs in the library's static
 scratch) against ember_moe_ffn on the same inputs: bit-identical outputs on two calls in a row, the
-second with a smaller batch, for a fused-routing decode layer and a prefill-sized MFMA layer; a batch
+second with a smaller batch, for a fused-routing decode layer, a prefill-sized MFMA layer and a layer
+whose one-token call takes the slice launch; a batch
 whose scratch exceeds the static buffer is refused with EMBER_ERR_SCRATCH and launches nothing."""
 import numpy as np
 import pytest
@@ -35,6 +36,26 @@ def test_noalloc_matches_ffn(gpu, name, spec, Ts):
         print(f"noalloc {name} call {i} T={T}", flush=True)
         got, want = _pair(dl, x)
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (name, T)
+
+
+def test_noalloc_slice_launch(gpu):
+    """A packed Q8_0 layer whose one-token call takes the slice launch (k * d_ff / 64 = 256 slices): its
+    partial rows live in the static scratch too."""
+    import torch
+
+    s = em.LayerSpec(d=1024, d_ff=8192, E=8, k=2, wtype=em.Q8_0, seed=33)
+    dl = em.DeviceLayer.upload(em.make_host_layer(s))
+    buf = torch.empty(em.prefill_pack_bytes(dl.desc), dtype=torch.uint8, device="cuda")
+    em.prefill_pack(dl.desc, buf)
+    dl.tensors["pack"] = buf
+    bits = em.path(dl.desc, 1)
+    if not bits & em.PATH_SLICES:
+        pytest.skip(f"this device does not take the slice launch for 256 slices (path bits {bits})")
+    for i, T in enumerate((8, 1)):
+        x = em.make_input(s, T, seed=600 + i)
+        print(f"noalloc slices call {i} T={T}", flush=True)
+        got, want = _pair(dl, x)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), T
 
 
 def test_noalloc_refuses_oversize(gpu):
